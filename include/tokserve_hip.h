@@ -1,0 +1,220 @@
+/*
+ * tokserve_hip.h -- C ABI of libtokserve_hip.so, the MI355X (gfx950) kernels of
+ * tokserve's continuous-batching hot path: KV append into paged blocks, block
+ * table gathers, paged attention (decode and chunked prefill), RMSNorm, RoPE
+ * and greedy token selection.
+ *
+ * Conventions shared by every entry point
+ *   - All pointers are device pointers (HBM), except where a comment says host.
+ *     The caller owns every buffer; the library never allocates device memory.
+ *     Scratch memory (split-K partials) comes in as a caller-owned workspace.
+ *   - Sizes and strides are in ELEMENTS, not bytes. The innermost (head_dim or
+ *     hidden) dimension must be contiguous.
+ *   - `stream` is a hipStream_t (NULL = the default stream). Kernels are only
+ *     enqueued; nothing synchronises.
+ *   - Return value: TKS_OK (0) or a negative tks_status. The library never
+ *     throws across this boundary. A host-side binding maps the codes to the
+ *     reference's exception types (ValueError / TypeError / IndexError).
+ *   - Paged KV pools use the reference layout [L, NB, Hkv, BS, Dh]
+ *     (tokserve/engine/paged/storage.py:40-56), one pool for K and one for V.
+ *     A "slot" is block_id * BS + offset (tokserve/engine/paged/block_table.py:53-67).
+ *
+ * The reference has no compiled code: its kernels are Triton JIT functions in
+ * tokserve/kernels/_triton_<op>.py behind the Python wrappers in tokserve/kernels/<op>.py.
+ * Each entry point below names the reference interface it replaces.
+ */
+#ifndef TOKSERVE_HIP_H
+#define TOKSERVE_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef void *tks_stream_t; /* hipStream_t */
+
+/* Element types. Values are part of the ABI. */
+enum tks_dtype {
+  TKS_FLOAT32 = 0,
+  TKS_FLOAT16 = 1,
+  TKS_BFLOAT16 = 2,
+};
+
+/* Status codes. Values are part of the ABI. */
+enum tks_status {
+  TKS_OK = 0,
+  TKS_ERR_VALUE = -1,     /* shape, size or range error       -> ValueError */
+  TKS_ERR_TYPE = -2,      /* unsupported dtype combination    -> TypeError  */
+  TKS_ERR_INDEX = -3,     /* layer index out of range         -> IndexError */
+  TKS_ERR_WORKSPACE = -4, /* workspace missing or too small   -> ValueError */
+  TKS_ERR_LAUNCH = -5,    /* HIP reported a launch error      -> RuntimeError */
+};
+
+/* ABI version of this header; bumped on any signature change. */
+int32_t tks_abi_version(void);
+
+/* Static description of a status code (never NULL). */
+const char *tks_status_string(int32_t status);
+
+/* Message of the last HIP error seen by this thread's last failing call. */
+const char *tks_last_hip_error(void);
+
+/* ------------------------------------------------------------------------
+ * KV append: scatter new K/V rows into the paged pools.
+ * Replaces SequencePagedKVCache.write_layer (tokserve/engine/paged/sequence_cache.py:86-131)
+ * and its per-token PagedKVStorage.write_token copies (tokserve/engine/paged/storage.py:64-89).
+ *
+ * For token t in [0, num_tokens), head h, dim d:
+ *   key_cache[layer, slot/BS, h, slot%BS, d] = key[t*key_token_stride + h*key_head_stride + d]
+ * (and the same for value), with slot = slot_mapping[t] (int64, device).
+ * A negative slot skips the token (padding). Slots >= num_blocks*block_size are
+ * never written (callers validate them; the kernel only guards memory).
+ * Bit-exact copy.
+ */
+int32_t tks_kv_append(const void *key, int64_t key_token_stride, int64_t key_head_stride,
+                      const void *value, int64_t value_token_stride, int64_t value_head_stride,
+                      int64_t num_tokens, void *key_cache, void *value_cache, int32_t num_layers,
+                      int64_t num_blocks, int32_t num_kv_heads, int32_t block_size,
+                      int32_t head_dim, int32_t layer_index, const int64_t *slot_mapping,
+                      int32_t dtype, tks_stream_t stream);
+
+/* ------------------------------------------------------------------------
+ * Block-table gather: rebuild logical-order K/V of a ragged batch.
+ * Replaces SequencePagedKVCache.read_layer (tokserve/engine/paged/sequence_cache.py:133-193)
+ * and PagedKVStorage.read_token (tokserve/engine/paged/storage.py:103-116).
+ *
+ * For sequence b, position p < seq_lens[b], head h:
+ *   key_out[(cu_seqlens[b] + p)*out_token_stride + h*out_head_stride + d]
+ *     = key_cache[layer, block_tables[b*block_table_stride + p/BS], h, p%BS, d]
+ * block_tables, seq_lens, cu_seqlens are int32 device arrays. Bit-exact copy.
+ * max_seq_len (host) must be >= every seq_lens[b].
+ */
+int32_t tks_paged_gather(const void *key_cache, const void *value_cache, int32_t num_layers,
+                         int64_t num_blocks, int32_t num_kv_heads, int32_t block_size,
+                         int32_t head_dim, int32_t layer_index, const int32_t *block_tables,
+                         int32_t block_table_stride, const int32_t *seq_lens,
+                         const int32_t *cu_seqlens, int32_t num_seqs, int32_t max_seq_len,
+                         void *key_out, void *value_out, int64_t out_token_stride,
+                         int64_t out_head_stride, int32_t dtype, tks_stream_t stream);
+
+/* ------------------------------------------------------------------------
+ * Paged attention, decode (one query token per sequence), split-K.
+ * Replaces triton_paged_attention for Tq == 1 (tokserve/kernels/paged_attention.py:11-88,
+ * kernel tokserve/kernels/_triton_paged_attention.py:12-149), batched over sequences.
+ *
+ * Query row of sequence b, head hq: query[b*q_seq_stride + hq*q_head_stride + d].
+ * It attends to keys 0..seq_lens[b]-1 of KV head hq / (num_q_heads/num_kv_heads)
+ * through block_tables[b*block_table_stride + p/BS]:
+ *   out = softmax(scale * q.K^T) V, accumulated in fp32, stored in `dtype`.
+ * max_seq_len (host) bounds every seq_lens[b] and sizes the grid.
+ * pages_per_split: KV blocks per split-K work item (0 = library heuristic).
+ * The workspace holds one arrival counter per (sequence, KV head) followed by
+ * the split partials; its size comes from
+ * tks_paged_attention_decode_workspace_bytes with the same arguments. The
+ * counters must be zero before the first launch (allocate the workspace zeroed
+ * once); every launch leaves them zero. The last split of a (sequence, KV head)
+ * to finish merges the partials, so one call is one kernel launch. Launches
+ * sharing a workspace must be stream-ordered.
+ * A sequence with seq_lens[b] == 0 gets an all-zero output row.
+ */
+int64_t tks_paged_attention_decode_workspace_bytes(int32_t num_seqs, int32_t num_q_heads,
+                                                   int32_t num_kv_heads, int32_t head_dim,
+                                                   int32_t block_size, int32_t max_seq_len,
+                                                   int32_t pages_per_split);
+
+int32_t tks_paged_attention_decode(const void *query, int64_t q_seq_stride, int64_t q_head_stride,
+                                   const void *key_cache, const void *value_cache,
+                                   int32_t num_layers, int64_t num_blocks, int32_t num_kv_heads,
+                                   int32_t block_size, int32_t head_dim, int32_t layer_index,
+                                   const int32_t *block_tables, int32_t block_table_stride,
+                                   const int32_t *seq_lens, int32_t num_seqs, int32_t num_q_heads,
+                                   int32_t max_seq_len, float scale, int32_t pages_per_split,
+                                   void *out, int64_t out_seq_stride, int64_t out_head_stride,
+                                   void *workspace, int64_t workspace_bytes, int32_t dtype,
+                                   tks_stream_t stream);
+
+/* ------------------------------------------------------------------------
+ * Paged attention over a ragged batch of query chunks (chunked prefill).
+ * Replaces triton_paged_attention for Tq >= 1 with query_position_offset
+ * (tokserve/kernels/paged_attention.py:11-88) and the contiguous
+ * triton_tiled_attention (tokserve/kernels/tiled_attention.py:9-73).
+ *
+ * Sequence b owns query tokens cu_seqlens_q[b] .. cu_seqlens_q[b+1]-1 (int32 device
+ * array, length num_seqs+1) and seq_lens[b] keys (its KV already appended).
+ * Query token i of sequence b sits at absolute position
+ *   seq_lens[b] - (cu_seqlens_q[b+1] - cu_seqlens_q[b]) + i
+ * and attends causally to keys 0..that position (mask k <= position,
+ * tokserve/kernels/_triton_paged_attention.py:118-123).
+ * Token n, head hq: query[n*q_token_stride + hq*q_head_stride + d], same for out.
+ * num_tokens (host) == cu_seqlens_q[num_seqs]; max_query_len and max_seq_len
+ * (host) bound the per-sequence query and key lengths.
+ */
+int32_t tks_paged_attention_prefill(const void *query, int64_t q_token_stride,
+                                    int64_t q_head_stride, const void *key_cache,
+                                    const void *value_cache, int32_t num_layers,
+                                    int64_t num_blocks, int32_t num_kv_heads, int32_t block_size,
+                                    int32_t head_dim, int32_t layer_index,
+                                    const int32_t *block_tables, int32_t block_table_stride,
+                                    const int32_t *seq_lens, const int32_t *cu_seqlens_q,
+                                    int32_t num_seqs, int64_t num_tokens, int32_t num_q_heads,
+                                    int32_t max_query_len,
+                                    int32_t max_seq_len, float scale, void *out,
+                                    int64_t out_token_stride, int64_t out_head_stride,
+                                    int32_t dtype, tks_stream_t stream);
+
+/* ------------------------------------------------------------------------
+ * RMSNorm over the last dimension.
+ * Replaces triton_rms_norm (tokserve/kernels/rmsnorm.py:6-45, kernel
+ * tokserve/kernels/_triton_rmsnorm.py:10-38) and RMSNorm.forward
+ * (tokserve/engine/layers.py:29-42):
+ *   out = weight * to_input_dtype(x * rsqrt(mean(x^2) + epsilon))
+ * reduced in fp32, rounded to input_dtype before the weight multiply, the
+ * product rounded once to out_dtype. Valid (input, weight, out) dtype triples
+ * follow torch type promotion: weight fp32 -> out fp32; weight == input -> out input.
+ * If residual != NULL (fused residual add, tokserve/engine/model.py:73,82):
+ *   x = to_input_dtype(input + residual) is written to residual_out first,
+ *   then normalised. residual_out may alias input or residual.
+ */
+int32_t tks_rms_norm(const void *input, int64_t input_row_stride, const void *residual,
+                     int64_t residual_row_stride, void *residual_out,
+                     int64_t residual_out_row_stride, const void *weight, void *out,
+                     int64_t out_row_stride, int64_t num_rows, int32_t hidden_size,
+                     float epsilon, int32_t input_dtype, int32_t weight_dtype,
+                     int32_t out_dtype, tks_stream_t stream);
+
+/* ------------------------------------------------------------------------
+ * Rotary position embedding (half rotation) on Q and K in one launch.
+ * Replaces triton_apply_rope (tokserve/kernels/rope.py:8-63, kernel
+ * tokserve/kernels/_triton_rope.py:10-68) and apply_rope (tokserve/engine/rope.py:106-153):
+ *   out[d] = r(x[d]*cos[p][d]) + r(rot(x)[d]*sin[p][d]),  rot(x) = cat(-x2, x1)
+ * with each product rounded to dtype before the add (r = round to dtype).
+ * Element (b, h, t, d) of Q lives at q[b*q_sb + h*q_sh + t*q_st + d] and is
+ * written to q_out[b*qo_sb + h*qo_sh + t*qo_st + d] (q_out may equal q).
+ * Same for K with num_kv_heads. Position of token t: positions[t] (int64).
+ * cos_cache / sin_cache: [cache_len, head_dim/2] in dtype, row p holding
+ * cos/sin(fp32(p) * inv_freq) cast to dtype (tokserve/engine/rope.py:28-87).
+ * Positions outside [0, cache_len) are clamped; callers validate them.
+ */
+int32_t tks_rope(const void *query, void *query_out, int64_t q_sb, int64_t q_sh, int64_t q_st,
+                 int64_t qo_sb, int64_t qo_sh, int64_t qo_st, int32_t num_q_heads,
+                 const void *key, void *key_out, int64_t k_sb, int64_t k_sh, int64_t k_st,
+                 int64_t ko_sb, int64_t ko_sh, int64_t ko_st, int32_t num_kv_heads,
+                 int32_t batch, int64_t num_tokens, int32_t head_dim, const int64_t *positions,
+                 const void *cos_cache, const void *sin_cache, int64_t cache_len, int32_t dtype,
+                 tks_stream_t stream);
+
+/* ------------------------------------------------------------------------
+ * Greedy token selection: first index of the row maximum (NaN counts as the
+ * maximum, as torch.argmax does).
+ * Replaces select_greedy (tokserve/generation/greedy.py:6-18) on a (B, V) batch.
+ * logits[r*row_stride + v]; out_ids[r] (int64).
+ */
+int32_t tks_argmax(const void *logits, int64_t row_stride, int64_t num_rows, int64_t vocab_size,
+                   int64_t *out_ids, int32_t dtype, tks_stream_t stream);
+
+#ifdef __cplusplus
+} /* extern "C" */
+#endif
+
+#endif /* TOKSERVE_HIP_H */

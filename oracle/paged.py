@@ -1,0 +1,105 @@
+"""Paged-KV attention as the reference's torch backend computes it (CPU).
+
+The torch backend writes the new K/V into the pool, rebuilds the layer's K/V in
+logical order through the block table (read_layer, include_pending=True) and
+runs repeat_kv + causal_attention over cache_len + T keys with offset
+cache_len (tokserve/engine/attention.py:298-356). The batched functions below
+are the per-request loop of tokserve/batching/execution.py:33-131 applied to a
+packed batch.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from oracle.torch_path import gqa_attention
+
+
+def read_layer(
+    key_cache: torch.Tensor,
+    value_cache: torch.Tensor,
+    block_ids: list[int] | torch.Tensor,
+    layer: int,
+    length: int,
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """(1, Hkv, S, Dh) K/V of positions 0..length-1 in logical order.
+
+    Position p lives at block_ids[p // BS], offset p % BS
+    (tokserve/engine/paged/sequence_cache.py:157-193, block_table.py:53-67).
+    """
+
+    block_size = key_cache.shape[3]
+    table = torch.as_tensor(block_ids, dtype=torch.int64)
+    positions = torch.arange(length)
+    blocks = table[positions // block_size]
+    offsets = positions % block_size
+    keys = key_cache[layer, blocks, :, offsets, :]  # (S, Hkv, Dh)
+    values = value_cache[layer, blocks, :, offsets, :]
+    return keys.permute(1, 0, 2).unsqueeze(0), values.permute(1, 0, 2).unsqueeze(0)
+
+
+def paged_attention(
+    query: torch.Tensor,
+    key_cache: torch.Tensor,
+    value_cache: torch.Tensor,
+    block_ids: list[int] | torch.Tensor,
+    *,
+    layer: int,
+    key_length: int,
+    query_position_offset: int,
+) -> torch.Tensor:
+    """query (1, Hq, Tq, Dh) -> (1, Hq, Tq, Dh) through the block table."""
+
+    keys, values = read_layer(key_cache, value_cache, block_ids, layer, key_length)
+    return gqa_attention(query, keys, values, query_position_offset=query_position_offset)
+
+
+def decode_batch(
+    query: torch.Tensor,
+    key_cache: torch.Tensor,
+    value_cache: torch.Tensor,
+    block_tables: torch.Tensor,
+    seq_lens: torch.Tensor,
+    layer: int,
+) -> torch.Tensor:
+    """One query per sequence: (B, Hq, Dh) -> (B, Hq, Dh); sequence b sees seq_lens[b] keys."""
+
+    out = torch.empty_like(query)
+    for b in range(query.shape[0]):
+        length = int(seq_lens[b])
+        if length == 0:
+            out[b] = 0
+            continue
+        q = query[b][None, :, None, :]
+        o = paged_attention(
+            q, key_cache, value_cache, block_tables[b], layer=layer, key_length=length,
+            query_position_offset=length - 1,
+        )
+        out[b] = o[0, :, 0, :]
+    return out
+
+
+def prefill_batch(
+    query: torch.Tensor,
+    key_cache: torch.Tensor,
+    value_cache: torch.Tensor,
+    block_tables: torch.Tensor,
+    seq_lens: torch.Tensor,
+    cu_seqlens_q: torch.Tensor,
+    layer: int,
+) -> torch.Tensor:
+    """Packed query chunks (N, Hq, Dh): sequence b's chunk sits at the end of its seq_lens[b] keys."""
+
+    out = torch.empty_like(query)
+    for b in range(seq_lens.shape[0]):
+        q0, q1 = int(cu_seqlens_q[b]), int(cu_seqlens_q[b + 1])
+        if q1 == q0:
+            continue
+        length = int(seq_lens[b])
+        q = query[q0:q1].permute(1, 0, 2).unsqueeze(0)  # (1, Hq, Tq, Dh)
+        o = paged_attention(
+            q, key_cache, value_cache, block_tables[b], layer=layer, key_length=length,
+            query_position_offset=length - (q1 - q0),
+        )
+        out[q0:q1] = o[0].permute(1, 0, 2)
+    return out

@@ -1,0 +1,179 @@
+"""Paged attention (decode split-K and ragged prefill) on the GPU against the CPU oracle.
+
+Tolerances (stated by the hot path's parity contract): fp32 within 1e-5
+relative (rtol 1e-5, atol 1e-6); bf16/fp16 within 2e-2 absolute. The oracle is
+the reference's torch backend (gather + repeat_kv + causal_attention in the
+input dtype, oracle/paged.py).
+"""
+
+import pytest
+import torch
+from torch.testing import assert_close
+
+from oracle import paged
+from tokserve_amd import workloads
+from tokserve_amd.kernels import ops
+
+pytestmark = pytest.mark.gpu
+
+TOL = {torch.float32: dict(rtol=1e-5, atol=1e-6), torch.float16: dict(rtol=0, atol=2e-2),
+       torch.bfloat16: dict(rtol=0, atol=2e-2)}
+
+
+def _cpu(batch: workloads.PagedBatch):
+    return (batch.query.cpu(), batch.key_cache.cpu(), batch.value_cache.cpu(),
+            batch.block_tables.cpu(), batch.seq_lens.cpu(), batch.cu_seqlens_q.cpu())
+
+
+def _decode(batch, **kw):
+    return ops.paged_attention_decode(
+        batch.query, batch.key_cache, batch.value_cache, batch.block_tables, batch.seq_lens,
+        layer_index=0, max_seq_len=batch.max_seq_len, **kw)
+
+
+def _decode_oracle(batch):
+    q, kc, vc, bt, lens, _ = _cpu(batch)
+    return paged.decode_batch(q, kc, vc, bt, lens, 0)
+
+
+def test_decode_fp32_small_config(device) -> None:
+    """8 sequences, U[16, 512] (+1) keys, 8/2 heads, Dh 64, fp32, 512-block pool."""
+
+    batch = workloads.decode_fp32_small(device, seed=0)
+    out = _decode(batch)
+    torch.cuda.synchronize()
+    assert_close(out.cpu(), _decode_oracle(batch), **TOL[torch.float32])
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize(("hq", "hkv", "dh"), [(32, 8, 128), (32, 4, 64), (8, 2, 64),
+                                               (16, 16, 128), (16, 1, 128), (4, 2, 16)])
+def test_decode_shapes_and_dtypes(device, dtype, hq, hkv, dh) -> None:
+    contexts = [1, 15, 16, 17, 100, 513, 1300]
+    batch = workloads.paged_batch(contexts, [1] * len(contexts), num_q_heads=hq,
+                                  num_kv_heads=hkv, head_dim=dh, block_size=16, dtype=dtype,
+                                  device=device, seed=hq * 7 + dh)
+    out = _decode(batch)
+    torch.cuda.synchronize()
+    assert_close(out.cpu(), _decode_oracle(batch), **TOL[dtype])
+
+
+@pytest.mark.parametrize("block_size", [1, 2, 5, 32])
+def test_decode_other_block_sizes(device, block_size) -> None:
+    contexts = [3, 40, 77]
+    batch = workloads.paged_batch(contexts, [1] * 3, num_q_heads=8, num_kv_heads=2, head_dim=32,
+                                  block_size=block_size, dtype=torch.float32, device=device,
+                                  seed=block_size)
+    out = _decode(batch)
+    torch.cuda.synchronize()
+    assert_close(out.cpu(), _decode_oracle(batch), **TOL[torch.float32])
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("pages_per_split", [1, 2, 3, 8, 64])
+def test_decode_split_k_matches_oracle(device, dtype, pages_per_split) -> None:
+    contexts = [5, 160, 2049, 700]
+    batch = workloads.paged_batch(contexts, [1] * 4, num_q_heads=32, num_kv_heads=8,
+                                  head_dim=128, block_size=16, dtype=dtype, device=device,
+                                  seed=pages_per_split)
+    out = _decode(batch, pages_per_split=pages_per_split)
+    torch.cuda.synchronize()
+    assert_close(out.cpu(), _decode_oracle(batch), **TOL[dtype])
+
+
+def test_decode_empty_sequence_gives_zeros(device) -> None:
+    batch = workloads.paged_batch([0, 33], [1, 1], num_q_heads=32, num_kv_heads=8, head_dim=128,
+                                  block_size=16, dtype=torch.bfloat16, device=device, seed=3)
+    out = _decode(batch, pages_per_split=1)
+    torch.cuda.synchronize()
+    assert torch.all(out[0] == 0)
+    assert_close(out[1:].cpu(), _decode_oracle(batch)[1:], **TOL[torch.bfloat16])
+
+
+def test_decode_llama3_8b_subset_matches_oracle(device) -> None:
+    """24 sequences drawn from the Llama-3-8B decode distribution (log-uniform 128..8192)."""
+
+    batch = workloads.decode_llama3_8b(device, seed=1, num_seqs=24)
+    out = _decode(batch)
+    torch.cuda.synchronize()
+    assert_close(out.cpu(), _decode_oracle(batch), **TOL[torch.bfloat16])
+
+
+def test_decode_llama3_8b_full_size_properties(device) -> None:
+    """Full 256-sequence shape: (1) relocating every physical block (new pool order and
+    tables) leaves the output bit-identical; (2) split-K on/off agree within rounding;
+    (3) a constant V row is reproduced exactly up to bf16 rounding."""
+
+    batch = workloads.decode_llama3_8b(device, seed=0)
+    out = _decode(batch)
+    nb = batch.key_cache.shape[1]
+    perm = torch.randperm(nb, generator=torch.Generator().manual_seed(5)).to(device)
+    inverse = torch.empty_like(perm)
+    inverse[perm] = torch.arange(nb, device=device)
+    moved_k = torch.empty_like(batch.key_cache)
+    moved_v = torch.empty_like(batch.value_cache)
+    moved_k[:, inverse] = batch.key_cache
+    moved_v[:, inverse] = batch.value_cache
+    tables = inverse[batch.block_tables.long()].to(torch.int32)
+    moved = ops.paged_attention_decode(batch.query, moved_k, moved_v, tables, batch.seq_lens,
+                                       layer_index=0, max_seq_len=batch.max_seq_len)
+    whole = _decode(batch, pages_per_split=1024)
+    torch.cuda.synchronize()
+    assert torch.equal(moved, out)
+    assert_close(whole, out, rtol=0, atol=2e-2)
+    const_v = torch.full_like(batch.value_cache, 0.75)
+    const = ops.paged_attention_decode(batch.query, batch.key_cache, const_v, batch.block_tables,
+                                       batch.seq_lens, layer_index=0,
+                                       max_seq_len=batch.max_seq_len)
+    torch.cuda.synchronize()
+    assert_close(const.float(), torch.full_like(const.float(), 0.75), rtol=0, atol=4e-3)
+
+
+# --------------------------------------------------------------------------
+# Prefill
+
+
+def _prefill(batch):
+    return ops.paged_attention_prefill(
+        batch.query, batch.key_cache, batch.value_cache, batch.block_tables, batch.seq_lens,
+        batch.cu_seqlens_q, layer_index=0, max_query_len=batch.max_query_len,
+        max_seq_len=batch.max_seq_len)
+
+
+def _prefill_oracle(batch):
+    q, kc, vc, bt, lens, cu = _cpu(batch)
+    return paged.prefill_batch(q, kc, vc, bt, lens, cu, 0)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("length", [1, 15, 16, 17, 35])
+def test_prefill_tile_boundaries(device, dtype, length) -> None:
+    """Sequence lengths around 16-token tiles (tests/gpu/test_tiled_attention_prefill.py:62-121)."""
+
+    batch = workloads.paged_batch([length], [length], num_q_heads=4, num_kv_heads=2, head_dim=16,
+                                  block_size=16, dtype=dtype, device=device, seed=500 + length)
+    out = _prefill(batch)
+    torch.cuda.synchronize()
+    assert_close(out.cpu(), _prefill_oracle(batch), **TOL[dtype])
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_prefill_ragged_chunks_with_history(device, dtype) -> None:
+    contexts = [40, 7, 300, 1, 129]
+    qlens = [8, 7, 100, 1, 1]
+    batch = workloads.paged_batch(contexts, qlens, num_q_heads=32, num_kv_heads=8, head_dim=128,
+                                  block_size=16, dtype=dtype, device=device, seed=77)
+    out = _prefill(batch)
+    torch.cuda.synchronize()
+    assert_close(out.cpu(), _prefill_oracle(batch), **TOL[dtype])
+
+
+def test_mixed_step_subset_matches_oracle(device) -> None:
+    """Two 512-token chunks and 16 decodes of the mixed chunked-prefill step shape."""
+
+    prefill, decode = workloads.mixed_llama3_8b(device, seed=2, chunks=2, decodes=16)
+    out_p = _prefill(prefill)
+    out_d = _decode(decode)
+    torch.cuda.synchronize()
+    assert_close(out_p.cpu(), _prefill_oracle(prefill), **TOL[torch.bfloat16])
+    assert_close(out_d.cpu(), _decode_oracle(decode), **TOL[torch.bfloat16])

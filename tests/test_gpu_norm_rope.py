@@ -1,0 +1,155 @@
+"""RMSNorm, RoPE and greedy argmax on the GPU against the CPU oracle.
+
+RoPE is expected to be bit-exact: the kernel reads the same fp32-angle cos/sin
+table (cast to the dtype) and rounds each product to the dtype before the add,
+as the reference does. RMSNorm differs from the oracle only by the order of the
+fp32 sum of squares; tolerances are the reference's own (fp32 2e-5, fp16 2e-3,
+bf16 1e-2; tests/gpu/test_rmsnorm.py:57-68) and 2e-2 absolute on the packed bf16 shape.
+"""
+
+from math import prod
+
+import pytest
+import torch
+from torch.testing import assert_close
+
+from oracle import torch_path
+from tokserve_amd import workloads
+from tokserve_amd.kernels import ops
+
+pytestmark = pytest.mark.gpu
+
+NORM_TOL = {torch.float32: 2e-5, torch.float16: 2e-3, torch.bfloat16: 1e-2}
+
+
+@pytest.mark.parametrize(("shape", "epsilon"), [((2, 7), 1e-6), ((2, 3, 13), 1e-3),
+                                                ((4, 128), 1e-6), ((3, 4096), 1e-5),
+                                                ((5, 2048), 1e-5), ((2, 9000), 1e-6)])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
+def test_rmsnorm_matches_oracle(device, shape, epsilon, dtype) -> None:
+    """Inputs of tests/gpu/test_rmsnorm.py:27-68 (arange/7 - 1, linspace weights)."""
+
+    hidden = shape[-1]
+    x = (torch.arange(prod(shape), dtype=torch.float32).reshape(shape) / 7.0 - 1.0).to(dtype)
+    w = torch.linspace(0.5, 1.5, hidden, dtype=torch.float32)
+    expected = torch_path.rms_norm(x, w, epsilon)
+    actual = ops.rms_norm(x.to(device), w.to(device), epsilon)
+    torch.cuda.synchronize()
+    assert actual.dtype == expected.dtype == torch.float32
+    assert_close(actual.cpu(), expected, rtol=NORM_TOL[dtype], atol=NORM_TOL[dtype])
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_rmsnorm_model_dtype_weight(device, dtype) -> None:
+    """A weight of the model dtype gives an output of that dtype (torch promotion)."""
+
+    g = torch.Generator().manual_seed(8)
+    x = torch.randn(33, 2048, generator=g).to(dtype)
+    w = (1 + 0.02 * torch.randn(2048, generator=g)).to(dtype)
+    expected = torch_path.rms_norm(x, w, 1e-5)
+    actual = ops.rms_norm(x.to(device), w.to(device), 1e-5)
+    torch.cuda.synchronize()
+    assert actual.dtype == dtype
+    assert_close(actual.cpu(), expected, rtol=NORM_TOL[dtype], atol=NORM_TOL[dtype])
+
+
+def test_rmsnorm_fused_residual(device) -> None:
+    """x = to_bf16(h + r) is written back, then normalised (tokserve/engine/model.py:73-82)."""
+
+    g = torch.Generator().manual_seed(9)
+    h = torch.randn(17, 2048, generator=g).to(torch.bfloat16)
+    r = torch.randn(17, 2048, generator=g).to(torch.bfloat16)
+    w = (1 + 0.02 * torch.randn(2048, generator=g)).to(torch.bfloat16)
+    summed = h + r
+    expected = torch_path.rms_norm(summed, w, 1e-5)
+    res_out = torch.empty(17, 2048, dtype=torch.bfloat16, device=device)
+    actual = ops.rms_norm(h.to(device), w.to(device), 1e-5, residual=r.to(device),
+                          residual_out=res_out)
+    torch.cuda.synchronize()
+    assert torch.equal(res_out.cpu(), summed)
+    assert_close(actual.cpu(), expected, rtol=1e-2, atol=1e-2)
+
+
+def test_rmsnorm_noncontiguous_input(device) -> None:
+    x = torch.randn(2, 3, 13).transpose(0, 1)
+    w = torch.linspace(0.5, 1.5, 13)
+    expected = torch_path.rms_norm(x, w, 1e-6)
+    actual = ops.rms_norm(x.to(device), w.to(device), 1e-6)
+    torch.cuda.synchronize()
+    assert_close(actual.cpu(), expected, rtol=2e-5, atol=2e-5)
+
+
+def test_packed_norm_rope_full_shape(device) -> None:
+    """64 sequences, lengths U[1,256] (~8.2k tokens), hidden 4096, 32/8 x 128, theta 5e5, bf16."""
+
+    data = workloads.norm_rope_packed(device, seed=0)
+    normed = ops.rms_norm(data.hidden, data.weight, data.epsilon)
+    table = ops.RotaryTable(128, theta=data.theta, max_position=4096 + 257,
+                            dtype=torch.bfloat16, device=device)
+    q4 = data.query.permute(1, 0, 2).unsqueeze(0)  # (1, Hq, N, Dh) view
+    k4 = data.key.permute(1, 0, 2).unsqueeze(0)
+    rq, rk = ops.rope(q4, k4, data.positions, table)
+    torch.cuda.synchronize()
+    expected_norm = torch_path.rms_norm(data.hidden.cpu(), data.weight.cpu(), data.epsilon)
+    assert_close(normed.cpu(), expected_norm, rtol=0, atol=2e-2)
+    assert (normed.cpu() == expected_norm).float().mean() > 0.99
+    eq, ek = torch_path.apply_rope(q4.cpu(), k4.cpu(), data.positions.cpu(), theta=data.theta)
+    assert torch.equal(rq.cpu(), eq)
+    assert torch.equal(rk.cpu(), ek)
+
+
+@pytest.mark.parametrize(("batch", "hq", "hkv", "length", "dh"), [(1, 4, 2, 3, 8),
+                                                                   (2, 6, 2, 5, 16),
+                                                                   (1, 32, 4, 7, 64)])
+@pytest.mark.parametrize("start", [0, 11])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
+def test_rope_bit_exact(device, batch, hq, hkv, length, dh, start, dtype) -> None:
+    """Shapes of tests/gpu/test_triton_rope.py:30-70; the oracle is matched bit for bit."""
+
+    g = torch.Generator().manual_seed(7)
+    q = torch.randn(batch, hq, length, dh, generator=g).to(dtype)
+    k = torch.randn(batch, hkv, length, dh, generator=g).to(dtype)
+    pos = torch.arange(start, start + length, dtype=torch.int64)
+    eq, ek = torch_path.apply_rope(q, k, pos, theta=10_000.0)
+    table = ops.RotaryTable(dh, theta=10_000.0, max_position=64, dtype=dtype, device=device)
+    aq, ak = ops.rope(q.to(device), k.to(device), pos.to(device), table)
+    torch.cuda.synchronize()
+    assert torch.equal(aq.cpu(), eq)
+    assert torch.equal(ak.cpu(), ek)
+
+
+def test_rope_noncontiguous_and_in_place(device) -> None:
+    """tests/gpu/test_triton_rope.py:73-92 layout, then an in-place packed rotation."""
+
+    q = torch.randn(1, 3, 4, 8).transpose(1, 2)
+    k = torch.randn(1, 3, 2, 8).transpose(1, 2)
+    pos = torch.tensor([5, 6, 7])
+    eq, ek = torch_path.apply_rope(q, k, pos, theta=10_000.0)
+    table = ops.RotaryTable(8, theta=10_000.0, max_position=16, dtype=torch.float32,
+                            device=device)
+    aq, ak = ops.rope(q.to(device), k.to(device), pos.to(device), table)
+    torch.cuda.synchronize()
+    assert torch.equal(aq.cpu(), eq)
+    assert torch.equal(ak.cpu(), ek)
+    packed_q = q[0].transpose(0, 1).contiguous().to(device)  # (T, H, Dh)
+    packed_k = k[0].transpose(0, 1).contiguous().to(device)
+    q4 = packed_q.permute(1, 0, 2).unsqueeze(0)
+    k4 = packed_k.permute(1, 0, 2).unsqueeze(0)
+    ops.rope(q4, k4, pos.to(device), table, query_out=q4, key_out=k4)
+    torch.cuda.synchronize()
+    assert torch.equal(packed_q.cpu(), eq[0].transpose(0, 1))
+    assert torch.equal(packed_k.cpu(), ek[0].transpose(0, 1))
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_greedy_argmax_matches_torch(device, dtype) -> None:
+    g = torch.Generator().manual_seed(12)
+    logits = torch.randn(128, 32000, generator=g).to(dtype)
+    logits[3, 100] = logits[3, 7] = 50.0  # tie: first index wins
+    logits[5, 9] = float("nan")
+    logits[5, 2] = float("nan")
+    expected = torch_path.select_greedy(logits)
+    actual = ops.greedy_argmax(logits.to(device))
+    torch.cuda.synchronize()
+    assert torch.equal(actual.cpu(), expected)
+    assert int(actual[3]) == 7 and int(actual[5]) == 2

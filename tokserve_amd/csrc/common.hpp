@@ -1,0 +1,199 @@
+// Shared device helpers for the gfx950 kernels: element conversions with
+// torch's rounding (round-to-nearest-even, canonical NaN), 16-byte vector
+// access, wave64 DPP reductions and the status plumbing of the C ABI.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "tokserve_hip.h"
+
+namespace tks {
+
+// ---------------------------------------------------------------- status ---
+
+// Records the HIP error of the last failing launch for tks_last_hip_error().
+void set_hip_error(hipError_t err);
+
+inline int32_t check_launch() {
+  hipError_t err = hipGetLastError();
+  if (err != hipSuccess) {
+    set_hip_error(err);
+    return TKS_ERR_LAUNCH;
+  }
+  return TKS_OK;
+}
+
+inline bool valid_dtype(int32_t dtype) {
+  return dtype == TKS_FLOAT32 || dtype == TKS_FLOAT16 || dtype == TKS_BFLOAT16;
+}
+
+inline int elem_bytes(int32_t dtype) { return dtype == TKS_FLOAT32 ? 4 : 2; }
+
+inline bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// ------------------------------------------------------------ elements ---
+
+struct bf16_t {
+  uint16_t bits;
+};
+
+__device__ __forceinline__ float to_float(float x) { return x; }
+__device__ __forceinline__ float to_float(_Float16 x) { return static_cast<float>(x); }
+__device__ __forceinline__ float to_float(bf16_t x) {
+  return __uint_as_float(static_cast<uint32_t>(x.bits) << 16);
+}
+
+// Round-to-nearest-even float -> bfloat16, NaN -> 0x7fc0 with the sign kept
+// (the conversion c10::BFloat16 performs).
+__device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x0040u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return static_cast<uint16_t>(u >> 16);
+}
+
+template <typename T>
+__device__ __forceinline__ T from_float(float f);
+template <>
+__device__ __forceinline__ float from_float<float>(float f) {
+  return f;
+}
+template <>
+__device__ __forceinline__ _Float16 from_float<_Float16>(float f) {
+  return static_cast<_Float16>(f);
+}
+template <>
+__device__ __forceinline__ bf16_t from_float<bf16_t>(float f) {
+  return bf16_t{f32_to_bf16_bits(f)};
+}
+
+// Round a float through T and back (the `.to(dtype)` of the torch path).
+template <typename T>
+__device__ __forceinline__ float round_through(float f) {
+  return to_float(from_float<T>(f));
+}
+
+// Elements per 16-byte vector.
+template <typename T>
+struct Vec {
+  static constexpr int N = 16 / sizeof(T);
+};
+
+// 16-byte vector load/store as four dwords.
+__device__ __forceinline__ uint4 ld16(const void *p) { return *reinterpret_cast<const uint4 *>(p); }
+__device__ __forceinline__ void st16(void *p, uint4 v) { *reinterpret_cast<uint4 *>(p) = v; }
+
+// Unpack the 16-byte vector `v` of T into floats.
+template <typename T>
+__device__ __forceinline__ void unpack(uint4 v, float *out);
+template <>
+__device__ __forceinline__ void unpack<float>(uint4 v, float *out) {
+  out[0] = __uint_as_float(v.x);
+  out[1] = __uint_as_float(v.y);
+  out[2] = __uint_as_float(v.z);
+  out[3] = __uint_as_float(v.w);
+}
+template <>
+__device__ __forceinline__ void unpack<bf16_t>(uint4 v, float *out) {
+  const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    out[2 * i] = __uint_as_float(w[i] << 16);
+    out[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+  }
+}
+template <>
+__device__ __forceinline__ void unpack<_Float16>(uint4 v, float *out) {
+  const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    _Float16 lo, hi;
+    uint16_t l16 = static_cast<uint16_t>(w[i] & 0xffffu), h16 = static_cast<uint16_t>(w[i] >> 16);
+    __builtin_memcpy(&lo, &l16, 2);
+    __builtin_memcpy(&hi, &h16, 2);
+    out[2 * i] = static_cast<float>(lo);
+    out[2 * i + 1] = static_cast<float>(hi);
+  }
+}
+
+template <typename T>
+__device__ __forceinline__ uint16_t bits16(T x) {
+  uint16_t b;
+  __builtin_memcpy(&b, &x, 2);
+  return b;
+}
+
+// Pack floats (rounded to T) into a 16-byte vector.
+template <typename T>
+__device__ __forceinline__ uint4 pack(const float *in);
+template <>
+__device__ __forceinline__ uint4 pack<float>(const float *in) {
+  return make_uint4(__float_as_uint(in[0]), __float_as_uint(in[1]), __float_as_uint(in[2]),
+                    __float_as_uint(in[3]));
+}
+template <>
+__device__ __forceinline__ uint4 pack<bf16_t>(const float *in) {
+  uint32_t w[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    w[i] = static_cast<uint32_t>(f32_to_bf16_bits(in[2 * i])) |
+           (static_cast<uint32_t>(f32_to_bf16_bits(in[2 * i + 1])) << 16);
+  return make_uint4(w[0], w[1], w[2], w[3]);
+}
+template <>
+__device__ __forceinline__ uint4 pack<_Float16>(const float *in) {
+  uint32_t w[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    w[i] = static_cast<uint32_t>(bits16(static_cast<_Float16>(in[2 * i]))) |
+           (static_cast<uint32_t>(bits16(static_cast<_Float16>(in[2 * i + 1]))) << 16);
+  return make_uint4(w[0], w[1], w[2], w[3]);
+}
+
+// ------------------------------------------------------- wave reductions ---
+
+// DPP controls (GCN/CDNA encoding).
+constexpr int kDppQuadSwap1 = 0xB1;  // quad_perm [1,0,3,2]
+constexpr int kDppQuadSwap2 = 0x4E;  // quad_perm [2,3,0,1]
+constexpr int kDppHalfMirror = 0x141;
+constexpr int kDppMirror = 0x140;
+
+template <int CTRL>
+__device__ __forceinline__ float dpp(float x) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), CTRL, 0xF, 0xF, true));
+}
+
+// All-reduce over the 16 lanes of a DPP row (lanes 16r .. 16r+15).
+__device__ __forceinline__ float row16_max(float x) {
+  x = fmaxf(x, dpp<kDppQuadSwap1>(x));
+  x = fmaxf(x, dpp<kDppQuadSwap2>(x));
+  x = fmaxf(x, dpp<kDppHalfMirror>(x));
+  x = fmaxf(x, dpp<kDppMirror>(x));
+  return x;
+}
+__device__ __forceinline__ float row16_sum(float x) {
+  x += dpp<kDppQuadSwap1>(x);
+  x += dpp<kDppQuadSwap2>(x);
+  x += dpp<kDppHalfMirror>(x);
+  x += dpp<kDppMirror>(x);
+  return x;
+}
+
+// All-reduce over the 64 lanes of a wave.
+__device__ __forceinline__ float wave_sum(float x) {
+  x = row16_sum(x);
+  x += __shfl_xor(x, 16, 64);
+  x += __shfl_xor(x, 32, 64);
+  return x;
+}
+__device__ __forceinline__ float wave_max(float x) {
+  x = row16_max(x);
+  x = fmaxf(x, __shfl_xor(x, 16, 64));
+  x = fmaxf(x, __shfl_xor(x, 32, 64));
+  return x;
+}
+
+__host__ __device__ __forceinline__ int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+}  // namespace tks

@@ -1,0 +1,160 @@
+// Half-rotation RoPE on Q and K of a packed (or (B, H, T, Dh)) token stream.
+//
+//   out[d]        = r(x[d]        * cos[d]) + r(-x[d + D/2] * sin[d])
+//   out[d + D/2]  = r(x[d + D/2]  * cos[d]) + r( x[d]       * sin[d])      (d < D/2)
+//
+// with every product rounded to the element type before the add, as
+// tokserve/kernels/_triton_rope.py:63-66 and apply_rope (tokserve/engine/rope.py:150-153)
+// do. cos/sin rows come from a per-position table already cast to the element
+// type (tokserve/engine/rope.py:78-87), so the kernel only gathers and rotates.
+// One workgroup per token: the table row is read once and shared by all
+// Hq + Hkv heads; each lane rotates one 16-byte chunk of the first half
+// together with its partner chunk of the second half.
+#include "common.hpp"
+
+namespace tks {
+namespace {
+
+constexpr int kThreads = 128;
+
+struct RopeTensor {
+  const void *in;
+  void *out;
+  int64_t sb, sh, st;     // input strides (batch, head, token)
+  int64_t osb, osh, ost;  // output strides
+  int32_t heads;
+};
+
+template <typename T, int V>
+__device__ __forceinline__ void rotate(const T *x, T *y, const float *c, const float *s,
+                                       int half) {
+#pragma clang fp contract(off)
+  float x1[V], x2[V], o1[V], o2[V];
+  if constexpr (V * sizeof(T) == 16) {
+    unpack<T>(ld16(x), x1);
+    unpack<T>(ld16(x + half), x2);
+  } else {
+#pragma unroll
+    for (int j = 0; j < V; ++j) {
+      x1[j] = to_float(x[j]);
+      x2[j] = to_float(x[half + j]);
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < V; ++j) {
+    const float a1 = round_through<T>(x1[j] * c[j]);
+    const float b1 = round_through<T>(-x2[j] * s[j]);
+    const float a2 = round_through<T>(x2[j] * c[j]);
+    const float b2 = round_through<T>(x1[j] * s[j]);
+    o1[j] = a1 + b1;
+    o2[j] = a2 + b2;
+  }
+  if constexpr (V * sizeof(T) == 16) {
+    st16(y, pack<T>(o1));
+    st16(y + half, pack<T>(o2));
+  } else {
+#pragma unroll
+    for (int j = 0; j < V; ++j) {
+      y[j] = from_float<T>(o1[j]);
+      y[half + j] = from_float<T>(o2[j]);
+    }
+  }
+}
+
+template <typename T, int V>
+__global__ __launch_bounds__(kThreads) void rope_kernel(RopeTensor q, RopeTensor k,
+                                                        const int64_t *__restrict__ positions,
+                                                        const T *__restrict__ cos_cache,
+                                                        const T *__restrict__ sin_cache,
+                                                        int64_t cache_len, int32_t head_dim) {
+  const int64_t t = blockIdx.x;
+  const int64_t b = blockIdx.y;
+  const int half = head_dim / 2;
+  const int chunks = half / V;
+  int64_t pos = positions[t];
+  pos = pos < 0 ? 0 : (pos >= cache_len ? cache_len - 1 : pos);
+  const T *crow = cos_cache + pos * half;
+  const T *srow = sin_cache + pos * half;
+  const int items = (q.heads + k.heads) * chunks;
+  for (int it = threadIdx.x; it < items; it += kThreads) {
+    const int h = it / chunks;
+    const int c = (it - h * chunks) * V;
+    float cf[V], sf[V];
+    if constexpr (V * sizeof(T) == 16) {
+      unpack<T>(ld16(crow + c), cf);
+      unpack<T>(ld16(srow + c), sf);
+    } else {
+#pragma unroll
+      for (int j = 0; j < V; ++j) {
+        cf[j] = to_float(crow[c + j]);
+        sf[j] = to_float(srow[c + j]);
+      }
+    }
+    const RopeTensor &x = h < q.heads ? q : k;
+    const int hh = h < q.heads ? h : h - q.heads;
+    const T *src = static_cast<const T *>(x.in) + b * x.sb + hh * x.sh + t * x.st + c;
+    T *dst = static_cast<T *>(x.out) + b * x.osb + hh * x.osh + t * x.ost + c;
+    rotate<T, V>(src, dst, cf, sf, half);
+  }
+}
+
+bool strides_ok(const RopeTensor &x, int v) {
+  return x.sb % v == 0 && x.sh % v == 0 && x.st % v == 0 && x.osb % v == 0 &&
+         x.osh % v == 0 && x.ost % v == 0 && aligned16(x.in) && aligned16(x.out);
+}
+
+template <typename T>
+int32_t launch(const RopeTensor &q, const RopeTensor &k, int32_t batch, int64_t tokens,
+               int32_t head_dim, const int64_t *pos, const void *cc, const void *sc,
+               int64_t cache_len, hipStream_t s) {
+  constexpr int V = Vec<T>::N;
+  const int half = head_dim / 2;
+  const bool vec = half % V == 0 && aligned16(cc) && aligned16(sc) && strides_ok(q, V) &&
+                   (k.heads == 0 || strides_ok(k, V));
+  const dim3 grid(static_cast<unsigned>(tokens), batch);
+  if (vec)
+    rope_kernel<T, V><<<grid, kThreads, 0, s>>>(q, k, pos, static_cast<const T *>(cc),
+                                                static_cast<const T *>(sc), cache_len, head_dim);
+  else
+    rope_kernel<T, 1><<<grid, kThreads, 0, s>>>(q, k, pos, static_cast<const T *>(cc),
+                                                static_cast<const T *>(sc), cache_len, head_dim);
+  return check_launch();
+}
+
+}  // namespace
+}  // namespace tks
+
+using namespace tks;
+
+extern "C" int32_t tks_rope(const void *query, void *query_out, int64_t q_sb, int64_t q_sh,
+                            int64_t q_st, int64_t qo_sb, int64_t qo_sh, int64_t qo_st,
+                            int32_t num_q_heads, const void *key, void *key_out, int64_t k_sb,
+                            int64_t k_sh, int64_t k_st, int64_t ko_sb, int64_t ko_sh,
+                            int64_t ko_st, int32_t num_kv_heads, int32_t batch,
+                            int64_t num_tokens, int32_t head_dim, const int64_t *positions,
+                            const void *cos_cache, const void *sin_cache, int64_t cache_len,
+                            int32_t dtype, tks_stream_t stream) {
+  if (!valid_dtype(dtype)) return TKS_ERR_TYPE;
+  if (head_dim < 2 || head_dim % 2 != 0 || num_q_heads < 0 || num_kv_heads < 0 || batch < 0 ||
+      num_tokens < 0 || cache_len <= 0)
+    return TKS_ERR_VALUE;
+  if (batch == 0 || num_tokens == 0 || num_q_heads + num_kv_heads == 0) return TKS_OK;
+  if (num_tokens > 0x7fffffff || batch > 65535) return TKS_ERR_VALUE;
+  if ((num_q_heads > 0 && (!query || !query_out)) || (num_kv_heads > 0 && (!key || !key_out)) ||
+      !positions || !cos_cache || !sin_cache)
+    return TKS_ERR_VALUE;
+  const RopeTensor q{query, query_out, q_sb, q_sh, q_st, qo_sb, qo_sh, qo_st, num_q_heads};
+  const RopeTensor k{key, key_out, k_sb, k_sh, k_st, ko_sb, ko_sh, ko_st, num_kv_heads};
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  switch (dtype) {
+    case TKS_FLOAT32:
+      return launch<float>(q, k, batch, num_tokens, head_dim, positions, cos_cache, sin_cache,
+                           cache_len, s);
+    case TKS_FLOAT16:
+      return launch<_Float16>(q, k, batch, num_tokens, head_dim, positions, cos_cache,
+                              sin_cache, cache_len, s);
+    default:
+      return launch<bf16_t>(q, k, batch, num_tokens, head_dim, positions, cos_cache, sin_cache,
+                            cache_len, s);
+  }
+}

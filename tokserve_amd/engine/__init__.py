@@ -1,0 +1,1 @@
+"""Host-side mirror of the matching tokserve package."""

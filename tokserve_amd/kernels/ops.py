@@ -1,0 +1,477 @@
+"""Batched device operators of the hot path, one C-ABI call each.
+
+These take the packed ragged-batch metadata (`cu_seqlens`, `block_tables`,
+`seq_lens`, `slot_mapping`, `positions`) that tokserve/batching lacks (it runs
+one request at a time, tokserve/batching/execution.py:33,81). Every function
+validates shapes and devices on the host, then enqueues the kernel on the
+current torch stream. Tensors must live on a HIP device: there is no CPU path.
+"""
+
+from __future__ import annotations
+
+from math import sqrt
+
+import torch
+
+from tokserve_amd.kernels import _lib
+
+
+def require_hip(operation: str, *tensors: torch.Tensor) -> torch.device:
+    """All tensors on one HIP device (torch reports HIP tensors as is_cuda)."""
+
+    device = tensors[0].device
+    for tensor in tensors:
+        if not tensor.is_cuda:
+            raise ValueError(f"{operation} requires HIP device tensors")
+        if tensor.device != device:
+            raise ValueError(f"{operation}: tensors must use the same device")
+    return device
+
+
+def _pool_shape(key_cache: torch.Tensor, value_cache: torch.Tensor) -> tuple[int, ...]:
+    if key_cache.ndim != 5 or key_cache.shape != value_cache.shape:
+        raise ValueError("KV pools must both have shape (L, NB, Hkv, BS, Dh)")
+    if key_cache.dtype != value_cache.dtype:
+        raise ValueError("KV pools must use the same dtype")
+    if not key_cache.is_contiguous() or not value_cache.is_contiguous():
+        raise ValueError("KV pools must be contiguous")
+    return tuple(key_cache.shape)
+
+
+def _last_dim_contiguous(tensor: torch.Tensor, name: str) -> torch.Tensor:
+    return tensor if tensor.stride(-1) == 1 else tensor.contiguous()
+
+
+def _int_tensor(tensor: torch.Tensor, dtype: torch.dtype, name: str) -> torch.Tensor:
+    if tensor.dtype != dtype:
+        raise TypeError(f"{name} must be {dtype}")
+    return tensor if tensor.is_contiguous() else tensor.contiguous()
+
+
+# ----------------------------------------------------------------------------
+# KV cache
+
+
+def kv_append(
+    key: torch.Tensor,
+    value: torch.Tensor,
+    key_cache: torch.Tensor,
+    value_cache: torch.Tensor,
+    slot_mapping: torch.Tensor,
+    layer_index: int,
+) -> None:
+    """Scatter K/V rows (N, Hkv, Dh) into the pools at slot_mapping (int64, N)."""
+
+    require_hip("kv_append", key, value, key_cache, value_cache, slot_mapping)
+    num_layers, num_blocks, num_kv_heads, block_size, head_dim = _pool_shape(
+        key_cache, value_cache
+    )
+    if key.ndim != 3 or key.shape != value.shape:
+        raise ValueError("key and value must have shape (N, Hkv, Dh)")
+    if key.shape[1:] != (num_kv_heads, head_dim):
+        raise ValueError("key rows must match the pool's (Hkv, Dh)")
+    if key.dtype != key_cache.dtype or value.dtype != key_cache.dtype:
+        raise ValueError("keys and values must match the storage dtype")
+    if slot_mapping.shape != (key.shape[0],):
+        raise ValueError("slot_mapping must have shape (N,)")
+    slots = _int_tensor(slot_mapping, torch.int64, "slot_mapping")
+    key = _last_dim_contiguous(key, "key")
+    value = _last_dim_contiguous(value, "value")
+    status = _lib.load().tks_kv_append(
+        key.data_ptr(), key.stride(0), key.stride(1),
+        value.data_ptr(), value.stride(0), value.stride(1),
+        key.shape[0], key_cache.data_ptr(), value_cache.data_ptr(),
+        num_layers, num_blocks, num_kv_heads, block_size, head_dim, layer_index,
+        slots.data_ptr(), _lib.dtype_code(key.dtype), _lib.stream_of(key),
+    )
+    _lib.check(status, "kv_append")
+
+
+def paged_gather(
+    key_cache: torch.Tensor,
+    value_cache: torch.Tensor,
+    block_tables: torch.Tensor,
+    seq_lens: torch.Tensor,
+    cu_seqlens: torch.Tensor,
+    layer_index: int,
+    max_seq_len: int,
+    key_out: torch.Tensor,
+    value_out: torch.Tensor,
+) -> None:
+    """Copy each sequence's K/V in logical order into key_out/value_out.
+
+    key_out/value_out are (S_total, Hkv, Dh) views (any token/head strides, Dh
+    contiguous); sequence b fills rows cu_seqlens[b] .. cu_seqlens[b]+seq_lens[b]-1.
+    """
+
+    require_hip(
+        "paged_gather", key_cache, value_cache, block_tables, seq_lens, cu_seqlens,
+        key_out, value_out,
+    )
+    num_layers, num_blocks, num_kv_heads, block_size, head_dim = _pool_shape(
+        key_cache, value_cache
+    )
+    if block_tables.ndim != 2:
+        raise ValueError("block_tables must have shape (B, max_blocks)")
+    tables = _int_tensor(block_tables, torch.int32, "block_tables")
+    lens = _int_tensor(seq_lens, torch.int32, "seq_lens")
+    cu = _int_tensor(cu_seqlens, torch.int32, "cu_seqlens")
+    if key_out.ndim != 3 or key_out.shape[1:] != (num_kv_heads, head_dim):
+        raise ValueError("outputs must have shape (S, Hkv, Dh)")
+    if value_out.shape != key_out.shape or value_out.stride() != key_out.stride():
+        raise ValueError("key_out and value_out must share shape and strides")
+    if key_out.stride(-1) != 1:
+        raise ValueError("outputs must be contiguous in head_dim")
+    status = _lib.load().tks_paged_gather(
+        key_cache.data_ptr(), value_cache.data_ptr(), num_layers, num_blocks, num_kv_heads,
+        block_size, head_dim, layer_index, tables.data_ptr(), tables.shape[1],
+        lens.data_ptr(), cu.data_ptr(), tables.shape[0], max_seq_len,
+        key_out.data_ptr(), value_out.data_ptr(), key_out.stride(0), key_out.stride(1),
+        _lib.dtype_code(key_cache.dtype), _lib.stream_of(key_cache),
+    )
+    _lib.check(status, "paged_gather")
+
+
+# ----------------------------------------------------------------------------
+# Attention
+
+
+def decode_workspace_bytes(
+    num_seqs: int,
+    num_q_heads: int,
+    num_kv_heads: int,
+    head_dim: int,
+    block_size: int,
+    max_seq_len: int,
+    pages_per_split: int = 0,
+) -> int:
+    """Bytes of split-K scratch the decode kernel needs for this batch."""
+
+    size = _lib.load().tks_paged_attention_decode_workspace_bytes(
+        num_seqs, num_q_heads, num_kv_heads, head_dim, block_size, max_seq_len,
+        pages_per_split,
+    )
+    if size < 0:
+        raise ValueError("invalid decode workspace query")
+    return int(size)
+
+
+_workspaces: dict[torch.device, torch.Tensor] = {}
+
+
+def _workspace(device: torch.device, nbytes: int) -> torch.Tensor | None:
+    if nbytes == 0:
+        return None
+    buffer = _workspaces.get(device)
+    if buffer is None or buffer.numel() < nbytes:
+        # Zeroed once: the leading arrival counters must start at zero, and every
+        # decode launch leaves them at zero again.
+        buffer = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+        _workspaces[device] = buffer
+    return buffer
+
+
+def paged_attention_decode(
+    query: torch.Tensor,
+    key_cache: torch.Tensor,
+    value_cache: torch.Tensor,
+    block_tables: torch.Tensor,
+    seq_lens: torch.Tensor,
+    *,
+    layer_index: int,
+    max_seq_len: int,
+    scale: float | None = None,
+    out: torch.Tensor | None = None,
+    workspace: torch.Tensor | None = None,
+    pages_per_split: int = 0,
+) -> torch.Tensor:
+    """One query token per sequence: query (B, Hq, Dh) -> out (B, Hq, Dh).
+
+    Sequence b attends to its seq_lens[b] keys through block_tables[b]
+    (int32, (B, max_blocks)); max_seq_len is a host bound on seq_lens.
+    A caller-supplied `workspace` (uint8, >= decode_workspace_bytes) must be
+    zero-filled before its first use; launches leave it reusable. Launches that
+    share a workspace must be ordered on one stream.
+    """
+
+    require_hip("paged_attention_decode", query, key_cache, value_cache, block_tables, seq_lens)
+    num_layers, num_blocks, num_kv_heads, block_size, head_dim = _pool_shape(
+        key_cache, value_cache
+    )
+    if query.ndim != 3 or query.shape[2] != head_dim:
+        raise ValueError("query must have shape (B, Hq, Dh) with the pool's Dh")
+    if query.dtype != key_cache.dtype:
+        raise ValueError("query and paged storage must use the same dtype")
+    num_seqs, num_q_heads, _ = query.shape
+    if num_q_heads % num_kv_heads != 0:
+        raise ValueError("query head count must be divisible by KV head count")
+    tables = _int_tensor(block_tables, torch.int32, "block_tables")
+    lens = _int_tensor(seq_lens, torch.int32, "seq_lens")
+    if tables.ndim != 2 or tables.shape[0] != num_seqs or lens.shape != (num_seqs,):
+        raise ValueError("block_tables (B, max_blocks) and seq_lens (B,) must match query")
+    query = _last_dim_contiguous(query, "query")
+    if out is None:
+        out = torch.empty(query.shape, dtype=query.dtype, device=query.device)
+    if scale is None:
+        scale = 1.0 / sqrt(head_dim)
+    library = _lib.load()
+    nbytes = decode_workspace_bytes(
+        num_seqs, num_q_heads, num_kv_heads, head_dim, block_size, max_seq_len, pages_per_split
+    )
+    if workspace is None:
+        workspace = _workspace(query.device, nbytes)
+    status = library.tks_paged_attention_decode(
+        query.data_ptr(), query.stride(0), query.stride(1),
+        key_cache.data_ptr(), value_cache.data_ptr(), num_layers, num_blocks, num_kv_heads,
+        block_size, head_dim, layer_index, tables.data_ptr(), tables.shape[1],
+        lens.data_ptr(), num_seqs, num_q_heads, max_seq_len, scale, pages_per_split,
+        out.data_ptr(), out.stride(0), out.stride(1),
+        _lib.ptr(workspace), 0 if workspace is None else workspace.numel(),
+        _lib.dtype_code(query.dtype), _lib.stream_of(query),
+    )
+    _lib.check(status, "paged_attention_decode")
+    return out
+
+
+def paged_attention_prefill(
+    query: torch.Tensor,
+    key_cache: torch.Tensor,
+    value_cache: torch.Tensor,
+    block_tables: torch.Tensor,
+    seq_lens: torch.Tensor,
+    cu_seqlens_q: torch.Tensor,
+    *,
+    layer_index: int,
+    max_query_len: int,
+    max_seq_len: int,
+    scale: float | None = None,
+    out: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """Causal attention of packed query chunks (N, Hq, Dh) over their paged KV.
+
+    Sequence b owns query rows cu_seqlens_q[b] .. cu_seqlens_q[b+1]-1; its
+    seq_lens[b] keys already include those rows, so query i sits at absolute
+    position seq_lens[b] - q_len_b + i.
+    """
+
+    require_hip(
+        "paged_attention_prefill", query, key_cache, value_cache, block_tables, seq_lens,
+        cu_seqlens_q,
+    )
+    num_layers, num_blocks, num_kv_heads, block_size, head_dim = _pool_shape(
+        key_cache, value_cache
+    )
+    if query.ndim != 3 or query.shape[2] != head_dim:
+        raise ValueError("query must have shape (N, Hq, Dh) with the pool's Dh")
+    if query.dtype != key_cache.dtype:
+        raise ValueError("query and paged storage must use the same dtype")
+    num_q_heads = query.shape[1]
+    if num_q_heads % num_kv_heads != 0:
+        raise ValueError("query head count must be divisible by KV head count")
+    tables = _int_tensor(block_tables, torch.int32, "block_tables")
+    lens = _int_tensor(seq_lens, torch.int32, "seq_lens")
+    cu = _int_tensor(cu_seqlens_q, torch.int32, "cu_seqlens_q")
+    num_seqs = lens.shape[0]
+    if tables.ndim != 2 or tables.shape[0] != num_seqs or cu.shape != (num_seqs + 1,):
+        raise ValueError("block_tables (B, max_blocks), seq_lens (B,), cu_seqlens_q (B+1,)")
+    query = _last_dim_contiguous(query, "query")
+    if out is None:
+        out = torch.empty(query.shape, dtype=query.dtype, device=query.device)
+    if scale is None:
+        scale = 1.0 / sqrt(head_dim)
+    status = _lib.load().tks_paged_attention_prefill(
+        query.data_ptr(), query.stride(0), query.stride(1),
+        key_cache.data_ptr(), value_cache.data_ptr(), num_layers, num_blocks, num_kv_heads,
+        block_size, head_dim, layer_index, tables.data_ptr(), tables.shape[1],
+        lens.data_ptr(), cu.data_ptr(), num_seqs, query.shape[0], num_q_heads,
+        max_query_len, max_seq_len, scale, out.data_ptr(), out.stride(0), out.stride(1),
+        _lib.dtype_code(query.dtype), _lib.stream_of(query),
+    )
+    _lib.check(status, "paged_attention_prefill")
+    return out
+
+
+# ----------------------------------------------------------------------------
+# RMSNorm
+
+
+def rms_norm(
+    inputs: torch.Tensor,
+    weight: torch.Tensor,
+    epsilon: float,
+    *,
+    residual: torch.Tensor | None = None,
+    residual_out: torch.Tensor | None = None,
+    out: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """weight * to_in(x * rsqrt(mean(x^2) + eps)) over the last dimension.
+
+    With `residual`, x = to_in(inputs + residual) is first written to
+    `residual_out` (defaults to a new tensor, returned via the second slot of
+    the tuple when residual is given).
+    """
+
+    require_hip("rms_norm", inputs, weight)
+    hidden = inputs.shape[-1]
+    if weight.shape != (hidden,):
+        raise ValueError("weight must have shape (D,)")
+    out_dtype = torch.promote_types(weight.dtype, inputs.dtype)
+    rows_in = inputs.reshape(-1, hidden)
+    if rows_in.stride(-1) != 1:
+        rows_in = rows_in.contiguous()
+    weight = weight.contiguous()
+    if out is None:
+        out = torch.empty(inputs.shape, dtype=out_dtype, device=inputs.device)
+    rows_out = out.view(-1, hidden)
+    res_rows = res_out_rows = None
+    if residual is not None:
+        require_hip("rms_norm", residual)
+        if residual.shape != inputs.shape or residual.dtype != inputs.dtype:
+            raise ValueError("residual must match inputs")
+        res_rows = residual.reshape(-1, hidden)
+        if res_rows.stride(-1) != 1:
+            res_rows = res_rows.contiguous()
+        if residual_out is None:
+            residual_out = torch.empty_like(inputs)
+        res_out_rows = residual_out.view(-1, hidden)
+    status = _lib.load().tks_rms_norm(
+        rows_in.data_ptr(), rows_in.stride(0),
+        _lib.ptr(res_rows), 0 if res_rows is None else res_rows.stride(0),
+        _lib.ptr(res_out_rows), 0 if res_out_rows is None else res_out_rows.stride(0),
+        weight.data_ptr(), rows_out.data_ptr(), rows_out.stride(0),
+        rows_in.shape[0], hidden, float(epsilon),
+        _lib.dtype_code(inputs.dtype), _lib.dtype_code(weight.dtype), _lib.dtype_code(out_dtype),
+        _lib.stream_of(inputs),
+    )
+    _lib.check(status, "rms_norm")
+    return out
+
+
+# ----------------------------------------------------------------------------
+# RoPE
+
+
+class RotaryTable:
+    """Per-position cos/sin rows, (cache_len, Dh/2) each, in the model dtype.
+
+    Row p holds cos/sin(fp32(p) * inv_freq) cast to dtype, with
+    inv_freq = theta ** (-arange(0, Dh, 2) / Dh) in fp32: the values
+    rotary_cos_sin computes (tokserve/engine/rope.py:28-87). The table is
+    computed once with torch on the host and copied to the device; the kernel
+    only gathers rows by position.
+    """
+
+    def __init__(
+        self,
+        head_dim: int,
+        *,
+        theta: float,
+        max_position: int,
+        dtype: torch.dtype,
+        device: torch.device,
+    ) -> None:
+        if head_dim < 2 or head_dim % 2 != 0:
+            raise ValueError("head_dim must be a positive even integer")
+        if theta <= 0.0:
+            raise ValueError("theta must be positive")
+        if max_position < 1:
+            raise ValueError("max_position must be positive")
+        self.head_dim = head_dim
+        self.theta = theta
+        self.dtype = dtype
+        self.device = torch.device(device)
+        self.length = 0
+        self.cos = torch.empty(0)
+        self.sin = torch.empty(0)
+        self.ensure(max_position)
+
+    def ensure(self, max_position: int) -> None:
+        """Grow the table to cover positions [0, max_position)."""
+
+        if max_position <= self.length:
+            return
+        length = max(max_position, 2 * self.length)
+        indices = torch.arange(0, self.head_dim, 2, dtype=torch.float32)
+        inv_freq = self.theta ** (-indices / self.head_dim)
+        positions = torch.arange(length, dtype=torch.int64).to(torch.float32)
+        angles = torch.outer(positions, inv_freq)
+        self.cos = angles.cos().to(self.dtype).to(self.device).contiguous()
+        self.sin = angles.sin().to(self.dtype).to(self.device).contiguous()
+        self.length = length
+
+
+def rope(
+    query: torch.Tensor,
+    key: torch.Tensor,
+    positions: torch.Tensor,
+    table: RotaryTable,
+    *,
+    query_out: torch.Tensor | None = None,
+    key_out: torch.Tensor | None = None,
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """Rotate Q (B, Hq, T, Dh) and K (B, Hkv, T, Dh) at positions (T,) in one launch.
+
+    Packed streams pass (1, H, N, Dh) views of (N, H, Dh) tensors. Outputs may
+    alias the inputs (in-place rotation). Positions must lie in [0, table.length).
+    """
+
+    require_hip("rope", query, key, positions)
+    if query.ndim != 4 or key.ndim != 4:
+        raise ValueError("query and key must have shape (B, H, T, Dh)")
+    if query.shape[0] != key.shape[0] or query.shape[2:] != key.shape[2:]:
+        raise ValueError("query and key batch, sequence and head dimensions must match")
+    if query.dtype != key.dtype or query.dtype != table.dtype:
+        raise ValueError("query, key and the rotary table must use the same dtype")
+    if query.shape[-1] != table.head_dim:
+        raise ValueError("head_dim must match the rotary table")
+    if positions.shape != (query.shape[2],):
+        raise ValueError("positions must have shape (T,)")
+    pos = positions if positions.dtype == torch.int64 else positions.to(torch.int64)
+    pos = pos.contiguous()
+    query = _last_dim_contiguous(query, "query")
+    key = _last_dim_contiguous(key, "key")
+    if query_out is None:
+        query_out = torch.empty(query.shape, dtype=query.dtype, device=query.device)
+    if key_out is None:
+        key_out = torch.empty(key.shape, dtype=key.dtype, device=key.device)
+    if query_out.stride(-1) != 1 or key_out.stride(-1) != 1:
+        raise ValueError("rope outputs must be contiguous in head_dim")
+    batch, num_q_heads, tokens, head_dim = query.shape
+    status = _lib.load().tks_rope(
+        query.data_ptr(), query_out.data_ptr(),
+        query.stride(0), query.stride(1), query.stride(2),
+        query_out.stride(0), query_out.stride(1), query_out.stride(2), num_q_heads,
+        key.data_ptr(), key_out.data_ptr(),
+        key.stride(0), key.stride(1), key.stride(2),
+        key_out.stride(0), key_out.stride(1), key_out.stride(2), key.shape[1],
+        batch, tokens, head_dim, pos.data_ptr(), table.cos.data_ptr(), table.sin.data_ptr(),
+        table.length, _lib.dtype_code(query.dtype), _lib.stream_of(query),
+    )
+    _lib.check(status, "rope")
+    return query_out, key_out
+
+
+# ----------------------------------------------------------------------------
+# Greedy selection
+
+
+def greedy_argmax(logits: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """(B, V) logits -> (B, 1) int64 first-maximum indices (torch.argmax rules)."""
+
+    require_hip("greedy_argmax", logits)
+    if logits.ndim != 2:
+        raise ValueError("logits must have shape (B, V)")
+    if logits.shape[0] < 1:
+        raise ValueError("logits must contain at least one batch row")
+    if logits.shape[1] < 1:
+        raise ValueError("vocabulary size must be positive")
+    if logits.stride(-1) != 1:
+        logits = logits.contiguous()
+    if out is None:
+        out = torch.empty((logits.shape[0], 1), dtype=torch.int64, device=logits.device)
+    status = _lib.load().tks_argmax(
+        logits.data_ptr(), logits.stride(0), logits.shape[0], logits.shape[1],
+        out.data_ptr(), _lib.dtype_code(logits.dtype), _lib.stream_of(logits),
+    )
+    _lib.check(status, "greedy_argmax")
+    return out
