@@ -51,7 +51,8 @@ def measured_traffic() -> float | None:
 
 def cpu_baseline(batch, target_seconds: float) -> dict:
     """Time the oracle's per-request decode (gather + repeat_kv + causal_attention, bf16)
-    on the host for the first sequences of the workload, until target_seconds."""
+    on the host over the sequences of the same workload, in batch order, repeating whole
+    passes until target_seconds of CPU work (at least one full pass)."""
 
     import torch
 
@@ -61,33 +62,32 @@ def cpu_baseline(batch, target_seconds: float) -> dict:
     torch.set_num_threads(cores)
     _, _, hkv, bs, dh = batch.key_cache.shape
     elem = batch.key_cache.element_size()
-    done_bytes = 0
-    elapsed = 0.0
-    seqs = 0
-    for b in range(batch.num_seqs):
+    requests = []
+    for b in range(batch.num_seqs):  # compact CPU pool per sequence (copy not timed)
         ctx = batch.contexts[b]
         nblk = (ctx + bs - 1) // bs
         ids = batch.block_tables[b, :nblk].long()
-        kc = batch.key_cache[:, ids].cpu()  # compact CPU pool of this sequence's blocks
-        vc = batch.value_cache[:, ids].cpu()
-        q = batch.query[b : b + 1].cpu()
-        table = torch.arange(nblk, dtype=torch.int32).unsqueeze(0)
-        lens = torch.tensor([ctx], dtype=torch.int32)
+        requests.append((batch.query[b : b + 1].cpu(), batch.key_cache[:, ids].cpu(),
+                         batch.value_cache[:, ids].cpu(),
+                         torch.arange(nblk, dtype=torch.int32).unsqueeze(0),
+                         torch.tensor([ctx], dtype=torch.int32)))
+    per_pass = sum(c * hkv * dh * 2 * elem for c in batch.contexts) + 2 * batch.query.numel() * elem
+    elapsed = 0.0
+    passes = 0
+    while passes == 0 or elapsed < target_seconds:
         start = time.perf_counter()
-        paged.decode_batch(q, kc, vc, table, lens, 0)
+        for q, kc, vc, table, lens in requests:
+            paged.decode_batch(q, kc, vc, table, lens, 0)
         elapsed += time.perf_counter() - start
-        done_bytes += ctx * hkv * dh * 2 * elem + 2 * q.numel() * elem
-        seqs += 1
-        if elapsed >= target_seconds:
-            break
+        passes += 1
     return {
-        "value": round(done_bytes / elapsed / 1e9, 4),
+        "value": round(per_pass * passes / elapsed / 1e9, 4),
         "unit": "GB/s",
         "cores": cores,
         "kind": "port",
-        "sample": f"first {seqs} of {batch.num_seqs} sequences of the same workload, "
-                  f"per-request torch-backend decode (bf16) on {cores} host threads, "
-                  f"{elapsed:.1f} s",
+        "sample": f"{passes} full pass(es) over all {batch.num_seqs} sequences of the same "
+                  f"workload, per-request torch-backend decode (bf16) on {cores} host "
+                  f"threads, {elapsed:.1f} s",
     }
 
 
@@ -100,6 +100,8 @@ def main() -> int:
     parser.add_argument("--pages-per-split", type=int, default=0)
     parser.add_argument("--cpu-seconds", type=float, default=10.0)
     parser.add_argument("--no-cpu-baseline", action="store_true")
+    parser.add_argument("--copy-calibration", action="store_true",
+                        help="after the bench, run a 1 GiB device copy (counter calibration)")
     args = parser.parse_args()
 
     if args.gpus != 1:
@@ -118,12 +120,14 @@ def main() -> int:
     nbytes = ops.decode_workspace_bytes(batch.num_seqs, 32, 8, 128, 16, batch.max_seq_len,
                                         args.pages_per_split)
     workspace = torch.zeros(max(nbytes, 1), dtype=torch.uint8, device=device)
+    # Host-side plan from the lengths the scheduler holds: longest sequences first.
+    order = ops.longest_first(batch.contexts, device)
 
     def step() -> None:
         ops.paged_attention_decode(
             batch.query, batch.key_cache, batch.value_cache, batch.block_tables,
             batch.seq_lens, layer_index=0, max_seq_len=batch.max_seq_len, out=out,
-            workspace=workspace, pages_per_split=args.pages_per_split,
+            workspace=workspace, pages_per_split=args.pages_per_split, seq_order=order,
         )
 
     for _ in range(args.warmup):
@@ -162,6 +166,7 @@ def main() -> int:
             "context_tokens": sum(batch.contexts),
             "algorithmic_bytes_per_step": total_bytes,
             "pages_per_split": args.pages_per_split or "auto",
+            "schedule": "longest-first sequence order (host plan)",
         },
         "pct_of_peak_hbm": round(100.0 * achieved / PEAK_HBM_GBPS, 2),
         "decode_tokens_per_s_one_layer": round(batch.num_seqs / (ms * 1e-3), 1),
@@ -177,7 +182,24 @@ def main() -> int:
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(batch, args.cpu_seconds)
     print(json.dumps(result), flush=True)
+    if args.copy_calibration:
+        copy_calibration(device)
     return 0
+
+
+def copy_calibration(device, gib: int = 1, repeats: int = 5) -> None:
+    """A plain device copy of known size, for scaling rocprofv3 FETCH_SIZE/WRITE_SIZE:
+    each launch reads and writes exactly `gib` GiB."""
+
+    import torch
+
+    src = torch.empty(gib << 30, dtype=torch.uint8, device=device).fill_(1)
+    dst = torch.empty_like(src)
+    for _ in range(repeats):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_calibration_bytes_per_launch": gib << 30, "launches": repeats}),
+          flush=True)
 
 
 if __name__ == "__main__":

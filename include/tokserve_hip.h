@@ -108,14 +108,19 @@ int32_t tks_paged_gather(const void *key_cache, const void *value_cache, int32_t
  * through block_tables[b*block_table_stride + p/BS]:
  *   out = softmax(scale * q.K^T) V, accumulated in fp32, stored in `dtype`.
  * max_seq_len (host) bounds every seq_lens[b] and sizes the grid.
- * pages_per_split: KV blocks per split-K work item (0 = library heuristic).
- * The workspace holds one arrival counter per (sequence, KV head) followed by
- * the split partials; its size comes from
- * tks_paged_attention_decode_workspace_bytes with the same arguments. The
- * counters must be zero before the first launch (allocate the workspace zeroed
- * once); every launch leaves them zero. The last split of a (sequence, KV head)
- * to finish merges the partials, so one call is one kernel launch. Launches
- * sharing a workspace must be stream-ordered.
+ * pages_per_split: KV blocks per workgroup along the keys (0 = library
+ * heuristic: a whole sequence per workgroup when the batch has at least 1024
+ * (sequence, KV head) pairs, otherwise split so the GPU fills). When some
+ * sequence spans more than one split, the partials go to the workspace and a
+ * second kernel merges them; the workspace size comes from
+ * tks_paged_attention_decode_workspace_bytes with the same arguments (0 when
+ * no split is needed; workspace may then be NULL). No initial contents are
+ * required. Launches sharing a workspace must be stream-ordered.
+ * seq_order (device int32 [num_seqs], may be NULL): the order in which
+ * sequences are handed to workgroups, a permutation of 0..num_seqs-1. Passing
+ * the sequences longest-first (a host-side plan built from the lengths the
+ * scheduler already knows) removes the tail of long sequences started last;
+ * results do not depend on it.
  * A sequence with seq_lens[b] == 0 gets an all-zero output row.
  */
 int64_t tks_paged_attention_decode_workspace_bytes(int32_t num_seqs, int32_t num_q_heads,
@@ -128,7 +133,8 @@ int32_t tks_paged_attention_decode(const void *query, int64_t q_seq_stride, int6
                                    int32_t num_layers, int64_t num_blocks, int32_t num_kv_heads,
                                    int32_t block_size, int32_t head_dim, int32_t layer_index,
                                    const int32_t *block_tables, int32_t block_table_stride,
-                                   const int32_t *seq_lens, int32_t num_seqs, int32_t num_q_heads,
+                                   const int32_t *seq_lens, const int32_t *seq_order,
+                                   int32_t num_seqs, int32_t num_q_heads,
                                    int32_t max_seq_len, float scale, int32_t pages_per_split,
                                    void *out, int64_t out_seq_stride, int64_t out_head_stride,
                                    void *workspace, int64_t workspace_bytes, int32_t dtype,

@@ -68,7 +68,7 @@ def test_argument_validation_happens_before_any_launch() -> None:
     ) == _lib.TKS_OK
     # Query heads not divisible by KV heads.
     assert library.tks_paged_attention_decode(
-        None, 0, 0, None, None, 1, 4, 3, 16, 64, 0, None, 4, None, 1, 8, 16, 1.0, 0,
+        None, 0, 0, None, None, 1, 4, 3, 16, 64, 0, None, 4, None, None, 1, 8, 16, 1.0, 0,
         None, 0, 0, None, 0, 2, None
     ) == _lib.TKS_ERR_VALUE
     # RMSNorm: bf16 weight with fp32 output breaks torch promotion.
@@ -86,11 +86,10 @@ def test_decode_workspace_sizes() -> None:
     library = _lib.load()
     # A single split needs no workspace.
     assert library.tks_paged_attention_decode_workspace_bytes(4, 32, 8, 128, 16, 256, 32) == 0
-    # Arrival counters (rows * Hkv int32, padded to 64) then split partials:
-    # rows * heads * splits * (2 + Dh) floats with m and l padded to 64.
+    # Split partials: rows * heads * splits * (2 + Dh) floats with m and l padded to 64
+    # (nothing else: splits are merged by a second launch).
     size = library.tks_paged_attention_decode_workspace_bytes(2, 4, 1, 64, 16, 1024, 16)
     splits = 4
     n = 2 * 4 * splits
-    counters = (2 * 1 + 63) // 64 * 64
-    assert size == counters * 4 + (2 * ((n + 63) // 64 * 64) + n * 64) * 4
+    assert size == (2 * ((n + 63) // 64 * 64) + n * 64) * 4
     assert library.tks_paged_attention_decode_workspace_bytes(-1, 4, 1, 64, 16, 1024, 16) == -1

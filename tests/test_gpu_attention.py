@@ -81,6 +81,25 @@ def test_decode_split_k_matches_oracle(device, dtype, pages_per_split) -> None:
     assert_close(out.cpu(), _decode_oracle(batch), **TOL[dtype])
 
 
+@pytest.mark.parametrize("pages_per_split", [0, 16])
+def test_decode_sequence_order_does_not_change_results(device, pages_per_split) -> None:
+    """Any schedule permutation gives bit-identical outputs (the plan is only an order)."""
+
+    contexts = [40, 3000, 17, 900, 1, 2200]
+    batch = workloads.paged_batch(contexts, [1] * 6, num_q_heads=32, num_kv_heads=8,
+                                  head_dim=128, block_size=16, dtype=torch.bfloat16,
+                                  device=device, seed=21)
+    natural = _decode(batch, pages_per_split=pages_per_split)
+    planned = _decode(batch, pages_per_split=pages_per_split,
+                      seq_order=ops.longest_first(contexts, device))
+    reverse = _decode(batch, pages_per_split=pages_per_split,
+                      seq_order=torch.arange(5, -1, -1, dtype=torch.int32, device=device))
+    torch.cuda.synchronize()
+    assert torch.equal(planned, natural)
+    assert torch.equal(reverse, natural)
+    assert_close(natural.cpu(), _decode_oracle(batch), **TOL[torch.bfloat16])
+
+
 def test_decode_empty_sequence_gives_zeros(device) -> None:
     batch = workloads.paged_batch([0, 33], [1, 1], num_q_heads=32, num_kv_heads=8, head_dim=128,
                                   block_size=16, dtype=torch.bfloat16, device=device, seed=3)
@@ -105,7 +124,7 @@ def test_decode_llama3_8b_full_size_properties(device) -> None:
     (3) a constant V row is reproduced exactly up to bf16 rounding."""
 
     batch = workloads.decode_llama3_8b(device, seed=0)
-    out = _decode(batch)
+    out = _decode(batch, seq_order=ops.longest_first(batch.contexts, device))
     nb = batch.key_cache.shape[1]
     perm = torch.randperm(nb, generator=torch.Generator().manual_seed(5)).to(device)
     inverse = torch.empty_like(perm)

@@ -1,0 +1,108 @@
+// Pieces shared by the paged-attention kernels: pool addressing, MFMA operand
+// types, split-K arrival/merge, and the argument blocks of the launchers.
+//
+// Scores are kept in the log2 domain: s2 = (q.k) * scale * log2(e), p = 2^(s2 - m).
+#pragma once
+
+#include "common.hpp"
+
+namespace tks {
+
+constexpr float kLog2e = 1.4426950408889634f;
+
+struct PoolView {
+  int64_t layer_base;    // layer * NB * Hkv * BS * Dh
+  int64_t block_stride;  // Hkv * BS * Dh
+  int64_t head_stride;   // BS * Dh
+  int64_t num_blocks;
+  int32_t block_size;
+  int32_t head_dim;
+};
+
+// Block id clamped into the pool, so a corrupt table entry cannot address
+// memory outside it.
+__device__ __forceinline__ int64_t clamp_block(int64_t blk, int64_t num_blocks) {
+  blk = blk < 0 ? 0 : blk;
+  return blk >= num_blocks ? num_blocks - 1 : blk;
+}
+
+__device__ __forceinline__ int64_t block_of(const int32_t *__restrict__ bt_row, int64_t page,
+                                            int64_t num_blocks) {
+  return clamp_block(bt_row[page], num_blocks);
+}
+
+// 2^x on the hardware exp unit (flushes results below 2^-126 to zero, exact at -inf).
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Merged output element of one (row, head, dim) from n_splits partials at w.
+__device__ __forceinline__ float merge_splits(const float *__restrict__ ws_m,
+                                              const float *__restrict__ ws_l,
+                                              const float *__restrict__ ws_acc, int64_t w,
+                                              int n_splits, int head_dim, int d, float *inv_l) {
+  float M = -INFINITY;
+  for (int s = 0; s < n_splits; ++s) M = fmaxf(M, ws_m[w + s]);
+  float L = 0.f, o = 0.f;
+  for (int s = 0; s < n_splits; ++s) {
+    const float e = exp2f(ws_m[w + s] - M);
+    L += e * ws_l[w + s];
+    o += e * ws_acc[(w + s) * head_dim + d];
+  }
+  *inv_l = 1.f / L;
+  return o;
+}
+
+template <typename T>
+struct Mfma;
+template <>
+struct Mfma<bf16_t> {
+  typedef __bf16 v8 __attribute__((ext_vector_type(8)));
+  typedef float f4 __attribute__((ext_vector_type(4)));
+  static __device__ __forceinline__ f4 run(v8 a, v8 b, f4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+  }
+};
+template <>
+struct Mfma<_Float16> {
+  typedef _Float16 v8 __attribute__((ext_vector_type(8)));
+  typedef float f4 __attribute__((ext_vector_type(4)));
+  static __device__ __forceinline__ f4 run(v8 a, v8 b, f4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+  }
+};
+
+template <typename T>
+__device__ __forceinline__ typename Mfma<T>::v8 as_v8(uint4 v) {
+  typename Mfma<T>::v8 r;
+  __builtin_memcpy(&r, &v, 16);
+  return r;
+}
+
+struct DecodeArgs {
+  const void *q;
+  int64_t q_ss, q_hs;
+  const void *kc, *vc;
+  PoolView pool;
+  const int32_t *bt;
+  int32_t bt_stride;
+  const int32_t *seq_lens;
+  const int32_t *seq_order;  // workgroup z -> sequence (null: identity)
+  int32_t num_q_heads;
+  float scale_log2;
+  int32_t pages_per_split;
+  int32_t max_splits;
+  int32_t key_cap;  // keys any sequence may have: min(table width, splits * split size) * BS
+  void *out;
+  int64_t o_ss, o_hs;
+  float *ws_m, *ws_l, *ws_acc;
+};
+
+// Shapes the MFMA decode kernel is instantiated for (block size 16).
+bool decode_mfma_supported(int32_t dtype, int32_t head_dim, int32_t group);
+
+// Launches the MFMA decode kernel over grid (max_splits, Hkv, B); returns a tks_status.
+// With max_splits == 1 it writes the output, otherwise split partials to be merged.
+int32_t launch_decode_mfma(const DecodeArgs &a, int32_t dtype, int32_t num_seqs,
+                           int32_t num_kv_heads, int32_t group, int32_t head_dim,
+                           hipStream_t stream);
+
+}  // namespace tks

@@ -15,7 +15,7 @@ from pathlib import Path
 import torch
 
 LIBRARY_NAME = "libtokserve_hip.so"
-ABI_VERSION = 1
+ABI_VERSION = 4
 
 TKS_OK = 0
 TKS_ERR_VALUE = -1
@@ -53,7 +53,8 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "tks_paged_attention_decode": (
         _i32,
         [_c_void_p, _i64, _i64, _c_void_p, _c_void_p, _i32, _i64, _i32, _i32, _i32, _i32,
-         _c_void_p, _i32, _c_void_p, _i32, _i32, _i32, _f32, _i32, _c_void_p, _i64, _i64,
+         _c_void_p, _i32, _c_void_p, _c_void_p, _i32, _i32, _i32, _f32, _i32, _c_void_p,
+         _i64, _i64,
          _c_void_p, _i64, _i32, _c_void_p],
     ),
     "tks_paged_attention_prefill": (

@@ -164,11 +164,20 @@ def _workspace(device: torch.device, nbytes: int) -> torch.Tensor | None:
         return None
     buffer = _workspaces.get(device)
     if buffer is None or buffer.numel() < nbytes:
-        # Zeroed once: the leading arrival counters must start at zero, and every
-        # decode launch leaves them at zero again.
-        buffer = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+        buffer = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
         _workspaces[device] = buffer
     return buffer
+
+
+def longest_first(seq_lens: list[int], device: torch.device | str) -> torch.Tensor:
+    """Host-side decode plan: sequence indices by decreasing length (int32, on device).
+
+    Built from the lengths the scheduler already holds on the host; ties keep
+    batch order so the plan is deterministic.
+    """
+
+    order = sorted(range(len(seq_lens)), key=lambda b: (-seq_lens[b], b))
+    return torch.tensor(order, dtype=torch.int32).to(device)
 
 
 def paged_attention_decode(
@@ -184,14 +193,18 @@ def paged_attention_decode(
     out: torch.Tensor | None = None,
     workspace: torch.Tensor | None = None,
     pages_per_split: int = 0,
+    seq_order: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """One query token per sequence: query (B, Hq, Dh) -> out (B, Hq, Dh).
 
     Sequence b attends to its seq_lens[b] keys through block_tables[b]
     (int32, (B, max_blocks)); max_seq_len is a host bound on seq_lens.
-    A caller-supplied `workspace` (uint8, >= decode_workspace_bytes) must be
-    zero-filled before its first use; launches leave it reusable. Launches that
-    share a workspace must be ordered on one stream.
+    `workspace` (uint8, >= decode_workspace_bytes) holds split partials when a
+    sequence is split across workgroups; it defaults to a per-device buffer.
+    Launches that share a workspace must be ordered on one stream.
+    `seq_order` (int32 permutation of 0..B-1, see longest_first) is the order in
+    which sequences reach workgroups; longest-first avoids a tail of long
+    sequences. Results do not depend on it.
     """
 
     require_hip("paged_attention_decode", query, key_cache, value_cache, block_tables, seq_lens)
@@ -214,6 +227,12 @@ def paged_attention_decode(
         out = torch.empty(query.shape, dtype=query.dtype, device=query.device)
     if scale is None:
         scale = 1.0 / sqrt(head_dim)
+    order = None
+    if seq_order is not None:
+        require_hip("paged_attention_decode", query, seq_order)
+        order = _int_tensor(seq_order, torch.int32, "seq_order")
+        if order.shape != (num_seqs,):
+            raise ValueError("seq_order must have shape (B,)")
     library = _lib.load()
     nbytes = decode_workspace_bytes(
         num_seqs, num_q_heads, num_kv_heads, head_dim, block_size, max_seq_len, pages_per_split
@@ -224,7 +243,8 @@ def paged_attention_decode(
         query.data_ptr(), query.stride(0), query.stride(1),
         key_cache.data_ptr(), value_cache.data_ptr(), num_layers, num_blocks, num_kv_heads,
         block_size, head_dim, layer_index, tables.data_ptr(), tables.shape[1],
-        lens.data_ptr(), num_seqs, num_q_heads, max_seq_len, scale, pages_per_split,
+        lens.data_ptr(), _lib.ptr(order), num_seqs, num_q_heads, max_seq_len, scale,
+        pages_per_split,
         out.data_ptr(), out.stride(0), out.stride(1),
         _lib.ptr(workspace), 0 if workspace is None else workspace.numel(),
         _lib.dtype_code(query.dtype), _lib.stream_of(query),
