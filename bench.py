@@ -100,6 +100,8 @@ def main() -> int:
     parser.add_argument("--pages-per-split", type=int, default=0)
     parser.add_argument("--cpu-seconds", type=float, default=10.0)
     parser.add_argument("--no-cpu-baseline", action="store_true")
+    parser.add_argument("--no-secondary", action="store_true",
+                        help="skip the mixed-step and packed norm/RoPE measurements")
     parser.add_argument("--copy-calibration", action="store_true",
                         help="after the bench, run a 1 GiB device copy (counter calibration)")
     args = parser.parse_args()
@@ -179,12 +181,123 @@ def main() -> int:
             "traffic": traffic,
         },
     }
+    if not args.no_secondary:
+        result["secondary"] = {
+            "mixed_step": measure_mixed(device, 20, 5),
+            "norm_rope": measure_norm_rope(device, 20, 5),
+        }
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(batch, args.cpu_seconds)
     print(json.dumps(result), flush=True)
     if args.copy_calibration:
         copy_calibration(device)
     return 0
+
+
+def _time_ms(fn, steps: int, warmup: int) -> float:
+    """Mean time of fn() over `steps` launches, HIP events on the current stream."""
+
+    import torch
+
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(steps):
+        fn()
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / steps
+
+
+def measure_mixed(device, steps: int, warmup: int) -> dict:
+    """Mixed chunked-prefill + decode step (Llama-3-8B layer shape, bf16): 16 chunks of
+    512 tokens on prior contexts U[0, 2048] and 240 decodes on contexts U[256, 4096]."""
+
+    import torch
+
+    from tokserve_amd import workloads
+    from tokserve_amd.kernels import ops
+
+    pre, dec = workloads.mixed_llama3_8b(device, seed=0)
+    out_p = torch.empty_like(pre.query)
+    out_d = torch.empty_like(dec.query)
+    order = ops.longest_first(dec.contexts, device)
+
+    def prefill() -> None:
+        ops.paged_attention_prefill(
+            pre.query, pre.key_cache, pre.value_cache, pre.block_tables, pre.seq_lens,
+            pre.cu_seqlens_q, layer_index=0, max_query_len=pre.max_query_len,
+            max_seq_len=pre.max_seq_len, out=out_p)
+
+    def decode() -> None:
+        ops.paged_attention_decode(
+            dec.query, dec.key_cache, dec.value_cache, dec.block_tables, dec.seq_lens,
+            layer_index=0, max_seq_len=dec.max_seq_len, out=out_d, seq_order=order)
+
+    def step() -> None:
+        prefill()
+        decode()
+
+    ms_pre = _time_ms(prefill, steps, warmup)
+    ms_dec = _time_ms(decode, steps, warmup)
+    ms_step = _time_ms(step, steps, warmup)
+    hq, dh = 32, 128
+    flops = 0
+    for ctx, ql in zip(pre.contexts, pre.query_lens):
+        prior = ctx - ql
+        visible = ql * prior + ql * (ql + 1) // 2  # sum over queries of (prior + i + 1)
+        flops += 4 * hq * dh * visible
+    dec_bytes = sum(dec.contexts) * 8 * dh * 2 * 2 + 2 * dec.query.numel() * 2
+    return {
+        "workload": "mixed_llama3_8b: 16 x 512-token prefill chunks (prior U[0,2048]) + 240 "
+                    "decodes (ctx U[256,4096]), Hq 32 / Hkv 8, Dh 128, block 16, bf16",
+        "ms_per_step": round(ms_step, 5),
+        "prefill_ms": round(ms_pre, 5),
+        "prefill_tflops": round(flops / (ms_pre * 1e-3) / 1e12, 2),
+        "prefill_mfma_frac_of_2500_tflops": round(flops / (ms_pre * 1e-3) / 2.5e15, 4),
+        "decode_ms": round(ms_dec, 5),
+        "decode_gbps": round(dec_bytes / (ms_dec * 1e-3) / 1e9, 1),
+    }
+
+
+def measure_norm_rope(device, steps: int, warmup: int) -> dict:
+    """RMSNorm (hidden 4096, fp32 weight -> fp32 out, the Triton wrapper's contract) and
+    RoPE (32 + 8 heads x 128, theta 5e5, in place) on a packed ragged bf16 stream."""
+
+    import torch
+
+    from tokserve_amd import workloads
+    from tokserve_amd.kernels import ops
+
+    data = workloads.norm_rope_packed(device, seed=0)
+    n = data.hidden.shape[0]
+    out = torch.empty(data.hidden.shape, dtype=torch.float32, device=device)
+    table = ops.RotaryTable(128, theta=data.theta, max_position=4096 + 257,
+                            dtype=torch.bfloat16, device=device)
+    q4 = data.query.permute(1, 0, 2).unsqueeze(0)
+    k4 = data.key.permute(1, 0, 2).unsqueeze(0)
+
+    def norm() -> None:
+        ops.rms_norm(data.hidden, data.weight, data.epsilon, out=out)
+
+    def rope() -> None:
+        ops.rope(q4, k4, data.positions, table, query_out=q4, key_out=k4)
+
+    ms_norm = _time_ms(norm, steps, warmup)
+    ms_rope = _time_ms(rope, steps, warmup)
+    norm_bytes = n * 4096 * (2 + 4) + 4096 * 4
+    rope_bytes = n * (40 * 128 * 2 * 2 + 8)
+    return {
+        "workload": f"norm_rope_packed: 64 seqs, {n} tokens (lengths U[1,256]), hidden 4096, "
+                    "Q 32 x 128 / K 8 x 128, bf16",
+        "rmsnorm_ms": round(ms_norm, 5),
+        "rmsnorm_gbps": round(norm_bytes / (ms_norm * 1e-3) / 1e9, 1),
+        "rope_ms": round(ms_rope, 5),
+        "rope_gbps": round(rope_bytes / (ms_rope * 1e-3) / 1e9, 1),
+    }
 
 
 def copy_calibration(device, gib: int = 1, repeats: int = 5) -> None:

@@ -187,6 +187,22 @@ def test_prefill_ragged_chunks_with_history(device, dtype) -> None:
     assert_close(out.cpu(), _prefill_oracle(batch), **TOL[dtype])
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize(("hq", "hkv", "dh"), [(32, 8, 128), (32, 4, 64), (16, 16, 128),
+                                               (8, 8, 64)])
+@pytest.mark.parametrize(("history", "length"), [(0, 1), (0, 31), (0, 32), (0, 33), (5, 64),
+                                                 (16, 100), (300, 513)])
+def test_prefill_mfma_tiles(device, dtype, hq, hkv, dh, history, length) -> None:
+    """MFMA prefill across query-tile (32 tokens at G=4) and key-step (32 keys) boundaries."""
+
+    batch = workloads.paged_batch([history + length], [length], num_q_heads=hq, num_kv_heads=hkv,
+                                  head_dim=dh, block_size=16, dtype=dtype, device=device,
+                                  seed=history * 1000 + length)
+    out = _prefill(batch)
+    torch.cuda.synchronize()
+    assert_close(out.cpu(), _prefill_oracle(batch), **TOL[dtype])
+
+
 def test_mixed_step_subset_matches_oracle(device) -> None:
     """Two 512-token chunks and 16 decodes of the mixed chunked-prefill step shape."""
 

@@ -55,6 +55,7 @@ template <typename T>
 struct Mfma;
 template <>
 struct Mfma<bf16_t> {
+  typedef __bf16 elem;
   typedef __bf16 v8 __attribute__((ext_vector_type(8)));
   typedef float f4 __attribute__((ext_vector_type(4)));
   static __device__ __forceinline__ f4 run(v8 a, v8 b, f4 c) {
@@ -63,6 +64,7 @@ struct Mfma<bf16_t> {
 };
 template <>
 struct Mfma<_Float16> {
+  typedef _Float16 elem;
   typedef _Float16 v8 __attribute__((ext_vector_type(8)));
   typedef float f4 __attribute__((ext_vector_type(4)));
   static __device__ __forceinline__ f4 run(v8 a, v8 b, f4 c) {
@@ -95,6 +97,34 @@ struct DecodeArgs {
   int64_t o_ss, o_hs;
   float *ws_m, *ws_l, *ws_acc;
 };
+
+struct PrefillArgs {
+  const void *q;
+  int64_t q_ts, q_hs;  // token and head strides of the packed query
+  const void *kc, *vc;
+  PoolView pool;
+  const int32_t *bt;
+  int32_t bt_stride;
+  const int32_t *seq_lens;
+  const int32_t *cu_q;
+  float scale_log2;
+  int32_t key_cap;
+  void *out;
+  int64_t o_ts, o_hs;
+};
+
+// Block ids of one sequence the MFMA prefill kernel holds in LDS: it serves
+// sequences of up to kPrefillBtWindow * 16 keys (block size 16).
+constexpr int kPrefillBtWindow = 4096;
+
+// Shapes the MFMA prefill kernel is instantiated for (block size 16, key_cap
+// keys per sequence at most).
+bool prefill_mfma_supported(int32_t dtype, int32_t head_dim, int32_t group, int32_t key_cap);
+
+// Launches the MFMA prefill kernel over grid (query tiles, Hkv, B); returns a tks_status.
+int32_t launch_prefill_mfma(const PrefillArgs &a, int32_t dtype, int32_t num_seqs,
+                            int32_t num_kv_heads, int32_t group, int32_t head_dim,
+                            int32_t max_query_len, hipStream_t stream);
 
 // Shapes the MFMA decode kernel is instantiated for (block size 16).
 bool decode_mfma_supported(int32_t dtype, int32_t head_dim, int32_t group);

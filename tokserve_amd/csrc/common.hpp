@@ -44,13 +44,13 @@ __device__ __forceinline__ float to_float(bf16_t x) {
   return __uint_as_float(static_cast<uint32_t>(x.bits) << 16);
 }
 
-// Round-to-nearest-even float -> bfloat16, NaN -> 0x7fc0 with the sign kept
-// (the conversion c10::BFloat16 performs).
+// Round-to-nearest-even float -> bfloat16 (the rounding c10::BFloat16 uses), done
+// by the hardware converter (v_cvt_pk_bf16_f32 on gfx950).
 __device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x0040u);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return static_cast<uint16_t>(u >> 16);
+  const __bf16 h = static_cast<__bf16>(f);
+  uint16_t b;
+  __builtin_memcpy(&b, &h, 2);
+  return b;
 }
 
 template <typename T>

@@ -416,6 +416,14 @@ extern "C" int32_t tks_paged_attention_prefill(
   // One split covering the whole key range: no partials, no workspace.
   const int32_t pps = static_cast<int32_t>(ceil_div(max_seq_len > 0 ? max_seq_len : 1, block_size));
   const int32_t key_cap = std::min(block_table_stride, pps) * block_size;
+  if (block_size == 16 && prefill_mfma_supported(dtype, head_dim, G, key_cap) && aligned16(query) &&
+      aligned16(key_cache) && aligned16(value_cache) && q_token_stride % 8 == 0 &&
+      q_head_stride % 8 == 0) {
+    PrefillArgs p{query,    q_token_stride, q_head_stride, key_cache,    value_cache,
+                  pool,     block_tables,   block_table_stride, seq_lens, cu_seqlens_q,
+                  scale_log2, key_cap,      out,           out_token_stride, out_head_stride};
+    return launch_prefill_mfma(p, dtype, num_seqs, num_kv_heads, G, head_dim, max_query_len, s);
+  }
   GenericArgs a{query,     q_token_stride, q_head_stride, key_cache,  value_cache, pool,
                 block_tables, block_table_stride, seq_lens, nullptr, cu_seqlens_q, num_seqs, num_q_heads,
                 G,         scale_log2,     pps,           1,          key_cap,     out,         out_token_stride,

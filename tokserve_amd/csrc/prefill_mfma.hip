@@ -1,0 +1,467 @@
+// Chunked-prefill paged attention with MFMA for both products, bf16/fp16, block size 16.
+//
+// One workgroup (4 waves) per (sequence, KV head, tile of QT query tokens). The
+// tile's rows are (token, query head) pairs, row = token * G + head, 128 rows
+// per workgroup, RT 16-row tiles per wave. Keys are processed 32 at a time
+// (two pages). Per step every wave computes, per 16-row tile,
+//
+//   S^T (32 keys x 16 rows) = K . Q^T          2 x (Dh/32) v_mfma_f32_16x16x32
+//     A = K rows from LDS, B = Q^T held in registers for the whole kernel;
+//     lane (g, r) receives keys g*4 + i (+16 for the second page) of row r,
+//   online softmax per row (running max / sum kept per lane for its row),
+//   O^T (Dh x 16 rows) += V^T . P^T            (Dh/16) v_mfma_f32_16x16x32
+//     B = P^T straight from the S^T accumulators, A = V^T.
+//
+// K and V pages move HBM -> LDS with global_load_lds_dwordx4 (16 bytes per lane
+// written straight into LDS, no registers) into a three-stage ring, two steps
+// ahead of the compute. Rows keep their natural [key][dim] layout with the 16-byte
+// chunks of row k XOR-swizzled by k % (Dh/8), which spreads the 16 rows an MFMA
+// operand read touches over all LDS banks. V^T operands come from the same
+// layout through ds_read_b64_tr_b16: within each 16-lane group, result element e
+// of lane j is element j % 4 of the 8 bytes that lane 4e + j / 4 addressed, so a
+// lane addressing dims 4c .. 4c+3 of key m hands dim j of keys 0..3 to lane j.
+//
+// All LDS reads of a step are issued in one inline-asm block that ends with its
+// own wait (compiled for the device only; the host pass sees no body): the
+// compiler, which cannot tell the LDS ring stages apart, would
+// otherwise wait for every outstanding HBM -> LDS load before each LDS read.
+// The step barrier is likewise explicit and waits only for the loads of the
+// step about to be read.
+//
+// The causal mask is key <= query position, query i of sequence b sitting at
+// seq_lens[b] - q_len_b + i (tokserve/kernels/_triton_paged_attention.py:118-123).
+#include "attention_common.hpp"
+
+namespace tks {
+namespace {
+
+constexpr int kPWaves = 4;
+constexpr int kKeysPerStep = 32;
+constexpr int kStages = 3;  // LDS ring: step s computes while s+1 and s+2 load
+
+typedef __attribute__((address_space(3))) void lds_void;
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+template <typename P>
+__device__ __forceinline__ uint32_t lds_address(P *p) {
+  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_void *)(p)));
+}
+
+// One 16-byte HBM -> LDS load per lane: lane i's bytes land at lds + 16 * i
+// (lds is wave-uniform).
+__device__ __forceinline__ void load_lds16(const void *src, void *lds) {
+#if __HIP_DEVICE_COMPILE__
+  __builtin_amdgcn_global_load_lds(src, (lds_void *)lds, 16, 0, 0);
+#endif
+}
+
+// Waits until at most N of this wave's vector-memory operations are
+// outstanding, then joins the workgroup barrier.
+template <int N>
+__device__ __forceinline__ void wait_loads_and_barrier() {
+  static_assert(N >= 0 && N < 64, "vmcnt");
+  asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(N) : "memory");
+}
+
+// Max and sum over lanes l, l^16, l^32, l^48 (the four k-groups of an MFMA
+// operand row), with the gfx950 cross-row lane swaps.
+//
+// The gfx950-only builtins and asm sit behind __HIP_DEVICE_COMPILE__: the
+// host pass instantiates the kernel templates too, and a target builtin it
+// does not know silently drops the kernel's launch stub.
+__device__ __forceinline__ float xgroup_max(float x) {
+#if __HIP_DEVICE_COMPILE__
+  auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+#endif
+  return x;
+}
+__device__ __forceinline__ float xgroup_sum(float x) {
+#if __HIP_DEVICE_COMPILE__
+  auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = __uint_as_float(b[0]) + __uint_as_float(b[1]);
+#endif
+  return x;
+}
+
+#define TKS_S(x) #x
+#define TKS_RD128(o, a, off) "ds_read_b128 %" TKS_S(o) ", %" TKS_S(a) " offset:" TKS_S(off) "\n\t"
+#define TKS_RDTR(o, a, off) "ds_read_b64_tr_b16 %" TKS_S(o) ", %" TKS_S(a) " offset:" TKS_S(off) "\n\t"
+#define TKS_RD32(o, a, off) "ds_read_b32 %" TKS_S(o) ", %" TKS_S(a) " offset:" TKS_S(off) "\n\t"
+
+// The LDS reads of one step: K operands k[kt * NC + c] (rows kt*16 + r),
+// V^T halves v[d * 2 + page] and the block ids of the step two ahead, all
+// complete when the block ends.
+template <int DH>
+struct StepReads;
+
+template <>
+struct StepReads<128> {
+  static constexpr int kRows16 = 16 * 128 * 2;  // bytes of 16 rows
+  static __device__ __forceinline__ void run(const uint32_t (&ka)[4], const uint32_t (&va)[8],
+                                             uint32_t ba, u32x4 (&k)[8], u32x2 (&v)[16],
+                                             uint32_t (&bid)[2]) {
+#if __HIP_DEVICE_COMPILE__
+    asm volatile(
+        TKS_RD128(0, 26, 0) TKS_RD128(1, 27, 0) TKS_RD128(2, 28, 0) TKS_RD128(3, 29, 0)
+        TKS_RD128(4, 26, 4096) TKS_RD128(5, 27, 4096) TKS_RD128(6, 28, 4096) TKS_RD128(7, 29, 4096)
+        TKS_RDTR(8, 30, 0) TKS_RDTR(9, 30, 4096) TKS_RDTR(10, 31, 0) TKS_RDTR(11, 31, 4096)
+        TKS_RDTR(12, 32, 0) TKS_RDTR(13, 32, 4096) TKS_RDTR(14, 33, 0) TKS_RDTR(15, 33, 4096)
+        TKS_RDTR(16, 34, 0) TKS_RDTR(17, 34, 4096) TKS_RDTR(18, 35, 0) TKS_RDTR(19, 35, 4096)
+        TKS_RDTR(20, 36, 0) TKS_RDTR(21, 36, 4096) TKS_RDTR(22, 37, 0) TKS_RDTR(23, 37, 4096)
+        TKS_RD32(24, 38, 0) TKS_RD32(25, 38, 4)
+        "s_waitcnt lgkmcnt(0)"
+        : "=&v"(k[0]), "=&v"(k[1]), "=&v"(k[2]), "=&v"(k[3]), "=&v"(k[4]), "=&v"(k[5]),
+          "=&v"(k[6]), "=&v"(k[7]), "=&v"(v[0]), "=&v"(v[1]), "=&v"(v[2]), "=&v"(v[3]),
+          "=&v"(v[4]), "=&v"(v[5]), "=&v"(v[6]), "=&v"(v[7]), "=&v"(v[8]), "=&v"(v[9]),
+          "=&v"(v[10]), "=&v"(v[11]), "=&v"(v[12]), "=&v"(v[13]), "=&v"(v[14]), "=&v"(v[15]),
+          "=&v"(bid[0]), "=&v"(bid[1])
+        : "v"(ka[0]), "v"(ka[1]), "v"(ka[2]), "v"(ka[3]), "v"(va[0]), "v"(va[1]), "v"(va[2]),
+          "v"(va[3]), "v"(va[4]), "v"(va[5]), "v"(va[6]), "v"(va[7]), "v"(ba)
+        : "memory");
+#endif
+  }
+};
+
+template <>
+struct StepReads<64> {
+  static constexpr int kRows16 = 16 * 64 * 2;
+  static __device__ __forceinline__ void run(const uint32_t (&ka)[2], const uint32_t (&va)[4],
+                                             uint32_t ba, u32x4 (&k)[4], u32x2 (&v)[8],
+                                             uint32_t (&bid)[1]) {
+#if __HIP_DEVICE_COMPILE__
+    asm volatile(
+        TKS_RD128(0, 13, 0) TKS_RD128(1, 14, 0) TKS_RD128(2, 13, 2048) TKS_RD128(3, 14, 2048)
+        TKS_RDTR(4, 15, 0) TKS_RDTR(5, 15, 2048) TKS_RDTR(6, 16, 0) TKS_RDTR(7, 16, 2048)
+        TKS_RDTR(8, 17, 0) TKS_RDTR(9, 17, 2048) TKS_RDTR(10, 18, 0) TKS_RDTR(11, 18, 2048)
+        TKS_RD32(12, 19, 0)
+        "s_waitcnt lgkmcnt(0)"
+        : "=&v"(k[0]), "=&v"(k[1]), "=&v"(k[2]), "=&v"(k[3]), "=&v"(v[0]), "=&v"(v[1]),
+          "=&v"(v[2]), "=&v"(v[3]), "=&v"(v[4]), "=&v"(v[5]), "=&v"(v[6]), "=&v"(v[7]),
+          "=&v"(bid[0])
+        : "v"(ka[0]), "v"(ka[1]), "v"(va[0]), "v"(va[1]), "v"(va[2]), "v"(va[3]), "v"(ba)
+        : "memory");
+#endif
+  }
+};
+
+#undef TKS_RD128
+#undef TKS_RDTR
+#undef TKS_RD32
+#undef TKS_S
+
+template <typename T, int DH, int G, int RT>
+__global__ __launch_bounds__(64 * kPWaves) __attribute__((amdgpu_waves_per_eu(2, 2))) void prefill_mfma_kernel(
+    PrefillArgs a) {
+  constexpr int ROWS = kPWaves * RT * 16;
+  constexpr int QT = ROWS / G;           // query tokens per workgroup
+  constexpr int NC = DH / 32;            // QK k-chunks
+  constexpr int DT = DH / 16;            // PV output dim tiles
+  constexpr int KS = kKeysPerStep;
+  constexpr int CPR = DH / 8;            // 16-byte chunks per key row
+  constexpr int TILE = KS * DH;          // elements of one K (or V) step tile
+  constexpr int STAGE = 2 * TILE;        // K tile then V tile
+  constexpr int LOADS = TILE / 8 / (64 * kPWaves);  // 16-byte loads per thread per tile
+  static_assert(LOADS >= 1 && (TILE / 8) % (64 * kPWaves) == 0, "tile");
+  static_assert(StepReads<DH>::kRows16 == 16 * DH * 2, "row offsets");
+  static_assert(16 % G == 0 || G % 16 == 0, "rows of a tile must be whole tokens");
+  using M = Mfma<T>;
+  typedef typename M::f4 f4;
+  typedef typename M::v8 v8;
+
+  __shared__ __attribute__((aligned(16))) T ring[kStages * STAGE];
+  __shared__ int32_t bt_s[kPrefillBtWindow];
+
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6;
+  const int lane = tid & 63;
+  const int r = lane & 15;
+  const int g = lane >> 4;
+
+  const int tile = blockIdx.x;
+  const int kvh = blockIdx.y;
+  const int b = blockIdx.z;
+  const int q0 = a.cu_q[b];
+  const int q_len = a.cu_q[b + 1] - q0;
+  const int t0 = tile * QT;
+  if (t0 >= q_len) return;
+  const int kv_len = min(a.seq_lens[b], a.key_cap);
+  const int base_pos = kv_len - q_len;  // absolute position of query token 0
+  const int t_end = min(q_len, t0 + QT);
+  // Keys needed by the last token of the tile (causal); the host keeps key_cap
+  // within the LDS block-id window.
+  const int n_keys = max(0, min(min(kv_len, base_pos + t_end), kPrefillBtWindow * 16));
+  const int n_steps = (n_keys + KS - 1) / KS;
+  const int n_pages = (n_keys + 15) / 16;
+
+  const T *q = static_cast<const T *>(a.q);
+  T *out = static_cast<T *>(a.out);
+  const T *kc = static_cast<const T *>(a.kc) + a.pool.layer_base + (int64_t)kvh * a.pool.head_stride;
+  const T *vc = static_cast<const T *>(a.vc) + a.pool.layer_base + (int64_t)kvh * a.pool.head_stride;
+  const int32_t *bt_row = a.bt + (int64_t)b * a.bt_stride;
+
+  // Block ids of the sequence (pages of the last step past the keys map to
+  // block 0: loaded, never used).
+  for (int i = tid; i < n_steps * (KS / 16); i += 64 * kPWaves)
+    bt_s[i] = i < n_pages ? (int32_t)clamp_block(bt_row[i], a.pool.num_blocks) : 0;
+
+  // Q^T operands: row tile j of this wave covers rows (wave*RT + j)*16 .. +16.
+  v8 qb[RT][NC];
+  int qpos[RT];  // absolute position of this lane's row (r) in tile j; -1 = padding
+#pragma unroll
+  for (int j = 0; j < RT; ++j) {
+    const int row = (wave * RT + j) * 16 + r;
+    const int t = t0 + row / G;
+    const int h = row % G;
+    qpos[j] = t < t_end ? base_pos + t : -1;
+    const T *qp = q + (int64_t)(q0 + min(t, q_len - 1)) * a.q_ts + (int64_t)(kvh * G + h) * a.q_hs + g * 8;
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      uint4 v = t < t_end ? ld16(qp + c * 32) : make_uint4(0, 0, 0, 0);
+      qb[j][c] = as_v8<T>(v);
+    }
+  }
+  // Smallest query position among this wave's rows: key steps entirely at or
+  // below it (and inside n_keys) need no mask.
+  int min_pos = qpos[0];
+#pragma unroll
+  for (int j = 1; j < RT; ++j) min_pos = min(min_pos, qpos[j]);
+  min_pos = __reduce_min_sync(~0ull, min_pos);
+  __syncthreads();  // bt_s ready
+
+  // Load k of wave w fills 16-byte slots (k*kPWaves + w)*64 + lane of a tile;
+  // slot = row * CPR + physical chunk. All rows of one load lie in one page.
+  auto page_of_load = [&](int step, int k) { return step * (KS / 16) + ((k * kPWaves + wave) * 64 / CPR) / 16; };
+  int64_t src_off[LOADS];  // element offset of this lane's chunk inside its page
+#pragma unroll
+  for (int k = 0; k < LOADS; ++k) {
+    const int slot = (k * kPWaves + wave) * 64 + lane;
+    const int row = slot / CPR;
+    src_off[k] = (int64_t)(row % 16) * DH + ((slot % CPR) ^ (row % CPR)) * 8;
+  }
+  const uint32_t ring_base = lds_address(&ring[0]);
+  auto issue = [&](int stage, const int32_t (&blk)[LOADS]) {
+#pragma unroll
+    for (int k = 0; k < LOADS; ++k) {
+      const int slot0 = (k * kPWaves + wave) * 64;
+      const int64_t off = (int64_t)blk[k] * a.pool.block_stride + src_off[k];
+      load_lds16(kc + off, &ring[stage * STAGE + slot0 * 8]);
+      load_lds16(vc + off, &ring[stage * STAGE + TILE + slot0 * 8]);
+    }
+  };
+
+  // Per-lane LDS byte addresses inside a stage.
+  uint32_t ka_addr[NC], va_addr[DT];
+#pragma unroll
+  for (int c = 0; c < NC; ++c) ka_addr[c] = (r * CPR + ((c * 4 + g) ^ (r % CPR))) * 16;
+#pragma unroll
+  for (int d = 0; d < DT; ++d) {
+    const int row = g * 4 + r / 4;  // + 16 for the second page (immediate offset)
+    const int lc = d * 2 + (r % 4) / 2;
+    va_addr[d] = TILE * (int)sizeof(T) + (row * CPR + (lc ^ (row % CPR))) * 16 + (r & 1) * 8;
+  }
+
+  f4 o[RT][DT];
+#pragma unroll
+  for (int j = 0; j < RT; ++j)
+#pragma unroll
+    for (int d = 0; d < DT; ++d) o[j][d] = f4{0.f, 0.f, 0.f, 0.f};
+  float m[RT], l[RT];
+#pragma unroll
+  for (int j = 0; j < RT; ++j) {
+    m[j] = -INFINITY;
+    l[j] = 0.f;
+  }
+
+  // Q is in registers before the first HBM -> LDS load, so no wait inside the
+  // loop has to count it.
+  __builtin_amdgcn_s_waitcnt(0);
+  {
+    int32_t blk[LOADS];
+#pragma unroll
+    for (int k = 0; k < LOADS; ++k) blk[k] = bt_s[min(page_of_load(0, k), kPrefillBtWindow - 1)];
+    int32_t blk1[LOADS];
+#pragma unroll
+    for (int k = 0; k < LOADS; ++k) blk1[k] = bt_s[min(page_of_load(1, k), kPrefillBtWindow - 1)];
+    if (n_steps > 0) issue(0, blk);
+    if (n_steps > 1) issue(1, blk1);
+  }
+
+  for (int s = 0; s < n_steps; ++s) {
+    const int stage = s % kStages;
+    if (s + 1 < n_steps)
+      wait_loads_and_barrier<2 * LOADS>();
+    else
+      wait_loads_and_barrier<0>();
+
+    const uint32_t sb = ring_base + stage * STAGE * (int)sizeof(T);
+    uint32_t ka_s[NC], va_s[DT];
+#pragma unroll
+    for (int c = 0; c < NC; ++c) ka_s[c] = sb + ka_addr[c];
+#pragma unroll
+    for (int d = 0; d < DT; ++d) va_s[d] = sb + va_addr[d];
+    const int ahead = min(s + 2, n_steps - 1);
+    const uint32_t ba = lds_address(&bt_s[0]) + page_of_load(ahead, 0) * 4;
+    u32x4 kraw[2 * NC];
+    u32x2 vraw[2 * DT];
+    uint32_t bid[LOADS];
+    StepReads<DH>::run(ka_s, va_s, ba, kraw, vraw, bid);
+    if (s + 2 < n_steps) {
+      int32_t blk[LOADS];
+#pragma unroll
+      for (int k = 0; k < LOADS; ++k) blk[k] = (int32_t)bid[k];
+      // Pages of one wave's loads are page_of_load(step, k); with LOADS == 2 the
+      // second is the first + 1, which the immediate offset 4 of the block-id
+      // read encodes, and with LOADS == 1 the page also depends on the wave.
+      issue((s + 2) % kStages, blk);
+    }
+
+    v8 ka[2][NC];
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        uint4 u = make_uint4(kraw[kt * NC + c][0], kraw[kt * NC + c][1], kraw[kt * NC + c][2],
+                             kraw[kt * NC + c][3]);
+        ka[kt][c] = as_v8<T>(u);
+      }
+    v8 va[DT];
+#pragma unroll
+    for (int d = 0; d < DT; ++d) {
+      uint4 u = make_uint4(vraw[2 * d][0], vraw[2 * d][1], vraw[2 * d + 1][0], vraw[2 * d + 1][1]);
+      va[d] = as_v8<T>(u);
+    }
+    const bool tail = s * KS + KS > n_keys;
+    if (tail) {
+      // V rows past the last key hold whatever the pool has there; their
+      // probabilities are 0, and 0 * NaN would not be.
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int key = s * KS + (e / 4) * 16 + g * 4 + (e % 4);
+        if (key >= n_keys) {
+#pragma unroll
+          for (int d = 0; d < DT; ++d) va[d][e] = static_cast<typename M::elem>(0.f);
+        }
+      }
+    }
+    const bool need_mask = s * KS + KS - 1 > min_pos || tail;
+
+#pragma unroll
+    for (int j = 0; j < RT; ++j) {
+      f4 st[2];
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt) {
+        st[kt] = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int c = 0; c < NC; ++c) st[kt] = M::run(ka[kt][c], qb[j][c], st[kt]);
+      }
+      float sv[8];
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) sv[kt * 4 + i] = st[kt][i];
+      if (need_mask) {
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int kp = s * KS + kt * 16 + g * 4 + i;
+            if (!(kp <= qpos[j] && kp < n_keys)) sv[kt * 4 + i] = -INFINITY;
+          }
+      }
+      // Row max of the raw scores (row r lives in lanes r, r+16, r+32, r+48);
+      // the scale is positive, so max(s * c) = max(s) * c.
+      float mx = fmaxf(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3])),
+                       fmaxf(fmaxf(sv[4], sv[5]), fmaxf(sv[6], sv[7])));
+      mx = xgroup_max(mx) * a.scale_log2;
+      const float mn = fmaxf(m[j], mx);
+      const float ref = mn == -INFINITY ? 0.f : mn;  // fully masked so far: p = 0
+      const float alpha = fast_exp2(m[j] - ref);
+      m[j] = mn;
+      float ps = 0.f;
+      v8 pb;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const float p = fast_exp2(__builtin_fmaf(sv[i], a.scale_log2, -ref));
+        ps += p;
+        pb[i] = static_cast<typename M::elem>(p);
+      }
+      l[j] = l[j] * alpha + ps;
+      // The running max rarely moves once a row has seen its first keys.
+      if (__builtin_amdgcn_ballot_w64(alpha != 1.f)) {
+#pragma unroll
+        for (int d = 0; d < DT; ++d) o[j][d] *= alpha;
+      }
+#pragma unroll
+      for (int d = 0; d < DT; ++d) o[j][d] = M::run(va[d], pb, o[j][d]);
+    }
+  }
+
+  // Row sums over the four lane groups, then O = O^T / l for the valid rows.
+#pragma unroll
+  for (int j = 0; j < RT; ++j) {
+    const float lj = xgroup_sum(l[j]);
+    const int row = (wave * RT + j) * 16 + r;
+    const int t = t0 + row / G;
+    const int h = row % G;
+    if (t >= t_end) continue;
+    const float inv = lj > 0.f ? 1.f / lj : 0.f;
+    T *op = out + (int64_t)(q0 + t) * a.o_ts + (int64_t)(kvh * G + h) * a.o_hs + g * 4;
+#pragma unroll
+    for (int d = 0; d < DT; ++d) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) op[d * 16 + i] = from_float<T>(o[j][d][i] * inv);
+    }
+  }
+}
+
+template <typename T>
+int32_t launch_typed(const PrefillArgs &a, int32_t num_seqs, int32_t num_kv_heads, int32_t G,
+                     int32_t head_dim, int32_t max_query_len, hipStream_t s) {
+  constexpr int RT = 2;
+  constexpr int ROWS = kPWaves * RT * 16;
+#define TKS_PREFILL(DH, GG)                                                                  \
+  if (head_dim == DH && G == GG) {                                                           \
+    const dim3 grid(static_cast<unsigned>(ceil_div(max_query_len, ROWS / GG)), num_kv_heads, \
+                    num_seqs);                                                               \
+    prefill_mfma_kernel<T, DH, GG, RT><<<grid, 64 * kPWaves, 0, s>>>(a);                     \
+    return check_launch();                                                                   \
+  }
+  TKS_PREFILL(128, 4)
+  TKS_PREFILL(128, 8)
+  TKS_PREFILL(128, 1)
+  TKS_PREFILL(128, 2)
+  TKS_PREFILL(128, 16)
+  TKS_PREFILL(64, 8)
+  TKS_PREFILL(64, 4)
+  TKS_PREFILL(64, 2)
+  TKS_PREFILL(64, 16)
+  TKS_PREFILL(64, 1)
+#undef TKS_PREFILL
+  return TKS_ERR_VALUE;
+}
+
+}  // namespace
+
+bool prefill_mfma_supported(int32_t dtype, int32_t head_dim, int32_t group, int32_t key_cap) {
+  if (dtype != TKS_BFLOAT16 && dtype != TKS_FLOAT16) return false;
+  if (key_cap > kPrefillBtWindow * 16) return false;
+  if (head_dim != 64 && head_dim != 128) return false;
+  return group == 1 || group == 2 || group == 4 || group == 8 || group == 16;
+}
+
+int32_t launch_prefill_mfma(const PrefillArgs &a, int32_t dtype, int32_t num_seqs,
+                            int32_t num_kv_heads, int32_t group, int32_t head_dim,
+                            int32_t max_query_len, hipStream_t stream) {
+  return dtype == TKS_BFLOAT16
+             ? launch_typed<bf16_t>(a, num_seqs, num_kv_heads, group, head_dim, max_query_len, stream)
+             : launch_typed<_Float16>(a, num_seqs, num_kv_heads, group, head_dim, max_query_len,
+                                      stream);
+}
+
+}  // namespace tks
