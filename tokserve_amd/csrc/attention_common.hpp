@@ -31,6 +31,11 @@ __device__ __forceinline__ int64_t block_of(const int32_t *__restrict__ bt_row, 
   return clamp_block(bt_row[page], num_blocks);
 }
 
+// NaN-propagating maximum (IEEE maximum, v_maximum3_f32 on gfx950). Unlike
+// fmaxf it needs no quieting of its inputs, so a tree of them is one
+// instruction per two or three values.
+__device__ __forceinline__ float nan_max(float a, float b) { return __builtin_elementwise_maximum(a, b); }
+
 // 2^x on the hardware exp unit (flushes results below 2^-126 to zero, exact at -inf).
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 

@@ -73,9 +73,9 @@ __device__ __forceinline__ void wait_loads_and_barrier() {
 __device__ __forceinline__ float xgroup_max(float x) {
 #if __HIP_DEVICE_COMPILE__
   auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  x = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  x = nan_max(__uint_as_float(a[0]), __uint_as_float(a[1]));
   auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  x = fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+  x = nan_max(__uint_as_float(b[0]), __uint_as_float(b[1]));
 #endif
   return x;
 }
@@ -90,30 +90,33 @@ __device__ __forceinline__ float xgroup_sum(float x) {
 }
 
 #define TKS_S(x) #x
-#define TKS_RD128(o, a, off) "ds_read_b128 %" TKS_S(o) ", %" TKS_S(a) " offset:" TKS_S(off) "\n\t"
-#define TKS_RDTR(o, a, off) "ds_read_b64_tr_b16 %" TKS_S(o) ", %" TKS_S(a) " offset:" TKS_S(off) "\n\t"
+#define TKS_RD128(o, a, off) "ds_read_b128 %" TKS_S(o) ", %" TKS_S(a) " offset:%" TKS_S(off) "\n\t"
+#define TKS_RDTR(o, a, off) "ds_read_b64_tr_b16 %" TKS_S(o) ", %" TKS_S(a) " offset:%" TKS_S(off) "\n\t"
 #define TKS_RD32(o, a, off) "ds_read_b32 %" TKS_S(o) ", %" TKS_S(a) " offset:" TKS_S(off) "\n\t"
 
 // The LDS reads of one step: K operands k[kt * NC + c] (rows kt*16 + r),
 // V^T halves v[d * 2 + page] and the block ids of the step two ahead, all
-// complete when the block ends.
+// complete when the block ends. O0 is the byte offset of the ring stage, O1 =
+// O0 + 16 rows (the second page).
 template <int DH>
 struct StepReads;
 
 template <>
 struct StepReads<128> {
   static constexpr int kRows16 = 16 * 128 * 2;  // bytes of 16 rows
+  template <int O0, int O1>
   static __device__ __forceinline__ void run(const uint32_t (&ka)[4], const uint32_t (&va)[8],
                                              uint32_t ba, u32x4 (&k)[8], u32x2 (&v)[16],
                                              uint32_t (&bid)[2]) {
+    static_assert(O1 == O0 + kRows16 && O1 < 65536, "offsets");
 #if __HIP_DEVICE_COMPILE__
     asm volatile(
-        TKS_RD128(0, 26, 0) TKS_RD128(1, 27, 0) TKS_RD128(2, 28, 0) TKS_RD128(3, 29, 0)
-        TKS_RD128(4, 26, 4096) TKS_RD128(5, 27, 4096) TKS_RD128(6, 28, 4096) TKS_RD128(7, 29, 4096)
-        TKS_RDTR(8, 30, 0) TKS_RDTR(9, 30, 4096) TKS_RDTR(10, 31, 0) TKS_RDTR(11, 31, 4096)
-        TKS_RDTR(12, 32, 0) TKS_RDTR(13, 32, 4096) TKS_RDTR(14, 33, 0) TKS_RDTR(15, 33, 4096)
-        TKS_RDTR(16, 34, 0) TKS_RDTR(17, 34, 4096) TKS_RDTR(18, 35, 0) TKS_RDTR(19, 35, 4096)
-        TKS_RDTR(20, 36, 0) TKS_RDTR(21, 36, 4096) TKS_RDTR(22, 37, 0) TKS_RDTR(23, 37, 4096)
+        TKS_RD128(0, 26, 39) TKS_RD128(1, 27, 39) TKS_RD128(2, 28, 39) TKS_RD128(3, 29, 39)
+        TKS_RD128(4, 26, 40) TKS_RD128(5, 27, 40) TKS_RD128(6, 28, 40) TKS_RD128(7, 29, 40)
+        TKS_RDTR(8, 30, 39) TKS_RDTR(9, 30, 40) TKS_RDTR(10, 31, 39) TKS_RDTR(11, 31, 40)
+        TKS_RDTR(12, 32, 39) TKS_RDTR(13, 32, 40) TKS_RDTR(14, 33, 39) TKS_RDTR(15, 33, 40)
+        TKS_RDTR(16, 34, 39) TKS_RDTR(17, 34, 40) TKS_RDTR(18, 35, 39) TKS_RDTR(19, 35, 40)
+        TKS_RDTR(20, 36, 39) TKS_RDTR(21, 36, 40) TKS_RDTR(22, 37, 39) TKS_RDTR(23, 37, 40)
         TKS_RD32(24, 38, 0) TKS_RD32(25, 38, 4)
         "s_waitcnt lgkmcnt(0)"
         : "=&v"(k[0]), "=&v"(k[1]), "=&v"(k[2]), "=&v"(k[3]), "=&v"(k[4]), "=&v"(k[5]),
@@ -122,7 +125,7 @@ struct StepReads<128> {
           "=&v"(v[10]), "=&v"(v[11]), "=&v"(v[12]), "=&v"(v[13]), "=&v"(v[14]), "=&v"(v[15]),
           "=&v"(bid[0]), "=&v"(bid[1])
         : "v"(ka[0]), "v"(ka[1]), "v"(ka[2]), "v"(ka[3]), "v"(va[0]), "v"(va[1]), "v"(va[2]),
-          "v"(va[3]), "v"(va[4]), "v"(va[5]), "v"(va[6]), "v"(va[7]), "v"(ba)
+          "v"(va[3]), "v"(va[4]), "v"(va[5]), "v"(va[6]), "v"(va[7]), "v"(ba), "i"(O0), "i"(O1)
         : "memory");
 #endif
   }
@@ -131,20 +134,23 @@ struct StepReads<128> {
 template <>
 struct StepReads<64> {
   static constexpr int kRows16 = 16 * 64 * 2;
+  template <int O0, int O1>
   static __device__ __forceinline__ void run(const uint32_t (&ka)[2], const uint32_t (&va)[4],
                                              uint32_t ba, u32x4 (&k)[4], u32x2 (&v)[8],
                                              uint32_t (&bid)[1]) {
+    static_assert(O1 == O0 + kRows16 && O1 < 65536, "offsets");
 #if __HIP_DEVICE_COMPILE__
     asm volatile(
-        TKS_RD128(0, 13, 0) TKS_RD128(1, 14, 0) TKS_RD128(2, 13, 2048) TKS_RD128(3, 14, 2048)
-        TKS_RDTR(4, 15, 0) TKS_RDTR(5, 15, 2048) TKS_RDTR(6, 16, 0) TKS_RDTR(7, 16, 2048)
-        TKS_RDTR(8, 17, 0) TKS_RDTR(9, 17, 2048) TKS_RDTR(10, 18, 0) TKS_RDTR(11, 18, 2048)
+        TKS_RD128(0, 13, 20) TKS_RD128(1, 14, 20) TKS_RD128(2, 13, 21) TKS_RD128(3, 14, 21)
+        TKS_RDTR(4, 15, 20) TKS_RDTR(5, 15, 21) TKS_RDTR(6, 16, 20) TKS_RDTR(7, 16, 21)
+        TKS_RDTR(8, 17, 20) TKS_RDTR(9, 17, 21) TKS_RDTR(10, 18, 20) TKS_RDTR(11, 18, 21)
         TKS_RD32(12, 19, 0)
         "s_waitcnt lgkmcnt(0)"
         : "=&v"(k[0]), "=&v"(k[1]), "=&v"(k[2]), "=&v"(k[3]), "=&v"(v[0]), "=&v"(v[1]),
           "=&v"(v[2]), "=&v"(v[3]), "=&v"(v[4]), "=&v"(v[5]), "=&v"(v[6]), "=&v"(v[7]),
           "=&v"(bid[0])
-        : "v"(ka[0]), "v"(ka[1]), "v"(va[0]), "v"(va[1]), "v"(va[2]), "v"(va[3]), "v"(ba)
+        : "v"(ka[0]), "v"(ka[1]), "v"(va[0]), "v"(va[1]), "v"(va[2]), "v"(va[3]), "v"(ba),
+          "i"(O0), "i"(O1)
         : "memory");
 #endif
   }
@@ -154,6 +160,11 @@ struct StepReads<64> {
 #undef TKS_RDTR
 #undef TKS_RD32
 #undef TKS_S
+
+template <int N>
+struct Const {
+  static constexpr int value = N;
+};
 
 template <typename T, int DH, int G, int RT>
 __global__ __launch_bounds__(64 * kPWaves) __attribute__((amdgpu_waves_per_eu(2, 2))) void prefill_mfma_kernel(
@@ -168,8 +179,10 @@ __global__ __launch_bounds__(64 * kPWaves) __attribute__((amdgpu_waves_per_eu(2,
   constexpr int STAGE = 2 * TILE;        // K tile then V tile
   constexpr int LOADS = TILE / 8 / (64 * kPWaves);  // 16-byte loads per thread per tile
   static_assert(LOADS >= 1 && (TILE / 8) % (64 * kPWaves) == 0, "tile");
-  static_assert(StepReads<DH>::kRows16 == 16 * DH * 2, "row offsets");
+  static_assert(StepReads<DH>::kRows16 == 16 * DH * (int)sizeof(T), "row offsets");
   static_assert(16 % G == 0 || G % 16 == 0, "rows of a tile must be whole tokens");
+  // A load's 64 lanes cover 64 / CPR rows from a multiple of that: one page.
+  static_assert(16 % (64 / CPR) == 0, "load rows within a page");
   using M = Mfma<T>;
   typedef typename M::f4 f4;
   typedef typename M::v8 v8;
@@ -178,7 +191,7 @@ __global__ __launch_bounds__(64 * kPWaves) __attribute__((amdgpu_waves_per_eu(2,
   __shared__ int32_t bt_s[kPrefillBtWindow];
 
   const int tid = threadIdx.x;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lane = tid & 63;
   const int r = lane & 15;
   const int g = lane >> 4;
@@ -201,8 +214,11 @@ __global__ __launch_bounds__(64 * kPWaves) __attribute__((amdgpu_waves_per_eu(2,
 
   const T *q = static_cast<const T *>(a.q);
   T *out = static_cast<T *>(a.out);
-  const T *kc = static_cast<const T *>(a.kc) + a.pool.layer_base + (int64_t)kvh * a.pool.head_stride;
-  const T *vc = static_cast<const T *>(a.vc) + a.pool.layer_base + (int64_t)kvh * a.pool.head_stride;
+  const char *kc = reinterpret_cast<const char *>(static_cast<const T *>(a.kc) + a.pool.layer_base +
+                                                  (int64_t)kvh * a.pool.head_stride);
+  const char *vc = reinterpret_cast<const char *>(static_cast<const T *>(a.vc) + a.pool.layer_base +
+                                                  (int64_t)kvh * a.pool.head_stride);
+  const int64_t block_bytes = a.pool.block_stride * (int64_t)sizeof(T);
   const int32_t *bt_row = a.bt + (int64_t)b * a.bt_stride;
 
   // Block ids of the sequence (pages of the last step past the keys map to
@@ -236,35 +252,40 @@ __global__ __launch_bounds__(64 * kPWaves) __attribute__((amdgpu_waves_per_eu(2,
 
   // Load k of wave w fills 16-byte slots (k*kPWaves + w)*64 + lane of a tile;
   // slot = row * CPR + physical chunk. All rows of one load lie in one page.
-  auto page_of_load = [&](int step, int k) { return step * (KS / 16) + ((k * kPWaves + wave) * 64 / CPR) / 16; };
-  int64_t src_off[LOADS];  // element offset of this lane's chunk inside its page
+  auto page_of_load = [&](int step, int k) {
+    return step * (KS / 16) + ((k * kPWaves + wave) * 64 / CPR) / 16;
+  };
+  uint32_t src_off[LOADS];  // byte offset of this lane's chunk inside its block
 #pragma unroll
   for (int k = 0; k < LOADS; ++k) {
     const int slot = (k * kPWaves + wave) * 64 + lane;
     const int row = slot / CPR;
-    src_off[k] = (int64_t)(row % 16) * DH + ((slot % CPR) ^ (row % CPR)) * 8;
+    src_off[k] = ((row % 16) * DH + ((slot % CPR) ^ (row % CPR)) * 8) * (int)sizeof(T);
   }
-  const uint32_t ring_base = lds_address(&ring[0]);
-  auto issue = [&](int stage, const int32_t (&blk)[LOADS]) {
+  // Issues the loads of one step into ring stage STG; blk[k] is wave-uniform.
+  auto issue = [&](auto stage_c, const int32_t (&blk)[LOADS]) {
+    constexpr int STG = decltype(stage_c)::value;
 #pragma unroll
     for (int k = 0; k < LOADS; ++k) {
       const int slot0 = (k * kPWaves + wave) * 64;
-      const int64_t off = (int64_t)blk[k] * a.pool.block_stride + src_off[k];
-      load_lds16(kc + off, &ring[stage * STAGE + slot0 * 8]);
-      load_lds16(vc + off, &ring[stage * STAGE + TILE + slot0 * 8]);
+      const int64_t base = (int64_t)__builtin_amdgcn_readfirstlane(blk[k]) * block_bytes;
+      load_lds16(kc + base + src_off[k], &ring[STG * STAGE + slot0 * 8]);
+      load_lds16(vc + base + src_off[k], &ring[STG * STAGE + TILE + slot0 * 8]);
     }
   };
 
-  // Per-lane LDS byte addresses inside a stage.
+  // Per-lane LDS byte addresses inside stage 0 (stages are immediate offsets).
+  const uint32_t ring_base = lds_address(&ring[0]);
   uint32_t ka_addr[NC], va_addr[DT];
 #pragma unroll
-  for (int c = 0; c < NC; ++c) ka_addr[c] = (r * CPR + ((c * 4 + g) ^ (r % CPR))) * 16;
+  for (int c = 0; c < NC; ++c) ka_addr[c] = ring_base + (r * CPR + ((c * 4 + g) ^ (r % CPR))) * 16;
 #pragma unroll
   for (int d = 0; d < DT; ++d) {
     const int row = g * 4 + r / 4;  // + 16 for the second page (immediate offset)
     const int lc = d * 2 + (r % 4) / 2;
-    va_addr[d] = TILE * (int)sizeof(T) + (row * CPR + (lc ^ (row % CPR))) * 16 + (r & 1) * 8;
+    va_addr[d] = ring_base + TILE * (int)sizeof(T) + (row * CPR + (lc ^ (row % CPR))) * 16 + (r & 1) * 8;
   }
+  const uint32_t bt_base = lds_address(&bt_s[0]);
 
   f4 o[RT][DT];
 #pragma unroll
@@ -282,43 +303,39 @@ __global__ __launch_bounds__(64 * kPWaves) __attribute__((amdgpu_waves_per_eu(2,
   // loop has to count it.
   __builtin_amdgcn_s_waitcnt(0);
   {
-    int32_t blk[LOADS];
+    int32_t blk[LOADS], blk1[LOADS];
 #pragma unroll
-    for (int k = 0; k < LOADS; ++k) blk[k] = bt_s[min(page_of_load(0, k), kPrefillBtWindow - 1)];
-    int32_t blk1[LOADS];
-#pragma unroll
-    for (int k = 0; k < LOADS; ++k) blk1[k] = bt_s[min(page_of_load(1, k), kPrefillBtWindow - 1)];
-    if (n_steps > 0) issue(0, blk);
-    if (n_steps > 1) issue(1, blk1);
+    for (int k = 0; k < LOADS; ++k) {
+      blk[k] = bt_s[min(page_of_load(0, k), kPrefillBtWindow - 1)];
+      blk1[k] = bt_s[min(page_of_load(1, k), kPrefillBtWindow - 1)];
+    }
+    if (n_steps > 0) issue(Const<0>{}, blk);
+    if (n_steps > 1) issue(Const<1>{}, blk1);
   }
 
-  for (int s = 0; s < n_steps; ++s) {
-    const int stage = s % kStages;
+  // One step: keys s*KS .. s*KS + KS - 1 from ring stage STG.
+  auto step = [&](auto stage_c, int s) {
+    constexpr int STG = decltype(stage_c)::value;
+    constexpr int O0 = STG * STAGE * (int)sizeof(T);
     if (s + 1 < n_steps)
       wait_loads_and_barrier<2 * LOADS>();
     else
       wait_loads_and_barrier<0>();
 
-    const uint32_t sb = ring_base + stage * STAGE * (int)sizeof(T);
-    uint32_t ka_s[NC], va_s[DT];
-#pragma unroll
-    for (int c = 0; c < NC; ++c) ka_s[c] = sb + ka_addr[c];
-#pragma unroll
-    for (int d = 0; d < DT; ++d) va_s[d] = sb + va_addr[d];
     const int ahead = min(s + 2, n_steps - 1);
-    const uint32_t ba = lds_address(&bt_s[0]) + page_of_load(ahead, 0) * 4;
+    const uint32_t ba = bt_base + page_of_load(ahead, 0) * 4;
     u32x4 kraw[2 * NC];
     u32x2 vraw[2 * DT];
     uint32_t bid[LOADS];
-    StepReads<DH>::run(ka_s, va_s, ba, kraw, vraw, bid);
+    StepReads<DH>::template run<O0, O0 + 16 * DH * (int)sizeof(T)>(ka_addr, va_addr, ba, kraw, vraw,
+                                                                     bid);
     if (s + 2 < n_steps) {
+      // With LOADS == 2 the second load's page is the first + 1 (the block-id
+      // read at offset 4); with LOADS == 1 the page depends on the wave.
       int32_t blk[LOADS];
 #pragma unroll
       for (int k = 0; k < LOADS; ++k) blk[k] = (int32_t)bid[k];
-      // Pages of one wave's loads are page_of_load(step, k); with LOADS == 2 the
-      // second is the first + 1, which the immediate offset 4 of the block-id
-      // read encodes, and with LOADS == 1 the page also depends on the wave.
-      issue((s + 2) % kStages, blk);
+      issue(Const<(STG + 2) % kStages>{}, blk);
     }
 
     v8 ka[2][NC];
@@ -376,13 +393,23 @@ __global__ __launch_bounds__(64 * kPWaves) __attribute__((amdgpu_waves_per_eu(2,
       }
       // Row max of the raw scores (row r lives in lanes r, r+16, r+32, r+48);
       // the scale is positive, so max(s * c) = max(s) * c.
-      float mx = fmaxf(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3])),
-                       fmaxf(fmaxf(sv[4], sv[5]), fmaxf(sv[6], sv[7])));
+      float mx = nan_max(nan_max(nan_max(sv[0], sv[1]), nan_max(sv[2], sv[3])),
+                         nan_max(nan_max(sv[4], sv[5]), nan_max(sv[6], sv[7])));
       mx = xgroup_max(mx) * a.scale_log2;
-      const float mn = fmaxf(m[j], mx);
-      const float ref = mn == -INFINITY ? 0.f : mn;  // fully masked so far: p = 0
-      const float alpha = fast_exp2(m[j] - ref);
-      m[j] = mn;
+      // The reference max only moves when the new scores exceed it by more
+      // than 8 (probabilities stay <= 2^8 meanwhile); the rescale of O and l
+      // that a move costs is then rare after the first keys of a row.
+      const float m_old = m[j];
+      const bool bump = mx > m_old + 8.f;
+      const float m_new = bump ? mx : m_old;
+      m[j] = m_new;
+      if (__builtin_amdgcn_ballot_w64(bump && m_old != -INFINITY)) {
+        const float alpha = fast_exp2(m_old - m_new);
+        l[j] *= alpha;
+#pragma unroll
+        for (int d = 0; d < DT; ++d) o[j][d] *= alpha;
+      }
+      const float ref = m_new == -INFINITY ? 0.f : m_new;  // fully masked so far: p = 0
       float ps = 0.f;
       v8 pb;
 #pragma unroll
@@ -391,15 +418,16 @@ __global__ __launch_bounds__(64 * kPWaves) __attribute__((amdgpu_waves_per_eu(2,
         ps += p;
         pb[i] = static_cast<typename M::elem>(p);
       }
-      l[j] = l[j] * alpha + ps;
-      // The running max rarely moves once a row has seen its first keys.
-      if (__builtin_amdgcn_ballot_w64(alpha != 1.f)) {
-#pragma unroll
-        for (int d = 0; d < DT; ++d) o[j][d] *= alpha;
-      }
+      l[j] += ps;
 #pragma unroll
       for (int d = 0; d < DT; ++d) o[j][d] = M::run(va[d], pb, o[j][d]);
     }
+  };
+
+  for (int s = 0; s < n_steps; s += kStages) {
+    step(Const<0>{}, s);
+    if (s + 1 < n_steps) step(Const<1>{}, s + 1);
+    if (s + 2 < n_steps) step(Const<2>{}, s + 2);
   }
 
   // Row sums over the four lane groups, then O = O^T / l for the valid rows.
