@@ -2,7 +2,7 @@
  * tokserve_hip.h -- C ABI of libtokserve_hip.so, the MI355X (gfx950) kernels of
  * tokserve's continuous-batching hot path: KV append into paged blocks, block
  * table gathers, paged attention (decode and chunked prefill), RMSNorm, RoPE
- * and greedy token selection.
+ * greedy token selection and the elementwise vector_add.
  *
  * Conventions shared by every entry point
  *   - All pointers are device pointers (HBM), except where a comment says host.
@@ -218,6 +218,14 @@ int32_t tks_rope(const void *query, void *query_out, int64_t q_sb, int64_t q_sh,
  */
 int32_t tks_argmax(const void *logits, int64_t row_stride, int64_t num_rows, int64_t vocab_size,
                    int64_t *out_ids, int32_t dtype, tks_stream_t stream);
+
+/* ------------------------------------------------------------------------
+ * Elementwise out[i] = x[i] + y[i] over num_elements contiguous elements.
+ * Replaces vector_add (tokserve/kernels/vector.py:6-41). dtype FLOAT32 or
+ * FLOAT16 (TKS_ERR_TYPE otherwise); num_elements == 0 launches nothing.
+ */
+int32_t tks_vector_add(const void *x, const void *y, void *out, int64_t num_elements, int32_t dtype,
+                       tks_stream_t stream);
 
 #ifdef __cplusplus
 } /* extern "C" */

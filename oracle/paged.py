@@ -6,6 +6,18 @@ runs repeat_kv + causal_attention over cache_len + T keys with offset
 cache_len (tokserve/engine/attention.py:298-356). The batched functions below
 are the per-request loop of tokserve/batching/execution.py:33-131 applied to a
 packed batch.
+
+Two arithmetics of the same attention exist in the reference, and both are
+available here:
+  compute_dtype=None     the torch backend: every op in the input dtype, so bf16
+                         rounds after the matmul, the scale, the softmax and the
+                         second matmul (tokserve/engine/attention.py:58-127);
+  compute_dtype=float32  the reference's GPU kernel: Q, K and V loaded as fp32,
+                         scores, online softmax and the accumulator in fp32, one
+                         rounding to the output dtype on the store
+                         (tokserve/kernels/_triton_paged_attention.py:60-66,101-149).
+The reference's own GPU tests bound the gap between the two at 4e-2 for bf16
+(tests/gpu/test_tiled_attention_prefill.py:50-59).
 """
 
 from __future__ import annotations
@@ -47,11 +59,16 @@ def paged_attention(
     layer: int,
     key_length: int,
     query_position_offset: int,
+    compute_dtype: torch.dtype | None = None,
 ) -> torch.Tensor:
     """query (1, Hq, Tq, Dh) -> (1, Hq, Tq, Dh) through the block table."""
 
     keys, values = read_layer(key_cache, value_cache, block_ids, layer, key_length)
-    return gqa_attention(query, keys, values, query_position_offset=query_position_offset)
+    if compute_dtype is None:
+        return gqa_attention(query, keys, values, query_position_offset=query_position_offset)
+    out = gqa_attention(query.to(compute_dtype), keys.to(compute_dtype), values.to(compute_dtype),
+                        query_position_offset=query_position_offset)
+    return out.to(query.dtype)
 
 
 def decode_batch(
@@ -61,6 +78,7 @@ def decode_batch(
     block_tables: torch.Tensor,
     seq_lens: torch.Tensor,
     layer: int,
+    compute_dtype: torch.dtype | None = None,
 ) -> torch.Tensor:
     """One query per sequence: (B, Hq, Dh) -> (B, Hq, Dh); sequence b sees seq_lens[b] keys."""
 
@@ -73,7 +91,7 @@ def decode_batch(
         q = query[b][None, :, None, :]
         o = paged_attention(
             q, key_cache, value_cache, block_tables[b], layer=layer, key_length=length,
-            query_position_offset=length - 1,
+            query_position_offset=length - 1, compute_dtype=compute_dtype,
         )
         out[b] = o[0, :, 0, :]
     return out
@@ -87,6 +105,7 @@ def prefill_batch(
     seq_lens: torch.Tensor,
     cu_seqlens_q: torch.Tensor,
     layer: int,
+    compute_dtype: torch.dtype | None = None,
 ) -> torch.Tensor:
     """Packed query chunks (N, Hq, Dh): sequence b's chunk sits at the end of its seq_lens[b] keys."""
 
@@ -99,7 +118,7 @@ def prefill_batch(
         q = query[q0:q1].permute(1, 0, 2).unsqueeze(0)  # (1, Hq, Tq, Dh)
         o = paged_attention(
             q, key_cache, value_cache, block_tables[b], layer=layer, key_length=length,
-            query_position_offset=length - (q1 - q0),
+            query_position_offset=length - (q1 - q0), compute_dtype=compute_dtype,
         )
         out[q0:q1] = o[0].permute(1, 0, 2)
     return out

@@ -1,9 +1,12 @@
 """Paged attention (decode split-K and ragged prefill) on the GPU against the CPU oracle.
 
 Tolerances (stated by the hot path's parity contract): fp32 within 1e-5
-relative (rtol 1e-5, atol 1e-6); bf16/fp16 within 2e-2 absolute. The oracle is
-the reference's torch backend (gather + repeat_kv + causal_attention in the
-input dtype, oracle/paged.py).
+relative (rtol 1e-5, atol 1e-6); bf16/fp16 within 2e-2 absolute of the
+reference's GPU-kernel arithmetic (fp32 scores, softmax and accumulator, one
+rounding on the store), and within the 4e-2 the reference's own tests allow
+between that kernel and its torch backend (per-op bf16 rounding). The oracle is
+the reference's torch backend (gather + repeat_kv + causal_attention,
+oracle/paged.py) run in either arithmetic.
 """
 
 import pytest
@@ -31,9 +34,22 @@ def _decode(batch, **kw):
         layer_index=0, max_seq_len=batch.max_seq_len, **kw)
 
 
-def _decode_oracle(batch):
+def _decode_oracle(batch, compute_dtype=None):
     q, kc, vc, bt, lens, _ = _cpu(batch)
-    return paged.decode_batch(q, kc, vc, bt, lens, 0)
+    return paged.decode_batch(q, kc, vc, bt, lens, 0, compute_dtype)
+
+
+def _assert_parity(actual, oracle, batch) -> None:
+    """fp32: the oracle within 1e-5 relative. bf16/fp16: the reference kernel's fp32
+    arithmetic within 2e-2 absolute, and the torch backend's per-op rounding within the
+    4e-2 the reference allows between the two (tests/gpu/test_tiled_attention_prefill.py:50-59)."""
+
+    actual = actual.cpu()
+    if actual.dtype == torch.float32:
+        assert_close(actual, oracle(batch, None), **TOL[torch.float32])
+        return
+    assert_close(actual, oracle(batch, torch.float32), rtol=0, atol=2e-2)
+    assert_close(actual, oracle(batch, None), rtol=0, atol=4e-2)
 
 
 def test_decode_fp32_small_config(device) -> None:
@@ -42,7 +58,7 @@ def test_decode_fp32_small_config(device) -> None:
     batch = workloads.decode_fp32_small(device, seed=0)
     out = _decode(batch)
     torch.cuda.synchronize()
-    assert_close(out.cpu(), _decode_oracle(batch), **TOL[torch.float32])
+    _assert_parity(out, _decode_oracle, batch)
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
@@ -55,7 +71,7 @@ def test_decode_shapes_and_dtypes(device, dtype, hq, hkv, dh) -> None:
                                   device=device, seed=hq * 7 + dh)
     out = _decode(batch)
     torch.cuda.synchronize()
-    assert_close(out.cpu(), _decode_oracle(batch), **TOL[dtype])
+    _assert_parity(out, _decode_oracle, batch)
 
 
 @pytest.mark.parametrize("block_size", [1, 2, 5, 32])
@@ -66,7 +82,7 @@ def test_decode_other_block_sizes(device, block_size) -> None:
                                   seed=block_size)
     out = _decode(batch)
     torch.cuda.synchronize()
-    assert_close(out.cpu(), _decode_oracle(batch), **TOL[torch.float32])
+    _assert_parity(out, _decode_oracle, batch)
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
@@ -78,7 +94,7 @@ def test_decode_split_k_matches_oracle(device, dtype, pages_per_split) -> None:
                                   seed=pages_per_split)
     out = _decode(batch, pages_per_split=pages_per_split)
     torch.cuda.synchronize()
-    assert_close(out.cpu(), _decode_oracle(batch), **TOL[dtype])
+    _assert_parity(out, _decode_oracle, batch)
 
 
 @pytest.mark.parametrize("pages_per_split", [0, 16])
@@ -97,7 +113,7 @@ def test_decode_sequence_order_does_not_change_results(device, pages_per_split) 
     torch.cuda.synchronize()
     assert torch.equal(planned, natural)
     assert torch.equal(reverse, natural)
-    assert_close(natural.cpu(), _decode_oracle(batch), **TOL[torch.bfloat16])
+    _assert_parity(natural, _decode_oracle, batch)
 
 
 def test_decode_empty_sequence_gives_zeros(device) -> None:
@@ -106,7 +122,7 @@ def test_decode_empty_sequence_gives_zeros(device) -> None:
     out = _decode(batch, pages_per_split=1)
     torch.cuda.synchronize()
     assert torch.all(out[0] == 0)
-    assert_close(out[1:].cpu(), _decode_oracle(batch)[1:], **TOL[torch.bfloat16])
+    _assert_parity(out[1:], lambda b, c: _decode_oracle(b, c)[1:], batch)
 
 
 def test_decode_llama3_8b_subset_matches_oracle(device) -> None:
@@ -115,7 +131,7 @@ def test_decode_llama3_8b_subset_matches_oracle(device) -> None:
     batch = workloads.decode_llama3_8b(device, seed=1, num_seqs=24)
     out = _decode(batch)
     torch.cuda.synchronize()
-    assert_close(out.cpu(), _decode_oracle(batch), **TOL[torch.bfloat16])
+    _assert_parity(out, _decode_oracle, batch)
 
 
 def test_decode_llama3_8b_full_size_properties(device) -> None:
@@ -159,9 +175,9 @@ def _prefill(batch):
         max_seq_len=batch.max_seq_len)
 
 
-def _prefill_oracle(batch):
+def _prefill_oracle(batch, compute_dtype=None):
     q, kc, vc, bt, lens, cu = _cpu(batch)
-    return paged.prefill_batch(q, kc, vc, bt, lens, cu, 0)
+    return paged.prefill_batch(q, kc, vc, bt, lens, cu, 0, compute_dtype)
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
@@ -173,7 +189,7 @@ def test_prefill_tile_boundaries(device, dtype, length) -> None:
                                   block_size=16, dtype=dtype, device=device, seed=500 + length)
     out = _prefill(batch)
     torch.cuda.synchronize()
-    assert_close(out.cpu(), _prefill_oracle(batch), **TOL[dtype])
+    _assert_parity(out, _prefill_oracle, batch)
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
@@ -184,7 +200,7 @@ def test_prefill_ragged_chunks_with_history(device, dtype) -> None:
                                   block_size=16, dtype=dtype, device=device, seed=77)
     out = _prefill(batch)
     torch.cuda.synchronize()
-    assert_close(out.cpu(), _prefill_oracle(batch), **TOL[dtype])
+    _assert_parity(out, _prefill_oracle, batch)
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
@@ -200,7 +216,20 @@ def test_prefill_mfma_tiles(device, dtype, hq, hkv, dh, history, length) -> None
                                   seed=history * 1000 + length)
     out = _prefill(batch)
     torch.cuda.synchronize()
-    assert_close(out.cpu(), _prefill_oracle(batch), **TOL[dtype])
+    _assert_parity(out, _prefill_oracle, batch)
+
+
+@pytest.mark.parametrize("block_size", [32, 64, 256])
+@pytest.mark.parametrize(("contexts", "qlens"), [([300, 45, 1000], [100, 45, 3]), ([17], [17])])
+def test_prefill_mfma_large_blocks(device, block_size, contexts, qlens) -> None:
+    """Blocks of several 16-key pages (the MFMA path pages inside a block)."""
+
+    batch = workloads.paged_batch(contexts, qlens, num_q_heads=32, num_kv_heads=8, head_dim=128,
+                                  block_size=block_size, dtype=torch.bfloat16, device=device,
+                                  seed=block_size + len(contexts))
+    out = _prefill(batch)
+    torch.cuda.synchronize()
+    _assert_parity(out, _prefill_oracle, batch)
 
 
 def test_mixed_step_subset_matches_oracle(device) -> None:
@@ -210,5 +239,5 @@ def test_mixed_step_subset_matches_oracle(device) -> None:
     out_p = _prefill(prefill)
     out_d = _decode(decode)
     torch.cuda.synchronize()
-    assert_close(out_p.cpu(), _prefill_oracle(prefill), **TOL[torch.bfloat16])
-    assert_close(out_d.cpu(), _decode_oracle(decode), **TOL[torch.bfloat16])
+    _assert_parity(out_p, _prefill_oracle, prefill)
+    _assert_parity(out_d, _decode_oracle, decode)

@@ -346,6 +346,29 @@ def test_batched_decode_and_prefill_oracles_match_fp64() -> None:
         np.testing.assert_allclose(dec[b].numpy(), exp[0, :, 0, :], rtol=1e-5, atol=1e-6)
 
 
+def test_kernel_arithmetic_oracle_is_fp64_rounded_once() -> None:
+    """compute_dtype=float32 (the reference GPU kernel's arithmetic) on bf16 inputs equals the
+    fp64 attention of the same bf16 values rounded once to bf16 (one bf16 ulp at most), while
+    the torch-backend arithmetic rounds after every op and lands measurably further away."""
+
+    g = torch.Generator().manual_seed(12)
+    hq, hkv, dh, bs, ctx, ql = 8, 2, 64, 16, 200, 40
+    kc = torch.randn(1, 16, hkv, bs, dh, generator=g).bfloat16()
+    vc = torch.randn(1, 16, hkv, bs, dh, generator=g).bfloat16()
+    table = torch.randperm(16, generator=g)[:13].to(torch.int32)[None]
+    q = torch.randn(ql, hq, dh, generator=g).bfloat16()
+    lens, cu = torch.tensor([ctx]), torch.tensor([0, ql], dtype=torch.int32)
+    fast = paged.prefill_batch(q, kc, vc, table, lens, cu, 0, torch.float32)
+    slow = paged.prefill_batch(q, kc, vc, table, lens, cu, 0)
+    k, v = paged.read_layer(kc, vc, table[0], 0, ctx)
+    exact = fp64.attention(q.permute(1, 0, 2)[None].double().numpy(), k.double().numpy(),
+                           v.double().numpy(), query_position_offset=ctx - ql)
+    exact = torch.from_numpy(exact[0]).permute(1, 0, 2)
+    ulp = torch.finfo(torch.bfloat16).eps * exact.abs().clamp_min(2.0 ** -8)
+    assert ((fast.double() - exact).abs() <= ulp).all()
+    assert (slow.double() - exact).abs().max() > (fast.double() - exact).abs().max()
+
+
 # --------------------------------------------------------------------------
 # Greedy
 

@@ -118,13 +118,14 @@ struct PrefillArgs {
   int64_t o_ts, o_hs;
 };
 
-// Block ids of one sequence the MFMA prefill kernel holds in LDS: it serves
-// sequences of up to kPrefillBtWindow * 16 keys (block size 16).
+// 16-key pages of one sequence the MFMA prefill kernel holds in LDS: it serves
+// sequences of up to kPrefillBtWindow * 16 keys.
 constexpr int kPrefillBtWindow = 4096;
 
-// Shapes the MFMA prefill kernel is instantiated for (block size 16, key_cap
-// keys per sequence at most).
-bool prefill_mfma_supported(int32_t dtype, int32_t head_dim, int32_t group, int32_t key_cap);
+// Shapes the MFMA prefill kernel is instantiated for: block sizes that are
+// multiples of 16, key_cap keys per sequence at most.
+bool prefill_mfma_supported(int32_t dtype, int32_t head_dim, int32_t group, int32_t key_cap,
+                            int32_t block_size, int64_t num_blocks, int32_t num_kv_heads);
 
 // Launches the MFMA prefill kernel over grid (query tiles, Hkv, B); returns a tks_status.
 int32_t launch_prefill_mfma(const PrefillArgs &a, int32_t dtype, int32_t num_seqs,

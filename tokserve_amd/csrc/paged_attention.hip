@@ -416,7 +416,8 @@ extern "C" int32_t tks_paged_attention_prefill(
   // One split covering the whole key range: no partials, no workspace.
   const int32_t pps = static_cast<int32_t>(ceil_div(max_seq_len > 0 ? max_seq_len : 1, block_size));
   const int32_t key_cap = std::min(block_table_stride, pps) * block_size;
-  if (block_size == 16 && prefill_mfma_supported(dtype, head_dim, G, key_cap) && aligned16(query) &&
+  if (prefill_mfma_supported(dtype, head_dim, G, key_cap, block_size, num_blocks, num_kv_heads) &&
+      aligned16(query) &&
       aligned16(key_cache) && aligned16(value_cache) && q_token_stride % 8 == 0 &&
       q_head_stride % 8 == 0) {
     PrefillArgs p{query,    q_token_stride, q_head_stride, key_cache,    value_cache,

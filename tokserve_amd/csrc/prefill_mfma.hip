@@ -1,4 +1,5 @@
-// Chunked-prefill paged attention with MFMA for both products, bf16/fp16, block size 16.
+// Chunked-prefill paged attention with MFMA for both products, bf16/fp16, block
+// sizes that are multiples of 16 (keys move in 16-key pages).
 //
 // One workgroup (4 waves) per (sequence, KV head, tile of QT query tokens). The
 // tile's rows are (token, query head) pairs, row = token * G + head, 128 rows
@@ -218,13 +219,19 @@ __global__ __launch_bounds__(64 * kPWaves) __attribute__((amdgpu_waves_per_eu(2,
                                                   (int64_t)kvh * a.pool.head_stride);
   const char *vc = reinterpret_cast<const char *>(static_cast<const T *>(a.vc) + a.pool.layer_base +
                                                   (int64_t)kvh * a.pool.head_stride);
-  const int64_t block_bytes = a.pool.block_stride * (int64_t)sizeof(T);
+  // K/V move in pages of 16 keys; a pool block of BS = 16 * ppb keys holds ppb
+  // of them per KV head. Page i of the sequence starts at page unit
+  // block * (Hkv * ppb) + i % ppb of the layer (unit = 16 rows of one head).
+  const int ppb = a.pool.block_size / 16;
+  const int units_per_block = (int)(a.pool.block_stride / (16 * DH));
+  constexpr int64_t kPageBytes = 16 * DH * (int64_t)sizeof(T);
   const int32_t *bt_row = a.bt + (int64_t)b * a.bt_stride;
 
-  // Block ids of the sequence (pages of the last step past the keys map to
-  // block 0: loaded, never used).
+  // Page units of the sequence (pages of the last step past the keys map to
+  // unit 0: loaded, never used).
   for (int i = tid; i < n_steps * (KS / 16); i += 64 * kPWaves)
-    bt_s[i] = i < n_pages ? (int32_t)clamp_block(bt_row[i], a.pool.num_blocks) : 0;
+    bt_s[i] = i < n_pages ? (int32_t)clamp_block(bt_row[i / ppb], a.pool.num_blocks) * units_per_block + i % ppb
+                          : 0;
 
   // Q^T operands: row tile j of this wave covers rows (wave*RT + j)*16 .. +16.
   v8 qb[RT][NC];
@@ -268,7 +275,7 @@ __global__ __launch_bounds__(64 * kPWaves) __attribute__((amdgpu_waves_per_eu(2,
 #pragma unroll
     for (int k = 0; k < LOADS; ++k) {
       const int slot0 = (k * kPWaves + wave) * 64;
-      const int64_t base = (int64_t)__builtin_amdgcn_readfirstlane(blk[k]) * block_bytes;
+      const int64_t base = (int64_t)__builtin_amdgcn_readfirstlane(blk[k]) * kPageBytes;
       load_lds16(kc + base + src_off[k], &ring[STG * STAGE + slot0 * 8]);
       load_lds16(vc + base + src_off[k], &ring[STG * STAGE + TILE + slot0 * 8]);
     }
@@ -476,9 +483,12 @@ int32_t launch_typed(const PrefillArgs &a, int32_t num_seqs, int32_t num_kv_head
 
 }  // namespace
 
-bool prefill_mfma_supported(int32_t dtype, int32_t head_dim, int32_t group, int32_t key_cap) {
+bool prefill_mfma_supported(int32_t dtype, int32_t head_dim, int32_t group, int32_t key_cap,
+                            int32_t block_size, int64_t num_blocks, int32_t num_kv_heads) {
   if (dtype != TKS_BFLOAT16 && dtype != TKS_FLOAT16) return false;
-  if (key_cap > kPrefillBtWindow * 16) return false;
+  if (key_cap > kPrefillBtWindow * 16 || block_size % 16 != 0) return false;
+  // Page units (16 rows of one head) of the layer are addressed with 32 bits.
+  if (num_blocks * num_kv_heads * (block_size / 16) >= (int64_t{1} << 31)) return false;
   if (head_dim != 64 && head_dim != 128) return false;
   return group == 1 || group == 2 || group == 4 || group == 8 || group == 16;
 }

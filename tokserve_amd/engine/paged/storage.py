@@ -1,0 +1,150 @@
+"""Paged K/V pools (tokserve/engine/paged/storage.py).
+
+Two pools, K and V, shaped [L, NB, Hkv, BS, Dh] (the reference layout,
+storage.py:40-56), allocated uninitialised like the reference's torch.empty.
+Writes go through the KV-append kernel (tks_kv_append), reads through the
+block-table gather kernel (tks_paged_gather); the kernels run on HIP devices
+only, and a storage on another device rejects them.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from tokserve_amd.kernels import ops
+
+__all__ = ["PagedKVStorage"]
+
+
+class PagedKVStorage:
+    """Per-layer K/V values in shared physical blocks."""
+
+    def __init__(
+        self,
+        *,
+        num_layers: int,
+        num_blocks: int,
+        num_key_value_heads: int,
+        block_size: int,
+        head_dim: int,
+        device: torch.device,
+        dtype: torch.dtype,
+    ) -> None:
+        for name, size in (
+            ("num_layers", num_layers),
+            ("num_blocks", num_blocks),
+            ("num_key_value_heads", num_key_value_heads),
+            ("block_size", block_size),
+            ("head_dim", head_dim),
+        ):
+            if size < 1:
+                raise ValueError(f"{name} must be positive")
+        self.num_layers = num_layers
+        self.num_blocks = num_blocks
+        self.num_key_value_heads = num_key_value_heads
+        self.block_size = block_size
+        self.head_dim = head_dim
+        self.device = torch.device(device)
+        self.dtype = dtype
+        shape = (num_layers, num_blocks, num_key_value_heads, block_size, head_dim)
+        self._key_storage = torch.empty(shape, device=self.device, dtype=dtype)
+        self._value_storage = torch.empty(shape, device=self.device, dtype=dtype)
+
+    @property
+    def storage_shape(self) -> tuple[int, ...]:
+        return tuple(self._key_storage.shape)
+
+    @property
+    def key_storage(self) -> torch.Tensor:
+        """The physical K pool, for kernels."""
+
+        return self._key_storage
+
+    @property
+    def value_storage(self) -> torch.Tensor:
+        """The physical V pool, for kernels."""
+
+        return self._value_storage
+
+    # ------------------------------------------------------------- single slot
+
+    def write_token(
+        self,
+        *,
+        layer_index: int,
+        block_id: int,
+        offset: int,
+        keys: torch.Tensor,
+        values: torch.Tensor,
+    ) -> None:
+        """Write one token's K/V, each shaped (Hkv, Dh)."""
+
+        self._check_location(layer_index, block_id, offset)
+        expected = (self.num_key_value_heads, self.head_dim)
+        if keys.shape != expected or values.shape != expected:
+            raise ValueError("keys and values must have shape (Hkv, Dh)")
+        if keys.device != self.device or values.device != self.device:
+            raise ValueError("keys and values must match the storage device")
+        if keys.dtype != self.dtype or values.dtype != self.dtype:
+            raise ValueError("keys and values must match the storage dtype")
+        slot = torch.tensor([block_id * self.block_size + offset], dtype=torch.int64)
+        self.write_slots(layer_index, slot.to(self.device), keys.unsqueeze(0), values.unsqueeze(0))
+
+    def read_token(
+        self,
+        *,
+        layer_index: int,
+        block_id: int,
+        offset: int,
+    ) -> tuple[torch.Tensor, torch.Tensor]:
+        """Copies of one physical slot's K/V, each shaped (Hkv, Dh)."""
+
+        self._check_location(layer_index, block_id, offset)
+        keys, values = self.gather(layer_index, (block_id,), offset + 1)
+        return keys[offset].clone(), values[offset].clone()
+
+    # ----------------------------------------------------------------- batched
+
+    def write_slots(
+        self,
+        layer_index: int,
+        slot_mapping: torch.Tensor,
+        keys: torch.Tensor,
+        values: torch.Tensor,
+    ) -> None:
+        """KV append: row i of keys/values (N, Hkv, Dh) goes to pool slot slot_mapping[i]."""
+
+        if layer_index < 0 or layer_index >= self.num_layers:
+            raise IndexError("layer_index is out of range")
+        ops.kv_append(keys, values, self._key_storage, self._value_storage, slot_mapping,
+                      layer_index)
+
+    def gather(
+        self, layer_index: int, block_ids: tuple[int, ...] | list[int], length: int
+    ) -> tuple[torch.Tensor, torch.Tensor]:
+        """K/V of logical positions 0 .. length-1 of a block table, each (length, Hkv, Dh)."""
+
+        if layer_index < 0 or layer_index >= self.num_layers:
+            raise IndexError("layer_index is out of range")
+        shape = (length, self.num_key_value_heads, self.head_dim)
+        keys = torch.empty(shape, device=self.device, dtype=self.dtype)
+        values = torch.empty(shape, device=self.device, dtype=self.dtype)
+        if length == 0:
+            return keys, values
+        needed = (length + self.block_size - 1) // self.block_size
+        if len(block_ids) < needed:
+            raise ValueError("block table does not cover the requested length")
+        meta = torch.tensor([*block_ids[:needed], length, 0], dtype=torch.int32).to(self.device)
+        ops.paged_gather(
+            self._key_storage, self._value_storage, meta[:needed].view(1, needed),
+            meta[needed : needed + 1], meta[needed + 1 :], layer_index, length, keys, values,
+        )
+        return keys, values
+
+    def _check_location(self, layer_index: int, block_id: int, offset: int) -> None:
+        if layer_index < 0 or layer_index >= self.num_layers:
+            raise IndexError("layer_index is out of range")
+        if block_id < 0 or block_id >= self.num_blocks:
+            raise IndexError("block_id is out of range")
+        if offset < 0 or offset >= self.block_size:
+            raise IndexError("offset is out of range")

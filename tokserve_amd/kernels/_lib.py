@@ -15,7 +15,7 @@ from pathlib import Path
 import torch
 
 LIBRARY_NAME = "libtokserve_hip.so"
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 TKS_OK = 0
 TKS_ERR_VALUE = -1
@@ -75,6 +75,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
          _i32, _i64, _i32, _c_void_p, _c_void_p, _c_void_p, _i64, _i32, _c_void_p],
     ),
     "tks_argmax": (_i32, [_c_void_p, _i64, _i64, _i64, _c_void_p, _i32, _c_void_p]),
+    "tks_vector_add": (_i32, [_c_void_p, _c_void_p, _c_void_p, _i64, _i32, _c_void_p]),
 }
 
 _lib: ctypes.CDLL | None = None

@@ -495,3 +495,25 @@ def greedy_argmax(logits: torch.Tensor, out: torch.Tensor | None = None) -> torc
     )
     _lib.check(status, "greedy_argmax")
     return out
+
+
+# ----------------------------------------------------------------------------
+# Elementwise
+
+
+def vector_add(x: torch.Tensor, y: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """out = x + y for contiguous 1-D fp32/fp16 HIP vectors of one shape."""
+
+    require_hip("vector_add", x, y)
+    if x.ndim != 1 or x.shape != y.shape or x.dtype != y.dtype:
+        raise ValueError("x and y must be matching one-dimensional vectors")
+    if not x.is_contiguous() or not y.is_contiguous():
+        raise ValueError("x and y must be contiguous")
+    if out is None:
+        out = torch.empty_like(x)
+    status = _lib.load().tks_vector_add(
+        x.data_ptr(), y.data_ptr(), out.data_ptr(), x.numel(), _lib.dtype_code(x.dtype),
+        _lib.stream_of(x),
+    )
+    _lib.check(status, "vector_add")
+    return out
