@@ -1,0 +1,161 @@
+"""End to end on the GPU: the Llama model, the batched executor and the
+continuous-batching engine against the reference fixture and the CPU oracle.
+
+fp32 greedy tokens must be identical to the oracle's (the parity contract for
+the fp32 end-to-end configuration); logits within the reference's own fp32
+model tolerance, rtol 1e-4 / atol 1e-5 (tokserve/benchmarking/optimized.py:34-35).
+"""
+
+from pathlib import Path
+
+import pytest
+import torch
+from torch.testing import assert_close
+
+from oracle import engine as oracle_engine
+from oracle import model as oracle_model
+from tokserve_amd.batching.engine import ContinuousBatchEngine
+from tokserve_amd.engine.config import LlamaConfig
+from tokserve_amd.engine.model import LlamaModel
+from tokserve_amd.engine.paged.inference import decode_paged, prefill_paged
+from tokserve_amd.engine.paged.manager import PagedKVCacheManager
+from tokserve_amd.generation.generate import generate, generate_with_paged_cache
+from tokserve_amd.generation.types import GenerationConfig
+from tokserve_amd.scheduler.request import ScheduledRequest
+from tokserve_amd.scheduler.scheduler import RequestScheduler
+
+pytestmark = pytest.mark.gpu
+
+FIXTURE = torch.load(Path(__file__).parent / "golden" / "tiny_llama_fp32.pt", weights_only=True)
+MODEL_TOL = dict(rtol=1e-4, atol=1e-5)
+
+
+def _fixture_model(device) -> LlamaModel:
+    model = LlamaModel(LlamaConfig(**FIXTURE["config"]))
+    model.load_state_dict(FIXTURE["state_dict"])
+    return model.to(device).eval()
+
+
+def _manager(model, device, *, num_blocks, block_size, dtype=torch.float32):
+    config = model.config
+    return PagedKVCacheManager(num_layers=config.num_hidden_layers, num_blocks=num_blocks,
+                               num_key_value_heads=config.num_key_value_heads,
+                               block_size=block_size, head_dim=config.head_dim, device=device,
+                               dtype=dtype)
+
+
+def test_model_reproduces_reference_fixture(device) -> None:
+    model = _fixture_model(device)
+    prompt = torch.tensor([FIXTURE["prompt"]], device=device)
+    logits = model(prompt)
+    torch.cuda.synchronize()
+    assert_close(logits.cpu(), FIXTURE["prompt_logits"], **MODEL_TOL)
+    manager = _manager(model, device, num_blocks=FIXTURE["num_blocks"],
+                       block_size=FIXTURE["block_size"])
+    result = prefill_paged(model, prompt, manager, sequence_id="s")
+    last = result.logits[:, -1, :]
+    steps, tokens = [last[0]], []
+    for _ in FIXTURE["decode_tokens"]:
+        token = torch.argmax(last, dim=-1, keepdim=True)
+        tokens.append(int(token))
+        last = decode_paged(model, token, result.cache)[:, -1, :]
+        steps.append(last[0])
+    assert tokens == FIXTURE["decode_tokens"]
+    assert list(result.cache.block_ids) == FIXTURE["block_ids"]
+    assert_close(torch.stack(steps).cpu(), FIXTURE["decode_logits"], **MODEL_TOL)
+
+
+def test_full_recompute_and_paged_generation_agree(device) -> None:
+    model = _fixture_model(device)
+    manager = _manager(model, device, num_blocks=8, block_size=4)
+    prompt = torch.tensor([[5, 17, 33, 2, 60]], device=device)
+    config = GenerationConfig(max_new_tokens=7)
+    full = generate(model, prompt, config)
+    paged = generate_with_paged_cache(model, prompt, config, manager, sequence_id="p")
+    assert full.token_ids.tolist() == paged.token_ids.tolist()
+    assert manager.allocator.allocated_count == 0
+
+
+def _run_both(model, device, specs, *, max_running, num_blocks, block_size):
+    manager = _manager(model, device, num_blocks=num_blocks, block_size=block_size,
+                       dtype=model.embed_tokens.weight.dtype)
+    scheduler = RequestScheduler(max_running_requests=max_running, cache_manager=manager)
+    engine = ContinuousBatchEngine(model, scheduler, manager)
+    released = {}
+    original = manager.release_sequence
+
+    def record(sequence_id):
+        released[sequence_id] = manager.get_sequence(sequence_id).block_ids
+        original(sequence_id)
+
+    manager.release_sequence = record
+    state = {k: v.detach().cpu() for k, v in model.state_dict().items()}
+    config = {k: getattr(model.config, k) for k in FIXTURE["config"]}
+    reference = oracle_engine.Engine(state, config, num_blocks=num_blocks, block_size=block_size,
+                                     max_running=max_running)
+    for rid, prompt, n in specs:
+        scheduler.submit(ScheduledRequest(rid, torch.tensor([prompt], device=device),
+                                          GenerationConfig(max_new_tokens=n)))
+        reference.submit(oracle_engine.Request(rid, list(prompt), n))
+    engine.run_until_idle()
+    expected = reference.run()
+    return engine, scheduler, manager, released, reference, expected
+
+
+def test_engine_ragged_known_answers_on_gpu(device) -> None:
+    model = _fixture_model(device)
+    specs = (("A", [1, 2, 3], 3), ("B", [4, 5, 6, 7], 2), ("C", [8, 9, 10, 11, 12, 13, 14], 1),
+             ("D", [15], 2))
+    engine, scheduler, manager, released, reference, expected = _run_both(
+        model, device, specs, max_running=3, num_blocks=8, block_size=4)
+    first, second, third = engine.history
+    assert first.prefill_ids == ("A", "B", "C") and first.completed_ids == ("C",)
+    assert second.decode_ids == ("A", "B") and second.completed_ids == ("B",)
+    assert third.completed_ids == ("A", "D") and third.active_ids == ()
+    assert released == {"C": (2, 3), "B": (1, 3), "A": (0, 1), "D": (2,)}
+    for rid, prompt, _ in specs:
+        assert scheduler.get_request(rid).result.generated_token_ids[0].tolist() == \
+            reference.finished[rid].generated
+    assert manager.allocator.allocated_count == 0
+
+
+@pytest.mark.parametrize("seed", [0, 1])
+def test_engine_random_workload_tokens_and_records_identical(device, seed) -> None:
+    g = torch.Generator().manual_seed(100 + seed)
+    specs = []
+    for i in range(16):
+        length = int(torch.randint(1, 20, (1,), generator=g))
+        prompt = torch.randint(0, 64, (length,), generator=g).tolist()
+        specs.append((f"q{i}", prompt, int(torch.randint(0, 9, (1,), generator=g))))
+    model = _fixture_model(device)
+    engine, _, _, released, reference, expected = _run_both(
+        model, device, specs, max_running=5, num_blocks=14, block_size=4)
+    assert [tuple(r.__dict__.values()) for r in engine.history] == \
+        [tuple(r.__dict__.values()) for r in expected]
+    for rid, prompt, n in specs:
+        result = engine.scheduler.get_request(rid).result
+        assert result.generated_token_ids[0].tolist() == reference.finished[rid].generated, rid
+        if n:
+            assert released[rid] == reference.finished[rid].released_blocks
+
+
+def test_tinyllama_width_fp32_greedy_tokens_identical(device) -> None:
+    """TinyLlama widths (hidden 2048, 32/4 heads of 64, MLP 5632, vocabulary 32000), two
+    layers, random init under a seed, block size 16: the MFMA prefill and decode kernels."""
+
+    config = LlamaConfig(vocab_size=32_000, hidden_size=2048, intermediate_size=5632,
+                         num_hidden_layers=2, num_attention_heads=32, num_key_value_heads=4,
+                         max_position_embeddings=1152, rms_norm_eps=1e-5, rope_theta=10_000.0)
+    torch.manual_seed(7)
+    model = LlamaModel(config).to(device).eval()
+    g = torch.Generator().manual_seed(8)
+    specs = []
+    for i in range(6):
+        length = int(torch.randint(40, 200, (1,), generator=g))
+        specs.append((f"t{i}", torch.randint(0, 32_000, (length,), generator=g).tolist(), 6))
+    engine, _, _, _, reference, expected = _run_both(model, device, specs, max_running=4,
+                                                     num_blocks=80, block_size=16)
+    for rid, _, _ in specs:
+        assert engine.scheduler.get_request(rid).result.generated_token_ids[0].tolist() == \
+            reference.finished[rid].generated, rid
+    assert [r.completed_ids for r in engine.history] == [r.completed_ids for r in expected]

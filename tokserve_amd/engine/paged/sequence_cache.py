@@ -121,6 +121,15 @@ class SequencePagedKVCache:
         )
         self._written.add(layer_index)
 
+    def mark_layers_written(self) -> None:
+        """Record that every layer's K/V of the pending positions was written by packed
+        KV-append launches (one per layer over a whole batch's slots)."""
+
+        self._require_active()
+        if self._pending == 0:
+            raise RuntimeError("begin_append must be called before write_layer")
+        self._written = set(range(self.storage.num_layers))
+
     def read_layer(
         self, layer_index: int, *, include_pending: bool = False
     ) -> tuple[torch.Tensor, torch.Tensor]:
