@@ -102,6 +102,8 @@ def main() -> int:
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--no-secondary", action="store_true",
                         help="skip the mixed-step and packed norm/RoPE measurements")
+    parser.add_argument("--no-e2e", action="store_true",
+                        help="skip the end-to-end TinyLlama serving run")
     parser.add_argument("--copy-calibration", action="store_true",
                         help="after the bench, run a 1 GiB device copy (counter calibration)")
     args = parser.parse_args()
@@ -186,6 +188,11 @@ def main() -> int:
             "mixed_step": measure_mixed(device, 20, 5),
             "norm_rope": measure_norm_rope(device, 20, 5),
         }
+    if not args.no_e2e:
+        e2e = measure_e2e(device, args.seed,
+                          None if args.no_cpu_baseline else args.cpu_seconds)
+        result["decode_tokens_per_s_e2e"] = e2e["tokens_per_s"]
+        result.setdefault("secondary", {})["e2e_tinyllama"] = e2e
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(batch, args.cpu_seconds)
     print(json.dumps(result), flush=True)
@@ -297,6 +304,122 @@ def measure_norm_rope(device, steps: int, warmup: int) -> dict:
         "rmsnorm_gbps": round(norm_bytes / (ms_norm * 1e-3) / 1e9, 1),
         "rope_ms": round(ms_rope, 5),
         "rope_gbps": round(rope_bytes / (ms_rope * 1e-3) / 1e9, 1),
+    }
+
+
+def _e2e_engine(model, specs, device, block_size: int = 16):
+    import torch
+
+    from tokserve_amd import workloads
+    from tokserve_amd.batching.engine import ContinuousBatchEngine
+    from tokserve_amd.engine.paged.manager import PagedKVCacheManager
+    from tokserve_amd.generation.types import GenerationConfig
+    from tokserve_amd.scheduler.request import ScheduledRequest
+    from tokserve_amd.scheduler.scheduler import RequestScheduler
+
+    config = model.config
+    manager = PagedKVCacheManager(
+        num_layers=config.num_hidden_layers, num_blocks=workloads.pool_blocks(specs, block_size),
+        num_key_value_heads=config.num_key_value_heads, block_size=block_size,
+        head_dim=config.head_dim, device=device, dtype=model.embed_tokens.weight.dtype)
+    scheduler = RequestScheduler(max_running_requests=128, cache_manager=manager)
+    for spec in specs:
+        prompt = torch.tensor([spec.prompt], dtype=torch.int64, device=device)
+        scheduler.submit(ScheduledRequest(spec.request_id, prompt,
+                                          GenerationConfig(max_new_tokens=spec.max_new_tokens)))
+    return ContinuousBatchEngine(model, scheduler, manager)
+
+
+def measure_e2e(device, seed: int, cpu_seconds: float | None) -> dict:
+    """TinyLlama-1.1B (random init, bf16) serving 128 requests, prompts U[64, 1024],
+    128 greedy tokens each, block size 16, max 128 running: the whole run through the
+    continuous-batching engine, timed on the host wall clock (each step ends with its
+    tokens on the host). tokens/s = generated tokens / wall time."""
+
+    import torch
+
+    from tokserve_amd import workloads
+    from tokserve_amd.engine.config import tinyllama_1_1b
+    from tokserve_amd.engine.model import LlamaModel
+
+    config = tinyllama_1_1b(max_position_embeddings=2048)
+    torch.manual_seed(seed)
+    with torch.device(device):
+        model = LlamaModel(config)
+    model = model.to(torch.bfloat16).eval()
+    specs = workloads.tinyllama_requests(seed=seed)
+    warm = workloads.tinyllama_requests(seed=seed + 1, num_requests=8, max_new_tokens=4)
+    _e2e_engine(model, warm, device).run_until_idle()
+    torch.cuda.synchronize()
+    engine = _e2e_engine(model, specs, device)
+    step_s = []
+    start = time.perf_counter()
+    while engine.scheduler.waiting_count or engine.scheduler.running_count:
+        t0 = time.perf_counter()
+        engine.step()
+        step_s.append(time.perf_counter() - t0)
+    wall = time.perf_counter() - start
+    generated = sum(r.num_generated_tokens for r in engine.results)
+    decode_steps = step_s[1:]
+    result = {
+        "workload": "e2e_tinyllama: TinyLlama-1.1B shape (22 layers, hidden 2048, 32/4 heads, "
+                    "Dh 64, MLP 5632, vocab 32000), random init, bf16; 128 requests, prompts "
+                    "U[64,1024], 128 greedy tokens, block 16, max_running 128",
+        "requests": len(specs),
+        "prompt_tokens": sum(len(s.prompt) for s in specs),
+        "generated_tokens": generated,
+        "iterations": len(step_s),
+        "wall_s": round(wall, 4),
+        "tokens_per_s": round(generated / wall, 1),
+        "prefill_step_s": round(step_s[0], 4),
+        "decode_step_ms_mean": round(1e3 * sum(decode_steps) / max(len(decode_steps), 1), 3),
+        "decode_tokens_per_s": round(
+            sum(len(r.decode_ids) for r in engine.history[1:]) / max(sum(decode_steps), 1e-9), 1),
+    }
+    if cpu_seconds is not None:
+        result["cpu_baseline"] = e2e_cpu_baseline(model, specs, cpu_seconds)
+    return result
+
+
+def e2e_cpu_baseline(model, specs, target_seconds: float) -> dict:
+    """The oracle's per-request engine (the reference's torch backend, bf16) on the host:
+    the first 4 requests of the same workload, engine steps until target_seconds (at
+    least the prefill step and one decode step); tokens/s over the steps run."""
+
+    import torch
+
+    from oracle import engine as oracle_engine
+
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    state = {k: v.detach().cpu() for k, v in model.state_dict().items()}
+    config = {k: getattr(model.config, k) for k in (
+        "vocab_size", "hidden_size", "intermediate_size", "num_hidden_layers",
+        "num_attention_heads", "num_key_value_heads", "max_position_embeddings",
+        "rms_norm_eps", "rope_theta")}
+    sample = specs[:4]
+    engine = oracle_engine.Engine(state, config, num_blocks=10_000, block_size=16, max_running=128)
+    for spec in sample:
+        engine.submit(oracle_engine.Request(spec.request_id, list(spec.prompt),
+                                            spec.max_new_tokens))
+    elapsed = 0.0
+    steps = 0
+    while (engine.waiting or engine.running) and (steps < 2 or elapsed < target_seconds):
+        start = time.perf_counter()
+        engine.step()
+        elapsed += time.perf_counter() - start
+        steps += 1
+    tokens = sum(len(r.generated) for r in
+                 list(engine.running.values()) + list(engine.finished.values()))
+    return {
+        "value": round(tokens / elapsed, 3),
+        "unit": "tokens/s",
+        "cores": cores,
+        "kind": "port",
+        "sample": f"{steps} engine steps (prefill + {steps - 1} decode) of the first "
+                  f"{len(sample)} requests ({sum(len(s.prompt) for s in sample)} prompt tokens), "
+                  f"per-request torch-backend forward in bf16 on {cores} host threads, "
+                  f"{tokens} tokens in {elapsed:.1f} s",
     }
 
 

@@ -159,3 +159,37 @@ def test_tinyllama_width_fp32_greedy_tokens_identical(device) -> None:
         assert engine.scheduler.get_request(rid).result.generated_token_ids[0].tolist() == \
             reference.finished[rid].generated, rid
     assert [r.completed_ids for r in engine.history] == [r.completed_ids for r in expected]
+
+
+def test_decode_graph_replays_match_eager_and_oracle(device) -> None:
+    """Decode-only iterations replay a captured HIP graph; between replays the engine does
+    its own eager work (metadata upload, prefill of late requests, token read-back). Every
+    step's tokens must equal the eager executor's and the oracle's."""
+
+    model = _fixture_model(device)
+    g = torch.Generator().manual_seed(321)
+    specs = [(f"g{i}", torch.randint(0, 64, (int(torch.randint(2, 30, (1,), generator=g)),),
+                                      generator=g).tolist(), 9) for i in range(7)]
+    runs = []
+    for use_graphs in (True, False):
+        manager = _manager(model, device, num_blocks=40, block_size=4)
+        scheduler = RequestScheduler(max_running_requests=5, cache_manager=manager)
+        engine = ContinuousBatchEngine(model, scheduler, manager)
+        if not use_graphs:
+            engine.executor.graphs = None
+        for rid, prompt, n in specs:
+            scheduler.submit(ScheduledRequest(rid, torch.tensor([prompt], device=device),
+                                              GenerationConfig(max_new_tokens=n)))
+        engine.run_until_idle()
+        runs.append(({rid: scheduler.get_request(rid).result.generated_token_ids[0].tolist()
+                      for rid, _, _ in specs}, engine))
+    (with_graphs, graph_engine), (eager, _) = runs
+    assert with_graphs == eager
+    assert graph_engine.executor.graphs._graphs, "no decode iteration was captured"
+    state = {k: v.detach().cpu() for k, v in model.state_dict().items()}
+    reference = oracle_engine.Engine(state, FIXTURE["config"], num_blocks=40, block_size=4,
+                                     max_running=5)
+    for rid, prompt, n in specs:
+        reference.submit(oracle_engine.Request(rid, list(prompt), n))
+    reference.run()
+    assert with_graphs == {rid: reference.finished[rid].generated for rid, _, _ in specs}

@@ -21,6 +21,7 @@ from collections.abc import Sequence
 
 import torch
 
+from tokserve_amd.batching.graphs import DecodeGraphs
 from tokserve_amd.batching.metadata import PackedBatchBuilder, SequenceWork
 from tokserve_amd.engine.model import LlamaModel
 from tokserve_amd.engine.paged.manager import PagedKVCacheManager
@@ -34,11 +35,14 @@ __all__ = ["BatchExecutor", "execute_prefill", "execute_decode"]
 class BatchExecutor:
     """Runs planned prefill and decode requests of one iteration as one packed forward."""
 
-    def __init__(self, model: LlamaModel, manager: PagedKVCacheManager) -> None:
+    def __init__(self, model: LlamaModel, manager: PagedKVCacheManager, *,
+                 use_graphs: bool = True) -> None:
         model.validate_storage(manager.storage)
         self.model = model
         self.manager = manager
         self.builder = PackedBatchBuilder(manager.storage.device, manager.storage.block_size)
+        graphs = DecodeGraphs(model, manager.storage)
+        self.graphs = graphs if use_graphs and graphs.supported() else None
 
     def execute(
         self, prefill: Sequence[ScheduledRequest], decode: Sequence[ScheduledRequest]
@@ -103,16 +107,20 @@ class BatchExecutor:
                  requests: list[ScheduledRequest]) -> list[int]:
         """One packed forward of the iteration; the next token of every sequence."""
 
+        if self.graphs is not None and not prefill:
+            logits, greedy = self.graphs.run(decode)
+            return self._select(logits, requests, greedy)
         batch = self.builder.build(prefill, decode)
         logits = self.model.forward_packed(batch, self.manager.storage)
         return self._select(logits, requests)
 
     @staticmethod
-    def _select(logits: torch.Tensor, requests: list[ScheduledRequest]) -> list[int]:
+    def _select(logits: torch.Tensor, requests: list[ScheduledRequest],
+                greedy: torch.Tensor | None = None) -> list[int]:
         """Greedy rows from one argmax launch; sampled rows one by one with their
         own generators; one device -> host copy."""
 
-        chosen = ops.greedy_argmax(logits).view(-1)
+        chosen = ops.greedy_argmax(logits).view(-1) if greedy is None else greedy.clone()
         for row, request in enumerate(requests):
             config = request.generation_config
             if config.do_sample:

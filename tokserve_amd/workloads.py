@@ -238,3 +238,32 @@ def norm_rope_packed(
         hidden.to(dev), weight.to(dev), query.to(dev), key.to(dev), positions.to(dev),
         cu.to(dev), 500000.0, 1e-5,
     )
+
+
+@dataclass(frozen=True)
+class RequestSpec:
+    request_id: str
+    prompt: tuple[int, ...]
+    max_new_tokens: int
+
+
+def tinyllama_requests(
+    *, seed: int = 0, num_requests: int = 128, min_prompt: int = 64, max_prompt: int = 1024,
+    max_new_tokens: int = 128, vocab_size: int = 32_000,
+) -> list[RequestSpec]:
+    """End-to-end serving workload: prompt lengths U[min_prompt, max_prompt] of random
+    token ids, max_new_tokens greedy tokens each (TinyLlama-1.1B shape, block size 16)."""
+
+    generator = torch.Generator().manual_seed(seed)
+    lengths = uniform_ints(num_requests, min_prompt, max_prompt, generator)
+    specs = []
+    for index, length in enumerate(lengths):
+        ids = torch.randint(0, vocab_size, (length,), generator=generator).tolist()
+        specs.append(RequestSpec(f"req{index:04d}", tuple(ids), max_new_tokens))
+    return specs
+
+
+def pool_blocks(specs: list[RequestSpec], block_size: int) -> int:
+    """Blocks that hold every request's prompt + generated tokens at once."""
+
+    return sum((len(s.prompt) + s.max_new_tokens + block_size - 1) // block_size for s in specs)
