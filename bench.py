@@ -361,6 +361,13 @@ def measure_e2e(device, seed: int, cpu_seconds: float | None) -> dict:
     wall = time.perf_counter() - start
     generated = sum(r.num_generated_tokens for r in engine.results)
     decode_steps = step_s[1:]
+    # Device time of one replay of the largest captured decode graph (the engine has
+    # finished; a replay rewrites the last step's K/V with the same values).
+    graphs = engine.executor.graphs
+    replay_ms = None
+    if graphs is not None and graphs._graphs:
+        captured = graphs._graphs[max(graphs._graphs)]
+        replay_ms = _time_ms(captured.graph.replay, 20, 3)
     result = {
         "workload": "e2e_tinyllama: TinyLlama-1.1B shape (22 layers, hidden 2048, 32/4 heads, "
                     "Dh 64, MLP 5632, vocab 32000), random init, bf16; 128 requests, prompts "
@@ -373,6 +380,9 @@ def measure_e2e(device, seed: int, cpu_seconds: float | None) -> dict:
         "tokens_per_s": round(generated / wall, 1),
         "prefill_step_s": round(step_s[0], 4),
         "decode_step_ms_mean": round(1e3 * sum(decode_steps) / max(len(decode_steps), 1), 3),
+        "decode_step_ms_median": round(1e3 * sorted(decode_steps)[len(decode_steps) // 2], 3)
+        if decode_steps else None,
+        "decode_graph_replay_ms": None if replay_ms is None else round(replay_ms, 4),
         "decode_tokens_per_s": round(
             sum(len(r.decode_ids) for r in engine.history[1:]) / max(sum(decode_steps), 1e-9), 1),
     }

@@ -72,9 +72,10 @@ class BatchExecutor:
             if len(prompt) > limit:
                 raise ValueError("sequence length exceeds max_position_embeddings")
             cache = self.manager.create_sequence(request.request_id, max_sequence_length=limit)
-            cache.begin_append(len(prompt))
-            pre_work.append((request, SequenceWork(prompt, 0, cache.block_ids)))
+            blocks = cache.reserve(len(prompt))
+            pre_work.append((request, SequenceWork(request.prompt_array, 0, blocks)))
         dec_work: list[tuple[ScheduledRequest, SequenceWork]] = []
+        caches = []
         for request in decode:
             cache = self.manager.get_sequence(request.request_id)
             length = cache.current_length
@@ -82,19 +83,19 @@ class BatchExecutor:
                 raise ValueError("paged decode requires a populated cache")
             if length >= cache.max_sequence_length:
                 raise ValueError("paged cache capacity exceeded")
-            cache.begin_append(1)
-            token = request.generated_tokens[-1]
-            dec_work.append((request, SequenceWork((token,), length, cache.block_ids)))
+            blocks = cache.reserve(1)
+            dec_work.append((request, SequenceWork((request.last_token,), length, blocks)))
+            caches.append(cache)
         work = pre_work + dec_work
         if not work:
             return tuple(completed)
 
         tokens = self._forward([w for _, w in pre_work], [w for _, w in dec_work],
                                [r for r, _ in work])
-        for request, _ in work:
-            cache = self.manager.get_sequence(request.request_id)
-            cache.mark_layers_written()
-            cache.finish_append()
+        for request, _ in pre_work:
+            self.manager.get_sequence(request.request_id).commit()
+        for cache in caches:
+            cache.commit()
         for index, (request, _) in enumerate(work):
             if index < len(pre_work):
                 request.mark_prefill_complete()

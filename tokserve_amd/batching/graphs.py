@@ -80,15 +80,13 @@ class DecodeGraphs:
         bs = self.block_size
         layout, total = self._layout(b, w)
         out = np.zeros(total, dtype=np.uint8)
-        starts = np.array([wk.start for wk in works], dtype=np.int64)
+        starts = np.fromiter((wk.start for wk in works), dtype=np.int64, count=b)
         tables = np.zeros((b, w), dtype=np.int32)
         for i, wk in enumerate(works):
-            if len(wk.tokens) != 1:
-                raise ValueError("a decode sequence appends exactly one token")
             tables[i, : len(wk.block_ids)] = wk.block_ids
         lens = (starts + 1).astype(np.int32)
         values = {
-            "token_ids": np.array([wk.tokens[0] for wk in works], dtype=np.int64),
+            "token_ids": np.fromiter((wk.tokens[0] for wk in works), dtype=np.int64, count=b),
             "positions": starts,
             "slot_mapping": tables[np.arange(b), starts // bs].astype(np.int64) * bs + starts % bs,
             "logits_rows": np.arange(b, dtype=np.int64),

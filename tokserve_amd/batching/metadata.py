@@ -21,6 +21,7 @@ device with a single asynchronous copy from a reused pinned staging buffer.
 
 from __future__ import annotations
 
+from collections.abc import Sequence
 from dataclasses import dataclass
 
 import numpy as np
@@ -34,9 +35,9 @@ class SequenceWork:
     """One sequence's share of an iteration: `tokens` appended at positions
     start .. start + len(tokens) - 1, through the sequence's block table."""
 
-    tokens: tuple[int, ...]
+    tokens: Sequence[int] | np.ndarray
     start: int
-    block_ids: tuple[int, ...]
+    block_ids: Sequence[int]
 
 
 @dataclass
@@ -91,7 +92,7 @@ class PackedBatchBuilder:
             raise ValueError("every sequence must append at least one token")
         starts = np.array([w.start for w in works], dtype=np.int64)
         n = int(lengths.sum())
-        token_ids = np.fromiter((t for w in works for t in w.tokens), dtype=np.int64, count=n)
+        token_ids = np.concatenate([np.asarray(w.tokens, dtype=np.int64) for w in works])
         offsets = np.concatenate(([0], np.cumsum(lengths)))
         row_seq = np.repeat(np.arange(len(works)), lengths)
         positions = starts[row_seq] + (np.arange(n) - offsets[row_seq])
@@ -144,7 +145,7 @@ class PackedBatchBuilder:
 
     def _staging_buffer(self, nbytes: int) -> torch.Tensor:
         if self._staging is None or self._staging.numel() < nbytes:
-            size = max(nbytes, 2 * (0 if self._staging is None else self._staging.numel()), 1 << 16)
+            size = max(nbytes, 2 * (0 if self._staging is None else self._staging.numel()), 1 << 22)
             pin = self.device.type == "cuda"
             self._staging = torch.empty(size, dtype=torch.uint8, pin_memory=pin)
         return self._staging

@@ -41,6 +41,7 @@ class SequencePagedKVCache:
         self._pending = 0
         self._pending_slots: torch.Tensor | None = None
         self._written: set[int] = set()
+        self._all_layers = frozenset(range(storage.num_layers))
         self._released = False
 
     @property
@@ -128,7 +129,26 @@ class SequencePagedKVCache:
         self._require_active()
         if self._pending == 0:
             raise RuntimeError("begin_append must be called before write_layer")
-        self._written = set(range(self.storage.num_layers))
+        self._written = self._all_layers
+
+    def reserve(self, sequence_length: int) -> list[int]:
+        """begin_append for the batched executor: returns the live block-id list
+        (read-only for the caller) after reserving the new positions."""
+
+        self.begin_append(sequence_length)
+        return self.block_table._ids
+
+    def commit(self) -> None:
+        """finish_append after packed KV-append launches wrote every layer."""
+
+        if self._released:
+            raise RuntimeError("sequence cache has been released")
+        if self._pending == 0:
+            raise RuntimeError("no append is in progress")
+        self._length += self._pending
+        self._pending = 0
+        self._pending_slots = None
+        self._written = set()
 
     def read_layer(
         self, layer_index: int, *, include_pending: bool = False

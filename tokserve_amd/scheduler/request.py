@@ -12,6 +12,7 @@ from __future__ import annotations
 
 from enum import Enum
 
+import numpy as np
 import torch
 
 from tokserve_amd.generation.types import GenerationConfig, GenerationResult, StopReason
@@ -48,6 +49,7 @@ class ScheduledRequest:
         self.generation_config = generation_config
         self._input_ids = input_ids.clone()
         self._prompt: tuple[int, ...] = tuple(int(t) for t in input_ids[0].tolist())
+        self._prompt_array = np.asarray(self._prompt, dtype=np.int64)
         self._generated: list[int] = []
         self._state = RequestState.WAITING
         self._result: GenerationResult | None = None
@@ -67,6 +69,18 @@ class ScheduledRequest:
     @property
     def prompt_tokens(self) -> tuple[int, ...]:
         return self._prompt
+
+    @property
+    def prompt_array(self) -> np.ndarray:
+        """The prompt as an int64 NumPy array (read-only use)."""
+
+        return self._prompt_array
+
+    @property
+    def last_token(self) -> int:
+        """The most recently generated token (the next decode input)."""
+
+        return self._generated[-1]
 
     @property
     def generated_tokens(self) -> tuple[int, ...]:
