@@ -220,6 +220,18 @@ int32_t tks_argmax(const void *logits, int64_t row_stride, int64_t num_rows, int
                    int64_t *out_ids, int32_t dtype, tks_stream_t stream);
 
 /* ------------------------------------------------------------------------
+ * SwiGLU activation on fused gate/up rows: for each row r and j < I,
+ *   out[r*out_row_stride + j] = r(r(silu(g)) * u),  g = gate_up[r*gate_up_row_stride + j],
+ *   u = gate_up[r*gate_up_row_stride + I + j],  silu(g) = g / (1 + exp(-g)) in fp32,
+ * r = rounding to dtype. Replaces `functional.silu(gate_proj(x)) * up_proj(x)` of
+ * SwiGLU.forward (tokserve/engine/layers.py:84-91) after one GEMM over the stacked
+ * gate/up weights.
+ */
+int32_t tks_silu_mul(const void *gate_up, int64_t gate_up_row_stride, int64_t num_rows,
+                     int64_t intermediate_size, void *out, int64_t out_row_stride, int32_t dtype,
+                     tks_stream_t stream);
+
+/* ------------------------------------------------------------------------
  * Elementwise out[i] = x[i] + y[i] over num_elements contiguous elements.
  * Replaces vector_add (tokserve/kernels/vector.py:6-41). dtype FLOAT32 or
  * FLOAT16 (TKS_ERR_TYPE otherwise); num_elements == 0 launches nothing.

@@ -5,8 +5,8 @@ modules, so a state dict moves between the two and a seeded random
 initialisation produces the same weights. The forward passes run on HIP
 tensors only: RMSNorm through the tks_rms_norm kernel (the reference's
 rounding: normalised value rounded to the input dtype, then times the weight,
-output dtype = promote(weight, input)), SwiGLU through library GEMMs with the
-gate and up projections fused into one.
+output dtype = promote(weight, input)), SwiGLU as one library GEMM over the
+stacked gate/up weights, the tks_silu_mul kernel, and the down GEMM.
 """
 
 from __future__ import annotations
@@ -112,5 +112,4 @@ class SwiGLU(nn.Module):
         gate_up = functional.linear(
             inputs, fused_weight(self, [self.gate_proj, self.up_proj], "_gate_up")
         )
-        gate, up = gate_up.split(self.intermediate_size, dim=-1)
-        return self.down_proj(functional.silu(gate) * up)
+        return self.down_proj(ops.silu_mul(gate_up))

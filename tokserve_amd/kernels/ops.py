@@ -517,3 +517,25 @@ def vector_add(x: torch.Tensor, y: torch.Tensor, out: torch.Tensor | None = None
     )
     _lib.check(status, "vector_add")
     return out
+
+
+def silu_mul(gate_up: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """SwiGLU activation: (..., 2I) stacked gate/up rows -> (..., I) silu(gate) * up,
+    rounded as functional.silu(gate) * up in the input dtype."""
+
+    require_hip("silu_mul", gate_up)
+    if gate_up.ndim < 1 or gate_up.shape[-1] % 2 != 0:
+        raise ValueError("gate_up must have an even last dimension (gate then up)")
+    inter = gate_up.shape[-1] // 2
+    rows = gate_up.reshape(-1, 2 * inter)
+    if rows.stride(-1) != 1:
+        rows = rows.contiguous()
+    if out is None:
+        out = torch.empty((*gate_up.shape[:-1], inter), dtype=gate_up.dtype, device=gate_up.device)
+    out_rows = out.view(-1, inter)
+    status = _lib.load().tks_silu_mul(
+        rows.data_ptr(), rows.stride(0), rows.shape[0], inter, out_rows.data_ptr(),
+        out_rows.stride(0), _lib.dtype_code(gate_up.dtype), _lib.stream_of(gate_up),
+    )
+    _lib.check(status, "silu_mul")
+    return out
