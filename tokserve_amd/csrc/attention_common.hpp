@@ -116,6 +116,9 @@ struct PrefillArgs {
   int32_t key_cap;
   void *out;
   int64_t o_ts, o_hs;
+  int32_t num_kv_heads;
+  int32_t num_pairs;  // sequences * KV heads
+  int32_t tiles;      // query tiles per (sequence, KV head): ceil(max_query_len / tile)
 };
 
 // 16-key pages of one sequence the MFMA prefill kernel holds in LDS: it serves

@@ -37,8 +37,9 @@ namespace tks {
 namespace {
 
 constexpr int kPWaves = 4;
+constexpr int kXcds = 8;  // MI355X: 8 accelerator dies, workgroups dealt round-robin
 constexpr int kKeysPerStep = 32;
-constexpr int kStages = 3;  // LDS ring: step s computes while s+1 and s+2 load
+constexpr int kStages = 3;  // LDS ring: steps s+1 and s+2 load while step s computes
 
 typedef __attribute__((address_space(3))) void lds_void;
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
@@ -54,6 +55,26 @@ __device__ __forceinline__ uint32_t lds_address(P *p) {
 __device__ __forceinline__ void load_lds16(const void *src, void *lds) {
 #if __HIP_DEVICE_COMPILE__
   __builtin_amdgcn_global_load_lds(src, (lds_void *)lds, 16, 0, 0);
+#endif
+}
+
+// Makes a wave-uniform value an SGPR that is ready here: every scalar load
+// behind it completes before this point, so no wait for such a load can land
+// inside the main loop (a scalar-load wait also waits for all pending LDS
+// reads, which would serialise the loop's LDS pipeline).
+template <typename V>
+__device__ __forceinline__ void settle_sgpr(V &v) {
+#if __HIP_DEVICE_COMPILE__
+  asm volatile("" : "+s"(v));
+#endif
+}
+
+// Orders the computation of v before the asm statements that follow (a
+// volatile asm that takes v as an operand; it emits nothing).
+template <typename V>
+__device__ __forceinline__ void pin_vgpr(V &v) {
+#if __HIP_DEVICE_COMPILE__
+  asm volatile("" : "+v"(v));
 #endif
 }
 
@@ -95,10 +116,12 @@ __device__ __forceinline__ float xgroup_sum(float x) {
 #define TKS_RDTR(o, a, off) "ds_read_b64_tr_b16 %" TKS_S(o) ", %" TKS_S(a) " offset:%" TKS_S(off) "\n\t"
 #define TKS_RD32(o, a, off) "ds_read_b32 %" TKS_S(o) ", %" TKS_S(a) " offset:" TKS_S(off) "\n\t"
 
-// The LDS reads of one step: K operands k[kt * NC + c] (rows kt*16 + r),
-// V^T halves v[d * 2 + page] and the block ids of the step two ahead, all
-// complete when the block ends. O0 is the byte offset of the ring stage, O1 =
-// O0 + 16 rows (the second page).
+// LDS reads of one step, issued without waiting: K operands k[kt * NC + c]
+// (rows kt*16 + r) of a stage, and V^T halves v[d * 2 + page] plus the block
+// ids of a later step. O0 is the byte offset of the ring stage, O1 = O0 + 16
+// rows (the second page). The results are valid only after lds_wait(...) on
+// them: the wait is a separate asm statement that names the same registers,
+// so nothing reads them before it.
 template <int DH>
 struct StepReads;
 
@@ -106,28 +129,51 @@ template <>
 struct StepReads<128> {
   static constexpr int kRows16 = 16 * 128 * 2;  // bytes of 16 rows
   template <int O0, int O1>
-  static __device__ __forceinline__ void run(const uint32_t (&ka)[4], const uint32_t (&va)[8],
-                                             uint32_t ba, u32x4 (&k)[8], u32x2 (&v)[16],
-                                             uint32_t (&bid)[2]) {
+  static __device__ __forceinline__ void keys(const uint32_t (&ka)[4], u32x4 (&k)[8]) {
     static_assert(O1 == O0 + kRows16 && O1 < 65536, "offsets");
 #if __HIP_DEVICE_COMPILE__
     asm volatile(
-        TKS_RD128(0, 26, 39) TKS_RD128(1, 27, 39) TKS_RD128(2, 28, 39) TKS_RD128(3, 29, 39)
-        TKS_RD128(4, 26, 40) TKS_RD128(5, 27, 40) TKS_RD128(6, 28, 40) TKS_RD128(7, 29, 40)
-        TKS_RDTR(8, 30, 39) TKS_RDTR(9, 30, 40) TKS_RDTR(10, 31, 39) TKS_RDTR(11, 31, 40)
-        TKS_RDTR(12, 32, 39) TKS_RDTR(13, 32, 40) TKS_RDTR(14, 33, 39) TKS_RDTR(15, 33, 40)
-        TKS_RDTR(16, 34, 39) TKS_RDTR(17, 34, 40) TKS_RDTR(18, 35, 39) TKS_RDTR(19, 35, 40)
-        TKS_RDTR(20, 36, 39) TKS_RDTR(21, 36, 40) TKS_RDTR(22, 37, 39) TKS_RDTR(23, 37, 40)
-        TKS_RD32(24, 38, 0) TKS_RD32(25, 38, 4)
-        "s_waitcnt lgkmcnt(0)"
+        TKS_RD128(0, 8, 12) TKS_RD128(1, 9, 12) TKS_RD128(2, 10, 12) TKS_RD128(3, 11, 12)
+        TKS_RD128(4, 8, 13) TKS_RD128(5, 9, 13) TKS_RD128(6, 10, 13) TKS_RD128(7, 11, 13)
         : "=&v"(k[0]), "=&v"(k[1]), "=&v"(k[2]), "=&v"(k[3]), "=&v"(k[4]), "=&v"(k[5]),
-          "=&v"(k[6]), "=&v"(k[7]), "=&v"(v[0]), "=&v"(v[1]), "=&v"(v[2]), "=&v"(v[3]),
-          "=&v"(v[4]), "=&v"(v[5]), "=&v"(v[6]), "=&v"(v[7]), "=&v"(v[8]), "=&v"(v[9]),
-          "=&v"(v[10]), "=&v"(v[11]), "=&v"(v[12]), "=&v"(v[13]), "=&v"(v[14]), "=&v"(v[15]),
-          "=&v"(bid[0]), "=&v"(bid[1])
-        : "v"(ka[0]), "v"(ka[1]), "v"(ka[2]), "v"(ka[3]), "v"(va[0]), "v"(va[1]), "v"(va[2]),
-          "v"(va[3]), "v"(va[4]), "v"(va[5]), "v"(va[6]), "v"(va[7]), "v"(ba), "i"(O0), "i"(O1)
+          "=&v"(k[6]), "=&v"(k[7])
+        : "v"(ka[0]), "v"(ka[1]), "v"(ka[2]), "v"(ka[3]), "i"(O0), "i"(O1)
         : "memory");
+#endif
+  }
+  template <int O0, int O1>
+  static __device__ __forceinline__ void values(const uint32_t (&va)[8], uint32_t ba, u32x2 (&v)[16],
+                                                uint32_t (&bid)[2]) {
+    static_assert(O1 == O0 + kRows16 && O1 < 65536, "offsets");
+#if __HIP_DEVICE_COMPILE__
+    asm volatile(
+        TKS_RDTR(0, 18, 27) TKS_RDTR(1, 18, 28) TKS_RDTR(2, 19, 27) TKS_RDTR(3, 19, 28)
+        TKS_RDTR(4, 20, 27) TKS_RDTR(5, 20, 28) TKS_RDTR(6, 21, 27) TKS_RDTR(7, 21, 28)
+        TKS_RDTR(8, 22, 27) TKS_RDTR(9, 22, 28) TKS_RDTR(10, 23, 27) TKS_RDTR(11, 23, 28)
+        TKS_RDTR(12, 24, 27) TKS_RDTR(13, 24, 28) TKS_RDTR(14, 25, 27) TKS_RDTR(15, 25, 28)
+        TKS_RD32(16, 26, 0) TKS_RD32(17, 26, 4)
+        : "=&v"(v[0]), "=&v"(v[1]), "=&v"(v[2]), "=&v"(v[3]), "=&v"(v[4]), "=&v"(v[5]),
+          "=&v"(v[6]), "=&v"(v[7]), "=&v"(v[8]), "=&v"(v[9]), "=&v"(v[10]), "=&v"(v[11]),
+          "=&v"(v[12]), "=&v"(v[13]), "=&v"(v[14]), "=&v"(v[15]), "=&v"(bid[0]), "=&v"(bid[1])
+        : "v"(va[0]), "v"(va[1]), "v"(va[2]), "v"(va[3]), "v"(va[4]), "v"(va[5]), "v"(va[6]),
+          "v"(va[7]), "v"(ba), "i"(O0), "i"(O1)
+        : "memory");
+#endif
+  }
+  static __device__ __forceinline__ void wait_keys(u32x4 (&k)[8]) {
+#if __HIP_DEVICE_COMPILE__
+    asm volatile("s_waitcnt lgkmcnt(0)"
+                 : "+v"(k[0]), "+v"(k[1]), "+v"(k[2]), "+v"(k[3]), "+v"(k[4]), "+v"(k[5]),
+                   "+v"(k[6]), "+v"(k[7])::"memory");
+#endif
+  }
+  static __device__ __forceinline__ void wait_values(u32x2 (&v)[16], uint32_t (&bid)[2]) {
+#if __HIP_DEVICE_COMPILE__
+    asm volatile("s_waitcnt lgkmcnt(0)"
+                 : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3]), "+v"(v[4]), "+v"(v[5]),
+                   "+v"(v[6]), "+v"(v[7]), "+v"(v[8]), "+v"(v[9]), "+v"(v[10]), "+v"(v[11]),
+                   "+v"(v[12]), "+v"(v[13]), "+v"(v[14]), "+v"(v[15]), "+v"(bid[0]),
+                   "+v"(bid[1])::"memory");
 #endif
   }
 };
@@ -136,23 +182,41 @@ template <>
 struct StepReads<64> {
   static constexpr int kRows16 = 16 * 64 * 2;
   template <int O0, int O1>
-  static __device__ __forceinline__ void run(const uint32_t (&ka)[2], const uint32_t (&va)[4],
-                                             uint32_t ba, u32x4 (&k)[4], u32x2 (&v)[8],
-                                             uint32_t (&bid)[1]) {
+  static __device__ __forceinline__ void keys(const uint32_t (&ka)[2], u32x4 (&k)[4]) {
+    static_assert(O1 == O0 + kRows16 && O1 < 65536, "offsets");
+#if __HIP_DEVICE_COMPILE__
+    asm volatile(TKS_RD128(0, 4, 6) TKS_RD128(1, 5, 6) TKS_RD128(2, 4, 7) TKS_RD128(3, 5, 7)
+                 : "=&v"(k[0]), "=&v"(k[1]), "=&v"(k[2]), "=&v"(k[3])
+                 : "v"(ka[0]), "v"(ka[1]), "i"(O0), "i"(O1)
+                 : "memory");
+#endif
+  }
+  template <int O0, int O1>
+  static __device__ __forceinline__ void values(const uint32_t (&va)[4], uint32_t ba, u32x2 (&v)[8],
+                                                uint32_t (&bid)[1]) {
     static_assert(O1 == O0 + kRows16 && O1 < 65536, "offsets");
 #if __HIP_DEVICE_COMPILE__
     asm volatile(
-        TKS_RD128(0, 13, 20) TKS_RD128(1, 14, 20) TKS_RD128(2, 13, 21) TKS_RD128(3, 14, 21)
-        TKS_RDTR(4, 15, 20) TKS_RDTR(5, 15, 21) TKS_RDTR(6, 16, 20) TKS_RDTR(7, 16, 21)
-        TKS_RDTR(8, 17, 20) TKS_RDTR(9, 17, 21) TKS_RDTR(10, 18, 20) TKS_RDTR(11, 18, 21)
-        TKS_RD32(12, 19, 0)
-        "s_waitcnt lgkmcnt(0)"
-        : "=&v"(k[0]), "=&v"(k[1]), "=&v"(k[2]), "=&v"(k[3]), "=&v"(v[0]), "=&v"(v[1]),
-          "=&v"(v[2]), "=&v"(v[3]), "=&v"(v[4]), "=&v"(v[5]), "=&v"(v[6]), "=&v"(v[7]),
-          "=&v"(bid[0])
-        : "v"(ka[0]), "v"(ka[1]), "v"(va[0]), "v"(va[1]), "v"(va[2]), "v"(va[3]), "v"(ba),
-          "i"(O0), "i"(O1)
+        TKS_RDTR(0, 9, 14) TKS_RDTR(1, 9, 15) TKS_RDTR(2, 10, 14) TKS_RDTR(3, 10, 15)
+        TKS_RDTR(4, 11, 14) TKS_RDTR(5, 11, 15) TKS_RDTR(6, 12, 14) TKS_RDTR(7, 12, 15)
+        TKS_RD32(8, 13, 0)
+        : "=&v"(v[0]), "=&v"(v[1]), "=&v"(v[2]), "=&v"(v[3]), "=&v"(v[4]), "=&v"(v[5]),
+          "=&v"(v[6]), "=&v"(v[7]), "=&v"(bid[0])
+        : "v"(va[0]), "v"(va[1]), "v"(va[2]), "v"(va[3]), "v"(ba), "i"(O0), "i"(O1)
         : "memory");
+#endif
+  }
+  static __device__ __forceinline__ void wait_keys(u32x4 (&k)[4]) {
+#if __HIP_DEVICE_COMPILE__
+    asm volatile("s_waitcnt lgkmcnt(0)"
+                 : "+v"(k[0]), "+v"(k[1]), "+v"(k[2]), "+v"(k[3])::"memory");
+#endif
+  }
+  static __device__ __forceinline__ void wait_values(u32x2 (&v)[8], uint32_t (&bid)[1]) {
+#if __HIP_DEVICE_COMPILE__
+    asm volatile("s_waitcnt lgkmcnt(0)"
+                 : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3]), "+v"(v[4]), "+v"(v[5]),
+                   "+v"(v[6]), "+v"(v[7]), "+v"(bid[0])::"memory");
 #endif
   }
 };
@@ -197,9 +261,19 @@ __global__ __launch_bounds__(64 * kPWaves) __attribute__((amdgpu_waves_per_eu(2,
   const int r = lane & 15;
   const int g = lane >> 4;
 
-  const int tile = blockIdx.x;
-  const int kvh = blockIdx.y;
-  const int b = blockIdx.z;
+  // XCD-aware work mapping. Workgroup i runs on XCD i % 8, and each XCD has its
+  // own L2. All query tiles of one (sequence, KV head) read the same K/V pages
+  // in the same order, so they are placed on one XCD and dispatched together
+  // (the pages come from HBM once per pair, then from that XCD's L2); pairs are
+  // dealt round-robin over the XCDs. Within a pair the later tiles (more keys)
+  // start first.
+  const int xcd = blockIdx.x % kXcds;
+  const int slot = blockIdx.x / kXcds;
+  const int pair = (slot / a.tiles) * kXcds + xcd;
+  if (pair >= a.num_pairs) return;
+  const int tile = a.tiles - 1 - slot % a.tiles;
+  const int kvh = pair % a.num_kv_heads;
+  const int b = pair / a.num_kv_heads;
   const int q0 = a.cu_q[b];
   const int q_len = a.cu_q[b + 1] - q0;
   const int t0 = tile * QT;
@@ -307,43 +381,51 @@ __global__ __launch_bounds__(64 * kPWaves) __attribute__((amdgpu_waves_per_eu(2,
   }
 
   // Q is in registers before the first HBM -> LDS load, so no wait inside the
-  // loop has to count it.
+  // loop has to count it; likewise the scalars the loop reads.
+  float scale_log2 = a.scale_log2;
+  settle_sgpr(scale_log2);
+  settle_sgpr(kc);
+  settle_sgpr(vc);
   __builtin_amdgcn_s_waitcnt(0);
   {
-    int32_t blk[LOADS], blk1[LOADS];
+    int32_t blk[3][LOADS];
 #pragma unroll
-    for (int k = 0; k < LOADS; ++k) {
-      blk[k] = bt_s[min(page_of_load(0, k), kPrefillBtWindow - 1)];
-      blk1[k] = bt_s[min(page_of_load(1, k), kPrefillBtWindow - 1)];
-    }
-    if (n_steps > 0) issue(Const<0>{}, blk);
-    if (n_steps > 1) issue(Const<1>{}, blk1);
+    for (int i = 0; i < 3; ++i)
+#pragma unroll
+      for (int k = 0; k < LOADS; ++k) blk[i][k] = bt_s[min(page_of_load(i, k), kPrefillBtWindow - 1)];
+    if (n_steps > 0) issue(Const<0>{}, blk[0]);
+    if (n_steps > 1) issue(Const<1>{}, blk[1]);
+    if (n_steps > 2) issue(Const<2>{}, blk[2]);
   }
-
-  // One step: keys s*KS .. s*KS + KS - 1 from ring stage STG.
-  auto step = [&](auto stage_c, int s) {
-    constexpr int STG = decltype(stage_c)::value;
-    constexpr int O0 = STG * STAGE * (int)sizeof(T);
-    if (s + 1 < n_steps)
+  using Reads = StepReads<DH>;
+  constexpr int kStageBytes = STAGE * (int)sizeof(T);
+  constexpr int kRowsBytes = 16 * DH * (int)sizeof(T);
+  u32x4 kraw[2 * NC];  // K operands of the step about to run
+  if (n_steps > 0) {
+    // Step 0's loads are the first issued: wait until only steps 1 and 2 remain.
+    if (n_steps > 2)
+      wait_loads_and_barrier<4 * LOADS>();
+    else if (n_steps > 1)
       wait_loads_and_barrier<2 * LOADS>();
     else
       wait_loads_and_barrier<0>();
+    Reads::template keys<0, kRowsBytes>(ka_addr, kraw);
+    Reads::wait_keys(kraw);
+  }
 
-    const int ahead = min(s + 2, n_steps - 1);
+  // One step: keys s*KS .. s*KS + KS - 1 from ring stage STG, whose K operands
+  // are already in kraw. Pipeline: V(s) LDS reads overlap QK(s) and the
+  // softmax; after a barrier that also frees stage s, K(s+1) is read while the
+  // PV(s) MFMAs run, and the loads of step s+3 go into stage s.
+  auto step = [&](auto stage_c, int s) {
+    constexpr int STG = decltype(stage_c)::value;
+    constexpr int O0 = STG * kStageBytes;
+    constexpr int N0 = ((STG + 1) % kStages) * kStageBytes;
+    const int ahead = min(s + 3, n_steps - 1);
     const uint32_t ba = bt_base + page_of_load(ahead, 0) * 4;
-    u32x4 kraw[2 * NC];
     u32x2 vraw[2 * DT];
     uint32_t bid[LOADS];
-    StepReads<DH>::template run<O0, O0 + 16 * DH * (int)sizeof(T)>(ka_addr, va_addr, ba, kraw, vraw,
-                                                                     bid);
-    if (s + 2 < n_steps) {
-      // With LOADS == 2 the second load's page is the first + 1 (the block-id
-      // read at offset 4); with LOADS == 1 the page depends on the wave.
-      int32_t blk[LOADS];
-#pragma unroll
-      for (int k = 0; k < LOADS; ++k) blk[k] = (int32_t)bid[k];
-      issue(Const<(STG + 2) % kStages>{}, blk);
-    }
+    Reads::template values<O0, O0 + kRowsBytes>(va_addr, ba, vraw, bid);
 
     v8 ka[2][NC];
 #pragma unroll
@@ -354,41 +436,27 @@ __global__ __launch_bounds__(64 * kPWaves) __attribute__((amdgpu_waves_per_eu(2,
                              kraw[kt * NC + c][3]);
         ka[kt][c] = as_v8<T>(u);
       }
-    v8 va[DT];
+    // S^T for both row tiles first: the softmax of tile 0 then overlaps tile 1's MFMAs.
+    f4 st[RT][2];
 #pragma unroll
-    for (int d = 0; d < DT; ++d) {
-      uint4 u = make_uint4(vraw[2 * d][0], vraw[2 * d][1], vraw[2 * d + 1][0], vraw[2 * d + 1][1]);
-      va[d] = as_v8<T>(u);
-    }
-    const bool tail = s * KS + KS > n_keys;
-    if (tail) {
-      // V rows past the last key hold whatever the pool has there; their
-      // probabilities are 0, and 0 * NaN would not be.
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const int key = s * KS + (e / 4) * 16 + g * 4 + (e % 4);
-        if (key >= n_keys) {
-#pragma unroll
-          for (int d = 0; d < DT; ++d) va[d][e] = static_cast<typename M::elem>(0.f);
-        }
-      }
-    }
-    const bool need_mask = s * KS + KS - 1 > min_pos || tail;
-
-#pragma unroll
-    for (int j = 0; j < RT; ++j) {
-      f4 st[2];
+    for (int j = 0; j < RT; ++j)
 #pragma unroll
       for (int kt = 0; kt < 2; ++kt) {
-        st[kt] = f4{0.f, 0.f, 0.f, 0.f};
+        st[j][kt] = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int c = 0; c < NC; ++c) st[kt] = M::run(ka[kt][c], qb[j][c], st[kt]);
+        for (int c = 0; c < NC; ++c) st[j][kt] = M::run(ka[kt][c], qb[j][c], st[j][kt]);
       }
+    const bool tail = s * KS + KS > n_keys;
+    const bool need_mask = s * KS + KS - 1 > min_pos || tail;
+
+    v8 pb[RT];
+#pragma unroll
+    for (int j = 0; j < RT; ++j) {
       float sv[8];
 #pragma unroll
       for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) sv[kt * 4 + i] = st[kt][i];
+        for (int i = 0; i < 4; ++i) sv[kt * 4 + i] = st[j][kt][i];
       if (need_mask) {
 #pragma unroll
         for (int kt = 0; kt < 2; ++kt)
@@ -402,7 +470,7 @@ __global__ __launch_bounds__(64 * kPWaves) __attribute__((amdgpu_waves_per_eu(2,
       // the scale is positive, so max(s * c) = max(s) * c.
       float mx = nan_max(nan_max(nan_max(sv[0], sv[1]), nan_max(sv[2], sv[3])),
                          nan_max(nan_max(sv[4], sv[5]), nan_max(sv[6], sv[7])));
-      mx = xgroup_max(mx) * a.scale_log2;
+      mx = xgroup_max(mx) * scale_log2;
       // The reference max only moves when the new scores exceed it by more
       // than 8 (probabilities stay <= 2^8 meanwhile); the rescale of O and l
       // that a move costs is then rare after the first keys of a row.
@@ -418,16 +486,58 @@ __global__ __launch_bounds__(64 * kPWaves) __attribute__((amdgpu_waves_per_eu(2,
       }
       const float ref = m_new == -INFINITY ? 0.f : m_new;  // fully masked so far: p = 0
       float ps = 0.f;
-      v8 pb;
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
-        const float p = fast_exp2(__builtin_fmaf(sv[i], a.scale_log2, -ref));
+        const float p = fast_exp2(__builtin_fmaf(sv[i], scale_log2, -ref));
         ps += p;
-        pb[i] = static_cast<typename M::elem>(p);
+        pb[j][i] = static_cast<typename M::elem>(p);
       }
       l[j] += ps;
+    }
+
+    // The probabilities are computed while the V reads are in flight, not after
+    // the wait (the compiler would otherwise sink them to their MFMA use).
 #pragma unroll
-      for (int d = 0; d < DT; ++d) o[j][d] = M::run(va[d], pb, o[j][d]);
+    for (int j = 0; j < RT; ++j) pin_vgpr(pb[j]);
+    Reads::wait_values(vraw, bid);
+    v8 va[DT];
+#pragma unroll
+    for (int d = 0; d < DT; ++d) {
+      uint4 u = make_uint4(vraw[2 * d][0], vraw[2 * d][1], vraw[2 * d + 1][0], vraw[2 * d + 1][1]);
+      va[d] = as_v8<T>(u);
+    }
+    if (tail) {
+      // V rows past the last key hold whatever the pool has there; their
+      // probabilities are 0, and 0 * NaN would not be.
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int key = s * KS + (e / 4) * 16 + g * 4 + (e % 4);
+        if (key >= n_keys) {
+#pragma unroll
+          for (int d = 0; d < DT; ++d) va[d][e] = static_cast<typename M::elem>(0.f);
+        }
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < RT; ++j)
+#pragma unroll
+      for (int d = 0; d < DT; ++d) o[j][d] = M::run(va[d], pb[j], o[j][d]);
+
+    if (s + 1 < n_steps) {
+      // Step s+1's loads done (only step s+2's may remain), and every wave is
+      // past its reads of stage s: K(s+1) can be read and stage s refilled.
+      if (s + 2 < n_steps)
+        wait_loads_and_barrier<2 * LOADS>();
+      else
+        wait_loads_and_barrier<0>();
+      Reads::template keys<N0, N0 + kRowsBytes>(ka_addr, kraw);
+      if (s + 3 < n_steps) {
+        int32_t blk[LOADS];
+#pragma unroll
+        for (int k = 0; k < LOADS; ++k) blk[k] = (int32_t)bid[k];
+        issue(Const<STG>{}, blk);
+      }
+      Reads::wait_keys(kraw);
     }
   };
 
@@ -462,9 +572,14 @@ int32_t launch_typed(const PrefillArgs &a, int32_t num_seqs, int32_t num_kv_head
   constexpr int ROWS = kPWaves * RT * 16;
 #define TKS_PREFILL(DH, GG)                                                                  \
   if (head_dim == DH && G == GG) {                                                           \
-    const dim3 grid(static_cast<unsigned>(ceil_div(max_query_len, ROWS / GG)), num_kv_heads, \
-                    num_seqs);                                                               \
-    prefill_mfma_kernel<T, DH, GG, RT><<<grid, 64 * kPWaves, 0, s>>>(a);                     \
+    PrefillArgs args = a;                                                                    \
+    args.num_kv_heads = num_kv_heads;                                                        \
+    args.num_pairs = num_seqs * num_kv_heads;                                                \
+    args.tiles = static_cast<int32_t>(ceil_div(max_query_len, ROWS / GG));                   \
+    if (args.tiles == 0 || args.num_pairs == 0) return TKS_OK;                               \
+    const int64_t groups = ceil_div(args.num_pairs, kXcds);                                  \
+    const dim3 grid(static_cast<unsigned>(groups * kXcds * args.tiles), 1, 1);               \
+    prefill_mfma_kernel<T, DH, GG, RT><<<grid, 64 * kPWaves, 0, s>>>(args);                  \
     return check_launch();                                                                   \
   }
   TKS_PREFILL(128, 4)
