@@ -224,8 +224,10 @@ __global__ __launch_bounds__(64) void merge_splits_kernel(
 // ------------------------------------------------------------------------
 
 // A batch with at least this many (sequence, KV head) pairs fills the GPU
-// without splitting a sequence across workgroups (3-4 workgroups per CU).
-constexpr int64_t kFillItems = 1024;
+// without splitting a sequence across workgroups: one 4-wave workgroup per CU.
+// (Splitting such batches measured slower: at 128 sequences x 4 KV heads,
+// Dh 64, contexts up to 1152, 21 us unsplit against 29 us split.)
+constexpr int64_t kFillItems = 256;
 constexpr int64_t kMinSplitPages = 16;
 
 int32_t choose_pages_per_split(int32_t num_seqs, int32_t num_kv_heads, int32_t block_size,
