@@ -187,6 +187,7 @@ def main() -> int:
         result["secondary"] = {
             "mixed_step": measure_mixed(device, 20, 5),
             "norm_rope": measure_norm_rope(device, 20, 5),
+            "small_fp32_step": measure_small_fp32_step(device, 50, 10),
         }
     if not args.no_e2e:
         e2e = measure_e2e(device, args.seed,
@@ -267,6 +268,60 @@ def measure_mixed(device, steps: int, warmup: int) -> dict:
         "prefill_mfma_frac_of_2500_tflops": round(flops / (ms_pre * 1e-3) / 2.5e15, 4),
         "decode_ms": round(ms_dec, 5),
         "decode_gbps": round(dec_bytes / (ms_dec * 1e-3) / 1e9, 1),
+    }
+
+
+def measure_small_fp32_step(device, steps: int, warmup: int) -> dict:
+    """The CPU-runnable fp32 decode step (8 sequences, contexts U[16, 512] + 1, 8/2 heads,
+    Dh 64, block 16, 512-block pool): RMSNorm (hidden 512, eps 1e-5), RoPE (theta 1e4) of
+    the new Q/K at each sequence's next position, KV append through slot_mapping, split-K
+    decode attention. Launch-bound: reported in microseconds, eager and as a HIP graph."""
+
+    import torch
+
+    from tokserve_amd import workloads
+    from tokserve_amd.kernels import ops
+
+    batch = workloads.decode_fp32_small(device, seed=0)
+    g = torch.Generator().manual_seed(1)
+    hidden = torch.randn(8, 512, generator=g).to(device)
+    weight = (1.0 + 0.02 * torch.randn(512, generator=g)).to(device)
+    normed = torch.empty_like(hidden)
+    new_k = torch.randn(8, 2, 64, generator=g).to(device)
+    new_v = torch.randn(8, 2, 64, generator=g).to(device)
+    positions = torch.tensor([c - 1 for c in batch.contexts], dtype=torch.int64, device=device)
+    tables = batch.block_tables.cpu()
+    slots = torch.tensor([int(tables[b, (c - 1) // 16]) * 16 + (c - 1) % 16
+                          for b, c in enumerate(batch.contexts)], dtype=torch.int64, device=device)
+    table = ops.RotaryTable(64, theta=10_000.0, max_position=1024, dtype=torch.float32, device=device)
+    out = torch.empty_like(batch.query)
+    q4 = batch.query.transpose(0, 1).unsqueeze(0)
+    k4 = new_k.transpose(0, 1).unsqueeze(0)
+    q_rot = torch.empty_like(q4)
+    k_rot = torch.empty_like(k4)
+
+    def step() -> None:
+        ops.rms_norm(hidden, weight, 1e-5, out=normed)
+        ops.rope(q4, k4, positions, table, query_out=q_rot, key_out=k_rot)
+        ops.kv_append(k_rot[0].transpose(0, 1), new_v, batch.key_cache, batch.value_cache, slots, 0)
+        ops.paged_attention_decode(
+            q_rot[0].transpose(0, 1), batch.key_cache, batch.value_cache, batch.block_tables,
+            batch.seq_lens, layer_index=0, max_seq_len=batch.max_seq_len, out=out)
+
+    eager_us = _time_ms(step, steps, warmup) * 1e3
+    step()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        step()
+    graph_us = _time_ms(graph.replay, steps, warmup) * 1e3
+    kv_bytes = sum(batch.contexts) * 2 * 64 * 2 * 4
+    return {
+        "workload": "decode_fp32_small: 8 seqs, ctx U[16,512]+1, Hq 8 / Hkv 2, Dh 64, block 16, "
+                    "fp32; RMSNorm 512 + RoPE + KV append + decode attention",
+        "step_us_eager": round(eager_us, 2),
+        "step_us_graph": round(graph_us, 2),
+        "kv_bytes": kv_bytes,
     }
 
 

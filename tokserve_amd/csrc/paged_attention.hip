@@ -30,7 +30,7 @@ namespace {
 
 constexpr int kGenMaxG = 16;
 constexpr int kGenMaxDh = 128;
-constexpr int kGenOut = kGenMaxG * kGenMaxDh / 64;  // outputs per lane
+constexpr int kGenDimsPerLane = kGenMaxDh / 64;  // lane owns dims lane, lane + 64
 
 struct GenericArgs {
   const void *q;
@@ -52,13 +52,18 @@ struct GenericArgs {
   void *out;
   int64_t o_rs, o_hs;
   float *ws_m, *ws_l, *ws_acc;
+  int32_t vec_rows;  // K/V rows are 16-byte aligned and head_dim is a multiple of 16 bytes
 };
 
+// Lane t of the wave scores key t0 + t against the G query heads (K row read
+// with 16-byte loads when aligned); for P.V, lane d accumulates dims d and
+// d + 64 of all G heads, so each V element is loaded once per key.
+// Tokens past the valid range keep a zero row offset: with j < n their V row
+// is never loaded.
 template <typename T>
 __global__ __launch_bounds__(64) void attn_generic_kernel(GenericArgs a) {
   __shared__ float q_s[kGenMaxG][kGenMaxDh];
-  __shared__ float p_s[kGenMaxG][64];
-  __shared__ int64_t row_s[64];
+  constexpr int V = Vec<T>::N;
 
   const int lane = threadIdx.x;
   const int slot = blockIdx.x / a.max_splits;
@@ -102,9 +107,11 @@ __global__ __launch_bounds__(64) void attn_generic_kernel(GenericArgs a) {
     q_s[g][d] = to_float(q[(int64_t)row * a.q_rs + (int64_t)(kvh * G + g) * a.q_hs + d]);
   }
 
-  float acc[kGenOut];
+  float acc[kGenMaxG][kGenDimsPerLane];
 #pragma unroll
-  for (int k = 0; k < kGenOut; ++k) acc[k] = 0.f;
+  for (int g = 0; g < kGenMaxG; ++g)
+#pragma unroll
+    for (int i = 0; i < kGenDimsPerLane; ++i) acc[g][i] = 0.f;
   float m[kGenMaxG], l[kGenMaxG];
 #pragma unroll
   for (int g = 0; g < kGenMaxG; ++g) {
@@ -125,72 +132,97 @@ __global__ __launch_bounds__(64) void attn_generic_kernel(GenericArgs a) {
       rb = a.pool.layer_base + blk * a.pool.block_stride + (int64_t)kvh * a.pool.head_stride +
            (int64_t)(t % BS) * DH;
     }
-    row_s[lane] = rb;
     float s[kGenMaxG];
 #pragma unroll
     for (int g = 0; g < kGenMaxG; ++g) s[g] = 0.f;
     if (valid) {
-      for (int d = 0; d < DH; ++d) {
-        const float kv = to_float(kc[rb + d]);
+      if (a.vec_rows) {
+        for (int d = 0; d < DH; d += V) {
+          float kv[V];
+          unpack<T>(ld16(kc + rb + d), kv);
 #pragma unroll
-        for (int g = 0; g < kGenMaxG; ++g)
-          if (g < G) s[g] += q_s[g][d] * kv;
+          for (int g = 0; g < kGenMaxG; ++g)
+            if (g < G) {
+#pragma unroll
+              for (int i = 0; i < V; ++i) s[g] += q_s[g][d + i] * kv[i];
+            }
+        }
+      } else {
+        for (int d = 0; d < DH; ++d) {
+          const float kv = to_float(kc[rb + d]);
+#pragma unroll
+          for (int g = 0; g < kGenMaxG; ++g)
+            if (g < G) s[g] += q_s[g][d] * kv;
+        }
       }
     }
+    float pv[kGenMaxG];
 #pragma unroll
     for (int g = 0; g < kGenMaxG; ++g) {
+      pv[g] = 0.f;
       if (g < G) {
         const float sv = valid ? s[g] * a.scale_log2 : -INFINITY;
         const float mt = wave_max(sv);
         const float mn = fmaxf(m[g], mt);
         const float alpha = fast_exp2(m[g] - mn);
-        const float pv = fast_exp2(sv - mn);
-        l[g] = l[g] * alpha + wave_sum(pv);
+        pv[g] = fast_exp2(sv - mn);
+        l[g] = l[g] * alpha + wave_sum(pv[g]);
         m[g] = mn;
-        p_s[g][lane] = pv;
 #pragma unroll
-        for (int k = 0; k < kGenOut; ++k)
-          if ((lane + 64 * k) / DH == g) acc[k] *= alpha;
+        for (int i = 0; i < kGenDimsPerLane; ++i) acc[g][i] *= alpha;
       }
     }
-    __syncthreads();
+    // P.V: token j's row address and probabilities come from lane j by
+    // readlane (no LDS round trip); 8 tokens' V loads are in flight at once.
     const int n = min(64, t_end - t0);
-    for (int j = 0; j < n; ++j) {
-      const int64_t vb = row_s[j];
+    const uint32_t rb_lo = static_cast<uint32_t>(rb);
+    const uint32_t rb_hi = static_cast<uint32_t>(rb >> 32);
+    for (int j0 = 0; j0 < n; j0 += 8) {
+      float v[8][kGenDimsPerLane];
 #pragma unroll
-      for (int k = 0; k < kGenOut; ++k) {
-        const int idx = lane + 64 * k;
-        if (idx < G * DH) {
-          const int g = idx / DH, d = idx % DH;
-          acc[k] += p_s[g][j] * to_float(vc[vb + d]);
+      for (int u = 0; u < 8; ++u) {
+        const int j = j0 + u;
+        const int64_t vb = (int64_t)(((uint64_t)__builtin_amdgcn_readlane(rb_hi, j) << 32) |
+                                     __builtin_amdgcn_readlane(rb_lo, j));
+#pragma unroll
+        for (int i = 0; i < kGenDimsPerLane; ++i) {
+          const int d = lane + 64 * i;
+          v[u][i] = (j < n && d < DH) ? to_float(vc[vb + d]) : 0.f;
         }
       }
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int j = j0 + u;
+        if (j >= n) break;
+#pragma unroll
+        for (int g = 0; g < kGenMaxG; ++g)
+          if (g < G) {
+            const float p = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pv[g]), j));
+#pragma unroll
+            for (int i = 0; i < kGenDimsPerLane; ++i) acc[g][i] += p * v[u][i];
+          }
+      }
     }
-    __syncthreads();
   }
 
 #pragma unroll
-  for (int k = 0; k < kGenOut; ++k) {
-    const int idx = lane + 64 * k;
-    if (idx >= G * DH) continue;
-    const int g = idx / DH, d = idx % DH;
+  for (int g = 0; g < kGenMaxG; ++g) {
+    if (g >= G) continue;
     const int qh = kvh * G + g;
-    float lg = 0.f, mg = 0.f;
 #pragma unroll
-    for (int gg = 0; gg < kGenMaxG; ++gg)
-      if (gg == g) {
-        lg = l[gg];
-        mg = m[gg];
+    for (int i = 0; i < kGenDimsPerLane; ++i) {
+      const int d = lane + 64 * i;
+      if (d >= DH) continue;
+      if (a.max_splits == 1) {
+        out[(int64_t)row * a.o_rs + (int64_t)qh * a.o_hs + d] = from_float<T>(acc[g][i] / l[g]);
+      } else {
+        const int64_t w = ((int64_t)row * a.num_q_heads + qh) * a.max_splits + split;
+        if (d == 0) {
+          a.ws_m[w] = m[g];
+          a.ws_l[w] = l[g];
+        }
+        a.ws_acc[w * DH + d] = acc[g][i];
       }
-    if (a.max_splits == 1) {
-      out[(int64_t)row * a.o_rs + (int64_t)qh * a.o_hs + d] = from_float<T>(acc[k] / lg);
-    } else {
-      const int64_t w = ((int64_t)row * a.num_q_heads + qh) * a.max_splits + split;
-      if (d == 0) {
-        a.ws_m[w] = mg;
-        a.ws_l[w] = lg;
-      }
-      a.ws_acc[w * DH + d] = acc[k];
     }
   }
 }
@@ -289,6 +321,11 @@ int32_t launch_generic(const GenericArgs &a, int32_t rows, int32_t num_kv_heads,
   return check_launch();
 }
 
+// K/V rows can be read 16 bytes at a time: pools aligned, rows a multiple of 16 bytes.
+int32_t vec_rows_ok(const void *kc, const void *vc, int32_t head_dim, int elem) {
+  return aligned16(kc) && aligned16(vc) && (head_dim * elem) % 16 == 0;
+}
+
 bool mfma_eligible(int32_t dtype, int32_t block_size, int32_t head_dim, int32_t G,
                    const void *q, int64_t q_ss, int64_t q_hs, const void *kc, const void *vc,
                    const void *out, int64_t o_ss, int64_t o_hs) {
@@ -367,7 +404,8 @@ extern "C" int32_t tks_paged_attention_decode(
     GenericArgs a{query,     q_seq_stride, q_head_stride, key_cache, value_cache, pool,
                   block_tables, block_table_stride, seq_lens, seq_order, nullptr, num_seqs, num_q_heads,
                   G,         scale_log2,   pps,           max_splits, key_cap,  out,
-                  out_seq_stride, out_head_stride, w.m,   w.l,        w.acc};
+                  out_seq_stride, out_head_stride, w.m,   w.l,        w.acc,
+                  vec_rows_ok(key_cache, value_cache, head_dim, elem_bytes(dtype))};
     switch (dtype) {
       case TKS_FLOAT32: st = launch_generic<float>(a, num_seqs, num_kv_heads, s); break;
       case TKS_FLOAT16: st = launch_generic<_Float16>(a, num_seqs, num_kv_heads, s); break;
@@ -430,7 +468,8 @@ extern "C" int32_t tks_paged_attention_prefill(
   GenericArgs a{query,     q_token_stride, q_head_stride, key_cache,  value_cache, pool,
                 block_tables, block_table_stride, seq_lens, nullptr, cu_seqlens_q, num_seqs, num_q_heads,
                 G,         scale_log2,     pps,           1,          key_cap,     out,         out_token_stride,
-                out_head_stride, nullptr,  nullptr,       nullptr};
+                out_head_stride, nullptr,  nullptr,       nullptr,
+                vec_rows_ok(key_cache, value_cache, head_dim, elem_bytes(dtype))};
   const int32_t rows = static_cast<int32_t>(num_tokens);
   switch (dtype) {
     case TKS_FLOAT32: return launch_generic<float>(a, rows, num_kv_heads, s);
