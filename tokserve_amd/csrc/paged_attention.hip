@@ -9,7 +9,8 @@
 // Decode (one query per sequence) goes to decode_mfma_kernel (decode_mfma.hip)
 // for bf16/fp16 with block size 16 and Dh 64/128; every other shape and fp32
 // (where 1e-5 parity wants fp32 products) uses attn_generic_kernel below:
-// one wave per (query row, KV head, split), 64 keys per step on the VALU. The
+// one 4-wave workgroup per (query row, KV head, split), 64 keys per wave step
+// on the VALU. The
 // generic kernel is also the ragged chunked-prefill path (one row per query
 // token, causal key length).
 //
@@ -25,12 +26,13 @@ namespace tks {
 namespace {
 
 // ------------------------------------------------------------------------
-// Generic kernel (VALU), one wave per (row, KV head, split)
+// Generic kernel (VALU), one 4-wave workgroup per (row, KV head, split)
 // ------------------------------------------------------------------------
 
 constexpr int kGenMaxG = 16;
 constexpr int kGenMaxDh = 128;
-constexpr int kGenDimsPerLane = kGenMaxDh / 64;  // lane owns dims lane, lane + 64
+constexpr int kGenWaves = 4;
+constexpr int kGenThreads = 64 * kGenWaves;
 
 struct GenericArgs {
   const void *q;
@@ -55,17 +57,31 @@ struct GenericArgs {
   int32_t vec_rows;  // K/V rows are 16-byte aligned and head_dim is a multiple of 16 bytes
 };
 
-// Lane t of the wave scores key t0 + t against the G query heads (K row read
-// with 16-byte loads when aligned); for P.V, lane d accumulates dims d and
-// d + 64 of all G heads, so each V element is loaded once per key.
-// Tokens past the valid range keep a zero row offset: with j < n their V row
-// is never loaded.
-template <typename T>
-__global__ __launch_bounds__(64) void attn_generic_kernel(GenericArgs a) {
-  __shared__ float q_s[kGenMaxG][kGenMaxDh];
+// The split's keys are dealt to the four waves 64 at a time (wave w takes keys
+// t_begin + 64 w + 256 i). In a step, lane t scores key t0 + t against the G
+// query heads, and every K and V element the step needs is requested before
+// the first is used, so a step costs about one memory latency. For P.V lane d
+// accumulates dims d and d + 64 of all G heads; token j's row offset and
+// probabilities are written to LDS by lane j and read back by all lanes as
+// broadcasts (cheaper than a readlane, whose SGPR result stalls the next VALU
+// use). Lanes past the valid range keep
+// a zero row offset (an in-bounds read whose score is masked and whose V is
+// zeroed). The waves' (m, l, acc) are combined through LDS at the end.
+// DHMAX (64 or 128) bounds head_dim; dims past head_dim are zero in q and K.
+template <typename T, int DHMAX>
+__global__ __launch_bounds__(kGenThreads) void attn_generic_kernel(GenericArgs a) {
   constexpr int V = Vec<T>::N;
+  constexpr int DPL = DHMAX / 64;  // dims per lane in P.V
+  __shared__ __align__(16) float q_s[kGenMaxG][DHMAX];
+  __shared__ float part_m[kGenWaves][kGenMaxG];
+  __shared__ float part_l[kGenWaves][kGenMaxG];
+  __shared__ __align__(16) float part_acc[kGenWaves][kGenMaxG][DHMAX];
+  __shared__ __align__(16) int64_t rb_s[kGenWaves][64];  // a wave's row offsets, read back as broadcasts
+  __shared__ __align__(16) float p_s[kGenWaves][kGenMaxG][64];  // a wave's probabilities, likewise
 
-  const int lane = threadIdx.x;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
   const int slot = blockIdx.x / a.max_splits;
   const int split = blockIdx.x - slot * a.max_splits;
   const int row = a.seq_order ? min(max(a.seq_order[slot], 0), a.num_seqs - 1) : slot;
@@ -95,73 +111,99 @@ __global__ __launch_bounds__(64) void attn_generic_kernel(GenericArgs a) {
   const int t_begin = split * tok_per_split;
   if (t_begin >= kv_len) {
     if (split == 0)
-      for (int i = lane; i < G * DH; i += 64)
+      for (int i = tid; i < G * DH; i += kGenThreads)
         out[(int64_t)row * a.o_rs + (int64_t)(kvh * G + i / DH) * a.o_hs + i % DH] =
             from_float<T>(0.f);
     return;
   }
   const int t_end = min(kv_len, t_begin + tok_per_split);
 
-  for (int i = lane; i < G * DH; i += 64) {
-    const int g = i / DH, d = i % DH;
-    q_s[g][d] = to_float(q[(int64_t)row * a.q_rs + (int64_t)(kvh * G + g) * a.q_hs + d]);
+  const T *kc = static_cast<const T *>(a.kc);
+  const T *vc = static_cast<const T *>(a.vc);
+  const int32_t *bt_row = a.bt + (int64_t)seq * a.bt_stride;
+
+  // Row offset of key t0 + lane (0 past the step's range) and the step's K row
+  // and V columns; the first step is requested before q is staged.
+  auto row_offset = [&](int t0) -> int64_t {
+    const int t = t0 + lane;
+    if (t >= t_end) return 0;
+    const int64_t blk = block_of(bt_row, t / BS, a.pool.num_blocks);
+    return a.pool.layer_base + blk * a.pool.block_stride + (int64_t)kvh * a.pool.head_stride +
+           (int64_t)(t % BS) * DH;
+  };
+  float kv[DHMAX];
+  float vv[64][DPL];
+  auto load_step = [&](int64_t rb, int n) {
+    if (a.vec_rows) {
+#pragma unroll
+      for (int d = 0; d < DHMAX; d += V) {
+        if (d < DH) {
+          unpack<T>(ld16(kc + rb + d), kv + d);
+        } else {
+#pragma unroll
+          for (int i = 0; i < V; ++i) kv[d + i] = 0.f;
+        }
+      }
+    } else {
+#pragma unroll
+      for (int d = 0; d < DHMAX; ++d) kv[d] = d < DH ? to_float(kc[rb + d]) : 0.f;
+    }
+    // LDS operations of one wave complete in order: the broadcast reads below
+    // see this write without a barrier.
+    rb_s[wave][lane] = rb;
+#pragma unroll
+    for (int u = 0; u < 64; ++u) {
+      const int64_t vb = rb_s[wave][u];
+#pragma unroll
+      for (int i = 0; i < DPL; ++i) {
+        const int d = lane + 64 * i;
+        const float x = d < DH ? to_float(vc[vb + d]) : 0.f;
+        vv[u][i] = u < n ? x : 0.f;
+      }
+    }
+  };
+  int t0 = t_begin + 64 * wave;
+  if (t0 < t_end) load_step(row_offset(t0), min(64, t_end - t0));
+
+  for (int i = tid; i < G * DHMAX; i += kGenThreads) {
+    const int g = i / DHMAX, d = i % DHMAX;
+    q_s[g][d] = d < DH ? to_float(q[(int64_t)row * a.q_rs + (int64_t)(kvh * G + g) * a.q_hs + d])
+                       : 0.f;
   }
 
-  float acc[kGenMaxG][kGenDimsPerLane];
-#pragma unroll
-  for (int g = 0; g < kGenMaxG; ++g)
-#pragma unroll
-    for (int i = 0; i < kGenDimsPerLane; ++i) acc[g][i] = 0.f;
+  float acc[kGenMaxG][DPL];
   float m[kGenMaxG], l[kGenMaxG];
 #pragma unroll
   for (int g = 0; g < kGenMaxG; ++g) {
     m[g] = -INFINITY;
     l[g] = 0.f;
+#pragma unroll
+    for (int i = 0; i < DPL; ++i) acc[g][i] = 0.f;
   }
-  const T *kc = static_cast<const T *>(a.kc);
-  const T *vc = static_cast<const T *>(a.vc);
-  const int32_t *bt_row = a.bt + (int64_t)seq * a.bt_stride;
   __syncthreads();
 
-  for (int t0 = t_begin; t0 < t_end; t0 += 64) {
-    const int t = t0 + lane;
-    const bool valid = t < t_end;
-    int64_t rb = 0;
-    if (valid) {
-      const int64_t blk = block_of(bt_row, t / BS, a.pool.num_blocks);
-      rb = a.pool.layer_base + blk * a.pool.block_stride + (int64_t)kvh * a.pool.head_stride +
-           (int64_t)(t % BS) * DH;
-    }
-    float s[kGenMaxG];
-#pragma unroll
-    for (int g = 0; g < kGenMaxG; ++g) s[g] = 0.f;
-    if (valid) {
-      if (a.vec_rows) {
-        for (int d = 0; d < DH; d += V) {
-          float kv[V];
-          unpack<T>(ld16(kc + rb + d), kv);
-#pragma unroll
-          for (int g = 0; g < kGenMaxG; ++g)
-            if (g < G) {
-#pragma unroll
-              for (int i = 0; i < V; ++i) s[g] += q_s[g][d + i] * kv[i];
-            }
-        }
-      } else {
-        for (int d = 0; d < DH; ++d) {
-          const float kv = to_float(kc[rb + d]);
-#pragma unroll
-          for (int g = 0; g < kGenMaxG; ++g)
-            if (g < G) s[g] += q_s[g][d] * kv;
-        }
-      }
-    }
+  for (; t0 < t_end; t0 += 64 * kGenWaves) {
+    const bool valid = t0 + lane < t_end;
+    // q_s is loop-invariant: an opaque zero offset keeps its (broadcast) reads
+    // inside the step instead of hoisted into G * DHMAX registers.
+    int q_off = 0;
+    asm volatile("" : "+v"(q_off));
+    const float4 *qrow = reinterpret_cast<const float4 *>(&q_s[0][0]) + q_off;
     float pv[kGenMaxG];
 #pragma unroll
     for (int g = 0; g < kGenMaxG; ++g) {
       pv[g] = 0.f;
       if (g < G) {
-        const float sv = valid ? s[g] * a.scale_log2 : -INFINITY;
+        float s = 0.f;
+#pragma unroll
+        for (int d = 0; d < DHMAX; d += 4) {
+          const float4 qd = qrow[(g * DHMAX + d) / 4];
+          s += qd.x * kv[d];
+          s += qd.y * kv[d + 1];
+          s += qd.z * kv[d + 2];
+          s += qd.w * kv[d + 3];
+        }
+        const float sv = valid ? s * a.scale_log2 : -INFINITY;
         const float mt = wave_max(sv);
         const float mn = fmaxf(m[g], mt);
         const float alpha = fast_exp2(m[g] - mn);
@@ -169,60 +211,61 @@ __global__ __launch_bounds__(64) void attn_generic_kernel(GenericArgs a) {
         l[g] = l[g] * alpha + wave_sum(pv[g]);
         m[g] = mn;
 #pragma unroll
-        for (int i = 0; i < kGenDimsPerLane; ++i) acc[g][i] *= alpha;
+        for (int i = 0; i < DPL; ++i) acc[g][i] *= alpha;
       }
     }
-    // P.V: token j's row address and probabilities come from lane j by
-    // readlane (no LDS round trip); 8 tokens' V loads are in flight at once.
-    const int n = min(64, t_end - t0);
-    const uint32_t rb_lo = static_cast<uint32_t>(rb);
-    const uint32_t rb_hi = static_cast<uint32_t>(rb >> 32);
-    for (int j0 = 0; j0 < n; j0 += 8) {
-      float v[8][kGenDimsPerLane];
 #pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        const int j = j0 + u;
-        const int64_t vb = (int64_t)(((uint64_t)__builtin_amdgcn_readlane(rb_hi, j) << 32) |
-                                     __builtin_amdgcn_readlane(rb_lo, j));
+    for (int g = 0; g < kGenMaxG; ++g)
+      if (g < G) p_s[wave][g][lane] = pv[g];
 #pragma unroll
-        for (int i = 0; i < kGenDimsPerLane; ++i) {
-          const int d = lane + 64 * i;
-          v[u][i] = (j < n && d < DH) ? to_float(vc[vb + d]) : 0.f;
+    for (int g = 0; g < kGenMaxG; ++g)
+      if (g < G) {
+#pragma unroll
+        for (int u = 0; u < 64; ++u) {
+          const float p = p_s[wave][g][u];
+#pragma unroll
+          for (int i = 0; i < DPL; ++i) acc[g][i] += p * vv[u][i];
         }
       }
-#pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        const int j = j0 + u;
-        if (j >= n) break;
-#pragma unroll
-        for (int g = 0; g < kGenMaxG; ++g)
-          if (g < G) {
-            const float p = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pv[g]), j));
-#pragma unroll
-            for (int i = 0; i < kGenDimsPerLane; ++i) acc[g][i] += p * v[u][i];
-          }
-      }
-    }
+    const int t_next = t0 + 64 * kGenWaves;
+    if (t_next < t_end) load_step(row_offset(t_next), min(64, t_end - t_next));
   }
 
 #pragma unroll
-  for (int g = 0; g < kGenMaxG; ++g) {
-    if (g >= G) continue;
-    const int qh = kvh * G + g;
-#pragma unroll
-    for (int i = 0; i < kGenDimsPerLane; ++i) {
-      const int d = lane + 64 * i;
-      if (d >= DH) continue;
-      if (a.max_splits == 1) {
-        out[(int64_t)row * a.o_rs + (int64_t)qh * a.o_hs + d] = from_float<T>(acc[g][i] / l[g]);
-      } else {
-        const int64_t w = ((int64_t)row * a.num_q_heads + qh) * a.max_splits + split;
-        if (d == 0) {
-          a.ws_m[w] = m[g];
-          a.ws_l[w] = l[g];
-        }
-        a.ws_acc[w * DH + d] = acc[g][i];
+  for (int g = 0; g < kGenMaxG; ++g)
+    if (g < G) {
+      if (lane == 0) {
+        part_m[wave][g] = m[g];
+        part_l[wave][g] = l[g];
       }
+#pragma unroll
+      for (int i = 0; i < DPL; ++i) part_acc[wave][g][lane + 64 * i] = acc[g][i];
+    }
+  __syncthreads();
+  // Wave 0 always has keys, so the maximum is finite for finite scores and a
+  // wave without keys (m = -inf, l = 0, acc = 0) contributes nothing.
+  for (int i = tid; i < G * DH; i += kGenThreads) {
+    const int g = i / DH, d = i % DH;
+    float mx = part_m[0][g];
+#pragma unroll
+    for (int w = 1; w < kGenWaves; ++w) mx = fmaxf(mx, part_m[w][g]);
+    float lsum = 0.f, o = 0.f;
+#pragma unroll
+    for (int w = 0; w < kGenWaves; ++w) {
+      const float f = fast_exp2(part_m[w][g] - mx);
+      lsum += part_l[w][g] * f;
+      o += part_acc[w][g][d] * f;
+    }
+    const int qh = kvh * G + g;
+    if (a.max_splits == 1) {
+      out[(int64_t)row * a.o_rs + (int64_t)qh * a.o_hs + d] = from_float<T>(o / lsum);
+    } else {
+      const int64_t w = ((int64_t)row * a.num_q_heads + qh) * a.max_splits + split;
+      if (d == 0) {
+        a.ws_m[w] = mx;
+        a.ws_l[w] = lsum;
+      }
+      a.ws_acc[w * DH + d] = o;
     }
   }
 }
@@ -317,7 +360,10 @@ int32_t launch_generic(const GenericArgs &a, int32_t rows, int32_t num_kv_heads,
                        hipStream_t s) {
   const dim3 grid(static_cast<unsigned>(static_cast<int64_t>(rows) * a.max_splits),
                   num_kv_heads);
-  attn_generic_kernel<T><<<grid, 64, 0, s>>>(a);
+  if (a.pool.head_dim <= 64)
+    attn_generic_kernel<T, 64><<<grid, kGenThreads, 0, s>>>(a);
+  else
+    attn_generic_kernel<T, 128><<<grid, kGenThreads, 0, s>>>(a);
   return check_launch();
 }
 
