@@ -19,8 +19,11 @@ Modules
               gather), bit-exact by construction.
   fp64        float64 NumPy closed forms (textbook attention, RoPE, RMSNorm)
               used to pin the torch-path restatement independently.
-  host        allocator / block-table / scheduler semantics restated in plain
-              Python for the continuous-batching engine's known answers.
+  model       the torch-backend Llama forward from a state dict, with a
+              contiguous per-sequence K/V cache (greedy-token identity).
+  engine      the reference's continuous-batching loop (FIFO admission under
+              slot and block reservations, per-request prefill then decode,
+              lowest-id block allocation) driving `model`.
 
 Each function cites the reference file:line it follows (paths relative to the
 reference repository root). Pinning: tests/test_oracle_pins.py checks every
