@@ -82,6 +82,13 @@ struct Vec {
 
 // 16-byte vector load/store as four dwords.
 __device__ __forceinline__ uint4 ld16(const void *p) { return *reinterpret_cast<const uint4 *>(p); }
+// Non-temporal 16-byte load (cache lines marked stream-once) for data read
+// exactly once per launch, such as K/V pages in decode.
+__device__ __forceinline__ uint4 ld16_stream(const void *p) {
+  typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+  const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(p));
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
 __device__ __forceinline__ void st16(void *p, uint4 v) { *reinterpret_cast<uint4 *>(p) = v; }
 
 // Unpack the 16-byte vector `v` of T into floats.

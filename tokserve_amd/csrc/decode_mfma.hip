@@ -118,9 +118,9 @@ __global__ __launch_bounds__(64 * kWaves) void decode_mfma_kernel(DecodeArgs a) 
     const T *kp = kc + blk * a.pool.block_stride + k_off;
     const T *vp = vc + blk * a.pool.block_stride + v_off;
 #pragma unroll
-    for (int c = 0; c < NC; ++c) kr[c] = ld16(kp + c * 32);
+    for (int c = 0; c < NC; ++c) kr[c] = ld16_stream(kp + c * 32);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) vr[j] = ld16(vp + j * DH);
+    for (int j = 0; j < 4; ++j) vr[j] = ld16_stream(vp + j * DH);
   };
 
   auto consume = [&](const uint4 (&kr)[NC], const uint4 (&vr)[4], int p) {
