@@ -113,6 +113,7 @@ __global__ __launch_bounds__(64 * kWaves) void decode_mfma_kernel(DecodeArgs a) 
     l[i] = 0.f;
   }
 
+  // Every page is read once: non-temporal loads.
   auto load_page = [&](int blk_reg, int idx, uint4 (&kr)[NC], uint4 (&vr)[4]) {
     const int64_t blk = clamp_block(__builtin_amdgcn_readlane(blk_reg, idx), a.pool.num_blocks);
     const T *kp = kc + blk * a.pool.block_stride + k_off;
@@ -159,21 +160,28 @@ __global__ __launch_bounds__(64 * kWaves) void decode_mfma_kernel(DecodeArgs a) 
     wave_lds_sync();
   };
 
-  // The prefetch is unconditional (past the end it re-reads the chunk's last
-  // page, an L2 hit) so that every consume has exactly one page of loads issued
-  // after its own and the wait before it covers only its own data.
+  // Two register pages in flight: the steady-state loop always has the next
+  // page's loads issued behind the page being consumed (straight-line, so the
+  // wait before each consume covers only its own page); the last one or two
+  // pages of a 64-page chunk drain in the epilogue.
   for (int c0 = w_begin; c0 < w_end; c0 += 64) {
-    const int c1 = min(w_end, c0 + 64);
-    const int last = c1 - 1 - c0;
-    const int blk_reg = lane < c1 - c0 ? bt_row[c0 + lane] : 0;
+    const int n = min(w_end, c0 + 64) - c0;
+    const int blk_reg = lane < n ? bt_row[c0 + lane] : 0;
     uint4 kA[NC], vA[4], kB[NC], vB[4];
     load_page(blk_reg, 0, kA, vA);
-    for (int p = c0; p < c1; p += 2) {
-      load_page(blk_reg, min(p + 1 - c0, last), kB, vB);
-      consume(kA, vA, p);
-      if (p + 1 >= c1) break;
-      load_page(blk_reg, min(p + 2 - c0, last), kA, vA);
-      consume(kB, vB, p + 1);
+    int i = 0;
+    for (; i + 2 < n; i += 2) {
+      load_page(blk_reg, i + 1, kB, vB);
+      consume(kA, vA, c0 + i);
+      load_page(blk_reg, i + 2, kA, vA);
+      consume(kB, vB, c0 + i + 1);
+    }
+    if (i + 1 < n) {
+      load_page(blk_reg, i + 1, kB, vB);
+      consume(kA, vA, c0 + i);
+      consume(kB, vB, c0 + i + 1);
+    } else {
+      consume(kA, vA, c0 + i);
     }
   }
 
