@@ -39,6 +39,7 @@ enum tks_dtype {
   TKS_FLOAT32 = 0,
   TKS_FLOAT16 = 1,
   TKS_BFLOAT16 = 2,
+  TKS_FLOAT8_E4M3 = 3, /* OCP e4m3fn (torch.float8_e4m3fn); K/V pools of the *_fp8 entries only */
 };
 
 /* Status codes. Values are part of the ABI. */
@@ -109,7 +110,7 @@ int32_t tks_paged_gather(const void *key_cache, const void *value_cache, int32_t
  *   out = softmax(scale * q.K^T) V, accumulated in fp32, stored in `dtype`.
  * max_seq_len (host) bounds every seq_lens[b] and sizes the grid.
  * pages_per_split: KV blocks per workgroup along the keys (0 = library
- * heuristic: a whole sequence per workgroup when the batch has at least 1024
+ * heuristic: a whole sequence per workgroup when the batch has at least 256
  * (sequence, KV head) pairs, otherwise split so the GPU fills). When some
  * sequence spans more than one split, the partials go to the workspace and a
  * second kernel merges them; the workspace size comes from
@@ -168,6 +169,59 @@ int32_t tks_paged_attention_prefill(const void *query, int64_t q_token_stride,
                                     int32_t max_seq_len, float scale, void *out,
                                     int64_t out_token_stride, int64_t out_head_stride,
                                     int32_t dtype, tks_stream_t stream);
+
+/* ------------------------------------------------------------------------
+ * fp8 K/V pools (a pool-layout variant behind PagedKVStorage,
+ * tokserve/engine/paged/storage.py:40-56, where the reference has only pools in
+ * the model dtype). Same layout [L, NB, Hkv, BS, Dh], elements OCP e4m3fn with
+ * one fp32 scale per pool (k_scale, v_scale > 0):
+ *   stored  = e4m3(clamp(x / scale, -448, 448))   round to nearest even, NaN kept
+ *   decoded = float(stored) * scale
+ * Each entry takes the arguments of its counterpart above plus the two scales;
+ * `dtype` is the type of the non-pool tensors (the new K/V rows, the gathered
+ * rows, the query and the output). Attention computes exactly the function of
+ * its counterpart on the decoded pools, in fp32, with the scales applied as
+ * factors on the scores and on the output.
+ */
+/* KV append with quantization (tks_kv_append on fp8 pools). */
+int32_t tks_kv_append_fp8(const void *key, int64_t key_token_stride, int64_t key_head_stride,
+                          const void *value, int64_t value_token_stride,
+                          int64_t value_head_stride, int64_t num_tokens, void *key_cache,
+                          void *value_cache, int32_t num_layers, int64_t num_blocks,
+                          int32_t num_kv_heads, int32_t block_size, int32_t head_dim,
+                          int32_t layer_index, const int64_t *slot_mapping, float k_scale,
+                          float v_scale, int32_t dtype, tks_stream_t stream);
+
+/* Block-table gather with decoding into `dtype` (tks_paged_gather on fp8 pools). */
+int32_t tks_paged_gather_fp8(const void *key_cache, const void *value_cache, int32_t num_layers,
+                             int64_t num_blocks, int32_t num_kv_heads, int32_t block_size,
+                             int32_t head_dim, int32_t layer_index, const int32_t *block_tables,
+                             int32_t block_table_stride, const int32_t *seq_lens,
+                             const int32_t *cu_seqlens, int32_t num_seqs, int32_t max_seq_len,
+                             void *key_out, void *value_out, int64_t out_token_stride,
+                             int64_t out_head_stride, float k_scale, float v_scale,
+                             int32_t dtype, tks_stream_t stream);
+
+/* Decode attention over fp8 pools (tks_paged_attention_decode; same workspace size). */
+int32_t tks_paged_attention_decode_fp8(
+    const void *query, int64_t q_seq_stride, int64_t q_head_stride, const void *key_cache,
+    const void *value_cache, int32_t num_layers, int64_t num_blocks, int32_t num_kv_heads,
+    int32_t block_size, int32_t head_dim, int32_t layer_index, const int32_t *block_tables,
+    int32_t block_table_stride, const int32_t *seq_lens, const int32_t *seq_order,
+    int32_t num_seqs, int32_t num_q_heads, int32_t max_seq_len, float scale,
+    int32_t pages_per_split, void *out, int64_t out_seq_stride, int64_t out_head_stride,
+    void *workspace, int64_t workspace_bytes, float k_scale, float v_scale, int32_t dtype,
+    tks_stream_t stream);
+
+/* Chunked-prefill attention over fp8 pools (tks_paged_attention_prefill). */
+int32_t tks_paged_attention_prefill_fp8(
+    const void *query, int64_t q_token_stride, int64_t q_head_stride, const void *key_cache,
+    const void *value_cache, int32_t num_layers, int64_t num_blocks, int32_t num_kv_heads,
+    int32_t block_size, int32_t head_dim, int32_t layer_index, const int32_t *block_tables,
+    int32_t block_table_stride, const int32_t *seq_lens, const int32_t *cu_seqlens_q,
+    int32_t num_seqs, int64_t num_tokens, int32_t num_q_heads, int32_t max_query_len,
+    int32_t max_seq_len, float scale, void *out, int64_t out_token_stride,
+    int64_t out_head_stride, float k_scale, float v_scale, int32_t dtype, tks_stream_t stream);
 
 /* ------------------------------------------------------------------------
  * RMSNorm over the last dimension.

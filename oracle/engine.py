@@ -50,8 +50,10 @@ class Record:
 
 class Engine:
     def __init__(self, state: dict[str, torch.Tensor], config: dict, *, num_blocks: int,
-                 block_size: int, max_running: int) -> None:
+                 block_size: int, max_running: int,
+                 kv_quant: tuple[float, float] | None = None) -> None:
         self.state, self.config = state, config
+        self.kv_quant = kv_quant
         self.block_size, self.num_blocks, self.max_running = block_size, num_blocks, max_running
         self.free = list(range(num_blocks))
         self.waiting: list[Request] = []
@@ -74,7 +76,7 @@ class Engine:
 
     def _next_token(self, request: Request, tokens: list[int]) -> int:
         ids = torch.tensor([tokens], dtype=torch.int64)
-        logits = oracle_model.forward(self.state, self.config, ids, request.kv)
+        logits = oracle_model.forward(self.state, self.config, ids, request.kv, self.kv_quant)
         return int(torch.argmax(logits[0, -1]))
 
     def _append(self, request: Request, token: int) -> None:

@@ -1,8 +1,9 @@
-"""ctypes binding of oracle/kvslots.c (TEST INFRASTRUCTURE ONLY).
+"""ctypes binding of oracle/kvslots.c and oracle/e4m3.c (TEST INFRASTRUCTURE ONLY).
 
 Bit-exact CPU restatement of slot mapping, KV append and block-table gather
 (tokserve/engine/paged/block_table.py:53-67, storage.py:64-116,
-sequence_cache.py:86-193). Operates on contiguous CPU tensors.
+sequence_cache.py:86-193), and of the OCP fp8 e4m3 encoding of fp8 pools.
+Operates on contiguous CPU tensors.
 """
 
 from __future__ import annotations
@@ -47,6 +48,10 @@ def _load() -> ctypes.CDLL:
         lib.oracle_paged_gather.argtypes = [
             _p, _p, _i64, _i32, _i32, _i32, _i32, _p, _i32, _p, _p, _i32, _p, _p, _i64, _i64, _i32,
         ]
+        lib.oracle_e4m3_encode_array.restype = None
+        lib.oracle_e4m3_encode_array.argtypes = [_p, _i64, ctypes.c_float, _p]
+        lib.oracle_e4m3_decode_array.restype = None
+        lib.oracle_e4m3_decode_array.argtypes = [_p, _i64, _p]
         _lib = lib
     return _lib
 
@@ -133,3 +138,23 @@ def paged_gather(
     if status != 0:
         raise IndexError("position exceeds block table capacity")
     return key_out, value_out
+
+
+def e4m3_encode(x: torch.Tensor, scale: float = 1.0) -> torch.Tensor:
+    """uint8 codes of e4m3(clamp(x / scale, -448, 448)) (x as float32), from e4m3.c."""
+
+    _cpu(x)
+    values = x.to(torch.float32).contiguous()
+    out = torch.empty(values.shape, dtype=torch.uint8)
+    _load().oracle_e4m3_encode_array(values.data_ptr(), values.numel(), scale, out.data_ptr())
+    return out
+
+
+def e4m3_decode(codes: torch.Tensor) -> torch.Tensor:
+    """float32 values of uint8 e4m3 codes, from e4m3.c."""
+
+    _cpu(codes)
+    codes = codes.to(torch.uint8).contiguous()
+    out = torch.empty(codes.shape, dtype=torch.float32)
+    _load().oracle_e4m3_decode_array(codes.data_ptr(), codes.numel(), out.data_ptr())
+    return out

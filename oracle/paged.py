@@ -122,3 +122,20 @@ def prefill_batch(
         )
         out[q0:q1] = o[0].permute(1, 0, 2)
     return out
+
+
+# fp8 pools (the build's pool variant; the reference keeps pools in the model
+# dtype, tokserve/engine/paged/storage.py:40-56). One fp32 scale per pool.
+FP8_MAX = 448.0
+
+
+def quantize_e4m3(x: torch.Tensor, scale: float) -> torch.Tensor:
+    """e4m3(clamp(x / scale, -448, 448)) as torch.float8_e4m3fn (round to nearest even)."""
+
+    return (x.to(torch.float32) / scale).clamp(-FP8_MAX, FP8_MAX).to(torch.float8_e4m3fn)
+
+
+def dequantize_e4m3(codes: torch.Tensor, scale: float, dtype: torch.dtype) -> torch.Tensor:
+    """float(code) * scale in fp32, rounded once to dtype."""
+
+    return (codes.to(torch.float32) * scale).to(dtype)

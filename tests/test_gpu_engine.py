@@ -36,12 +36,14 @@ def _fixture_model(device) -> LlamaModel:
     return model.to(device).eval()
 
 
-def _manager(model, device, *, num_blocks, block_size, dtype=torch.float32):
+def _manager(model, device, *, num_blocks, block_size, dtype=torch.float32, kv_dtype=None,
+             scales=(1.0, 1.0)):
     config = model.config
     return PagedKVCacheManager(num_layers=config.num_hidden_layers, num_blocks=num_blocks,
                                num_key_value_heads=config.num_key_value_heads,
                                block_size=block_size, head_dim=config.head_dim, device=device,
-                               dtype=dtype)
+                               dtype=dtype, kv_dtype=kv_dtype, k_scale=scales[0],
+                               v_scale=scales[1])
 
 
 def test_model_reproduces_reference_fixture(device) -> None:
@@ -76,9 +78,10 @@ def test_full_recompute_and_paged_generation_agree(device) -> None:
     assert manager.allocator.allocated_count == 0
 
 
-def _run_both(model, device, specs, *, max_running, num_blocks, block_size):
+def _run_both(model, device, specs, *, max_running, num_blocks, block_size, kv_dtype=None,
+              scales=(1.0, 1.0)):
     manager = _manager(model, device, num_blocks=num_blocks, block_size=block_size,
-                       dtype=model.embed_tokens.weight.dtype)
+                       dtype=model.embed_tokens.weight.dtype, kv_dtype=kv_dtype, scales=scales)
     scheduler = RequestScheduler(max_running_requests=max_running, cache_manager=manager)
     engine = ContinuousBatchEngine(model, scheduler, manager)
     released = {}
@@ -92,7 +95,8 @@ def _run_both(model, device, specs, *, max_running, num_blocks, block_size):
     state = {k: v.detach().cpu() for k, v in model.state_dict().items()}
     config = {k: getattr(model.config, k) for k in FIXTURE["config"]}
     reference = oracle_engine.Engine(state, config, num_blocks=num_blocks, block_size=block_size,
-                                     max_running=max_running)
+                                     max_running=max_running,
+                                     kv_quant=None if kv_dtype is None else scales)
     for rid, prompt, n in specs:
         scheduler.submit(ScheduledRequest(rid, torch.tensor([prompt], device=device),
                                           GenerationConfig(max_new_tokens=n)))
@@ -193,3 +197,26 @@ def test_decode_graph_replays_match_eager_and_oracle(device) -> None:
         reference.submit(oracle_engine.Request(rid, list(prompt), n))
     reference.run()
     assert with_graphs == {rid: reference.finished[rid].generated for rid, _, _ in specs}
+
+
+@pytest.mark.parametrize("scales", [(1.0, 1.0), (0.25, 0.5)])
+def test_engine_fp8_kv_pools_fp32_tokens_identical(device, scales) -> None:
+    """fp8 e4m3 K/V pools under the fp32 fixture model: the engine's greedy tokens and
+    records equal the oracle engine whose K/V rows go through the same e4m3 rounding."""
+
+    g = torch.Generator().manual_seed(300)
+    specs = []
+    for i in range(10):
+        length = int(torch.randint(1, 24, (1,), generator=g))
+        prompt = torch.randint(0, 64, (length,), generator=g).tolist()
+        specs.append((f"f{i}", prompt, int(torch.randint(1, 9, (1,), generator=g))))
+    model = _fixture_model(device)
+    engine, _, manager, _, reference, expected = _run_both(
+        model, device, specs, max_running=4, num_blocks=24, block_size=4,
+        kv_dtype=torch.float8_e4m3fn, scales=scales)
+    assert manager.storage.key_storage.dtype == torch.float8_e4m3fn
+    assert [tuple(r.__dict__.values()) for r in engine.history] == \
+        [tuple(r.__dict__.values()) for r in expected]
+    for rid, _, _ in specs:
+        assert engine.scheduler.get_request(rid).result.generated_token_ids[0].tolist() == \
+            reference.finished[rid].generated, rid

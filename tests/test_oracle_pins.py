@@ -377,3 +377,76 @@ def test_greedy_first_index_on_ties_and_nan() -> None:
     logits = torch.tensor([[1.0, 3.0, 3.0, 2.0], [0.0, float("nan"), 5.0, float("nan")],
                            [-float("inf")] * 4])
     assert torch_path.select_greedy(logits).flatten().tolist() == [1, 1, 0]
+
+
+# --------------------------------------------------------------------------
+# fp8 (e4m3) pools: the torch restatement (oracle/paged.py) against the C
+# encoder written from the OCP format definition (oracle/e4m3.c) and against
+# hand-worked codes.
+
+
+def _e4m3_values() -> torch.Tensor:
+    codes = torch.arange(256, dtype=torch.int32).to(torch.uint8)
+    return codes.view(torch.float8_e4m3fn).float()
+
+
+def test_e4m3_decode_known_codes_and_table() -> None:
+    """All 256 codes decode alike in C and torch; hand-worked codes pin the format."""
+
+    codes = torch.arange(256, dtype=torch.int32).to(torch.uint8)
+    c = kvslots.e4m3_decode(codes)
+    t = _e4m3_values()
+    assert torch.equal(torch.isnan(c), torch.isnan(t))
+    assert torch.equal(c[~torch.isnan(c)], t[~torch.isnan(t)])
+    known = {0x00: 0.0, 0x01: 2.0 ** -9, 0x07: 7 * 2.0 ** -9, 0x08: 2.0 ** -6, 0x38: 1.0,
+             0x39: 1.125, 0x3F: 1.875, 0x40: 2.0, 0x7E: 448.0, 0xB8: -1.0, 0xFE: -448.0}
+    for code, value in known.items():
+        assert float(c[code]) == value, hex(code)
+    assert torch.isnan(c[0x7F]) and torch.isnan(c[0xFF])
+    assert int(torch.isnan(c).sum()) == 2
+
+
+def test_e4m3_encode_ties_saturation_and_nan_known_answers() -> None:
+    x = torch.tensor([1.0625, 1.1875, 2.0 ** -10, 3 * 2.0 ** -10, 464.0, 1e30, float("inf"),
+                      -float("inf"), -0.0, 0.0, 440.0, 432.0, float("nan"), 2.0 ** -6 - 2.0 ** -10])
+    # 1.0625 is the midpoint of 1.0 (m 0) and 1.125 (m 1): even -> 0x38; 1.1875 -> 1.25 (m 2);
+    # 2^-10 -> 0 (even), 3*2^-10 -> 2^-8 (m 2); beyond 448 saturates to 448 (0x7E);
+    # 440 lies above 432, the midpoint of 416 (m 5) and 448 (m 6) -> 448; 432 itself ties
+    # -> even m 6 = 448; 2^-6 - 2^-10 = 7.5 * 2^-9 ties -> 8 * 2^-9 = 2^-6 (0x08).
+    expected = [0x38, 0x3A, 0x00, 0x02, 0x7E, 0x7E, 0x7E, 0xFE, 0x80, 0x00, 0x7E, 0x7E, None,
+                0x08]
+    for got in (kvslots.e4m3_encode(x), paged.quantize_e4m3(x, 1.0).view(torch.uint8)):
+        for i, want in enumerate(expected):
+            if want is None:
+                assert int(got[i]) & 0x7F == 0x7F
+            else:
+                assert int(got[i]) == want, (float(x[i]), hex(int(got[i])))
+
+
+@pytest.mark.parametrize("scale", [1.0, 0.37, 3.3, 2.0 ** -4])
+def test_e4m3_quantize_matches_c_encoder(scale: float) -> None:
+    """Random magnitudes over 2^-14 .. 2^11, every midpoint between neighbouring codes and
+    the floats either side of it: torch's conversion equals the C encoder."""
+
+    g = torch.Generator().manual_seed(7)
+    x = torch.cat([torch.randn(50_000, generator=g) * 2.0 ** e for e in range(-14, 12, 2)])
+    pos = _e4m3_values()
+    pos = pos[~torch.isnan(pos) & (pos >= 0)].unique().sort().values
+    mids = ((pos[:-1].double() + pos[1:].double()) / 2).float() * scale
+    up = torch.nextafter(mids, torch.full_like(mids, float("inf")))
+    down = torch.nextafter(mids, torch.zeros_like(mids))
+    x = torch.cat([x, mids, -mids, up, down])
+    assert torch.equal(kvslots.e4m3_encode(x, scale), paged.quantize_e4m3(x, scale).view(torch.uint8))
+
+
+def test_e4m3_planted_truncation_is_caught() -> None:
+    """A quantizer that truncates (largest code <= |x|) instead of rounding to nearest
+    even disagrees with the C encoder; the torch restatement agrees with it."""
+
+    x = torch.linspace(0.01, 400.0, 10_001)
+    values = _e4m3_values()
+    values = values[~torch.isnan(values) & (values >= 0)].unique().sort().values
+    truncated = values[torch.searchsorted(values, x, right=True) - 1]
+    rounded = kvslots.e4m3_decode(kvslots.e4m3_encode(x))
+    assert not torch.equal(truncated, rounded)
+    assert torch.equal(kvslots.e4m3_encode(x), paged.quantize_e4m3(x, 1.0).view(torch.uint8))

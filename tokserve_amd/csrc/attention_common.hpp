@@ -101,6 +101,7 @@ struct DecodeArgs {
   void *out;
   int64_t o_ss, o_hs;
   float *ws_m, *ws_l, *ws_acc;
+  float v_scale;  // V decode factor of fp8 pools (1 otherwise)
 };
 
 struct PrefillArgs {
@@ -140,8 +141,10 @@ bool decode_mfma_supported(int32_t dtype, int32_t head_dim, int32_t group);
 
 // Launches the MFMA decode kernel over grid (max_splits, Hkv, B); returns a tks_status.
 // With max_splits == 1 it writes the output, otherwise split partials to be merged.
+// fp8_pools: K/V pools hold e4m3 (DecodeArgs.scale_log2 then carries k_scale,
+// DecodeArgs.v_scale the V factor).
 int32_t launch_decode_mfma(const DecodeArgs &a, int32_t dtype, int32_t num_seqs,
                            int32_t num_kv_heads, int32_t group, int32_t head_dim,
-                           hipStream_t stream);
+                           hipStream_t stream, bool fp8_pools);
 
 }  // namespace tks

@@ -30,6 +30,9 @@ inline bool valid_dtype(int32_t dtype) {
 
 inline int elem_bytes(int32_t dtype) { return dtype == TKS_FLOAT32 ? 4 : 2; }
 
+// A pool scale must be a positive finite float.
+inline bool valid_scale(float s) { return s > 0.f && s <= 3.4028234663852886e38f; }
+
 inline bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 // ------------------------------------------------------------ elements ---
@@ -122,6 +125,81 @@ __device__ __forceinline__ void unpack<_Float16>(uint4 v, float *out) {
     out[2 * i] = static_cast<float>(lo);
     out[2 * i + 1] = static_cast<float>(hi);
   }
+}
+
+// --------------------------------------------------------- fp8 (e4m3) ---
+//
+// OCP FP8 E4M3 (torch.float8_e4m3fn): sign, 4 exponent bits (bias 7), 3
+// mantissa bits, subnormals, no infinities, NaN = S.1111.111, largest finite
+// 448. Used only for K/V pools. Decoding is exact into f32, f16 and bf16;
+// encoding (v_cvt_pk_fp8_f32) rounds to nearest even after the value is
+// clamped to [-448, 448], and a NaN keeps its sign (fp8x4_nan_sign): the
+// result of torch's x.clamp(-448, 448).to(torch.float8_e4m3fn).
+
+struct fp8e4m3_t {
+  uint8_t bits;
+};
+constexpr float kFp8Max = 448.f;
+
+// Bytes 0, 1 (hi = false) or 2, 3 (hi = true) of w as floats.
+__device__ __forceinline__ void fp8x2_to_float(uint32_t w, bool hi, float *out) {
+#if __HIP_DEVICE_COMPILE__
+  const auto f = hi ? __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(w), true)
+                    : __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(w), false);
+  out[0] = f[0];
+  out[1] = f[1];
+#else
+  (void)w; (void)hi; (void)out;
+#endif
+}
+
+__device__ __forceinline__ void fp8x4_to_float(uint32_t w, float *out) {
+  fp8x2_to_float(w, false, out);
+  fp8x2_to_float(w, true, out + 2);
+}
+
+__device__ __forceinline__ float to_float(fp8e4m3_t x) {
+  float f[2];
+  fp8x2_to_float(x.bits, false, f);
+  return f[0];
+}
+
+__device__ __forceinline__ float fp8_clamp(float x) {
+  return x > kFp8Max ? kFp8Max : (x < -kFp8Max ? -kFp8Max : x);  // NaN compares false: kept
+}
+
+// Four floats -> four e4m3 bytes (element 0 in the low byte).
+__device__ __forceinline__ uint32_t float4_to_fp8x4(float a, float b, float c, float d) {
+#if __HIP_DEVICE_COMPILE__
+  int w = __builtin_amdgcn_cvt_pk_fp8_f32(fp8_clamp(a), fp8_clamp(b), 0, false);
+  w = __builtin_amdgcn_cvt_pk_fp8_f32(fp8_clamp(c), fp8_clamp(d), w, true);
+  return static_cast<uint32_t>(w);
+#else
+  (void)a; (void)b; (void)c; (void)d;
+  return 0;
+#endif
+}
+
+// The converter writes one NaN code whatever the input's sign; torch keeps the
+// sign (S.1111.111). Rewrites the NaN bytes of w from the signs of the four
+// source values x[0..3] (NaN before any scaling, so the sign is the input's).
+__device__ __forceinline__ uint32_t fp8x4_nan_sign(uint32_t w, const float *x) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t bits = __float_as_uint(x[i]);
+    const bool nan = (bits & 0x7fffffffu) > 0x7f800000u;
+    const uint32_t code = (bits >> 31) ? 0xffu : 0x7fu;
+    w = nan ? ((w & ~(0xffu << (8 * i))) | (code << (8 * i))) : w;
+  }
+  return w;
+}
+
+template <>
+__device__ __forceinline__ void unpack<fp8e4m3_t>(uint4 v, float *out) {
+  fp8x4_to_float(v.x, out);
+  fp8x4_to_float(v.y, out + 4);
+  fp8x4_to_float(v.z, out + 8);
+  fp8x4_to_float(v.w, out + 12);
 }
 
 template <typename T>

@@ -48,11 +48,64 @@ __device__ __forceinline__ void wave_lds_sync() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-template <typename T, int DH, int G>
+// K/V rows as stored: T itself, or fp8 e4m3 decoded to T (K, exactly: every
+// e4m3 value is a bf16 and an f16) or to f32 (V) right after the load. A lane's
+// 8 elements are one 16-byte load of T or one 8-byte load of fp8.
+template <typename T, typename KV>
+struct PageIO {
+  typedef uint4 raw;
+  static __device__ __forceinline__ raw load(const KV *p) { return ld16_stream(p); }
+  static __device__ __forceinline__ typename Mfma<T>::v8 k_operand(raw r) { return as_v8<T>(r); }
+  static __device__ __forceinline__ void v_floats(raw r, float *f) { unpack<T>(r, f); }
+};
+template <typename T>
+struct PageIO<T, fp8e4m3_t> {
+  typedef uint2 raw;
+  static __device__ __forceinline__ raw load(const fp8e4m3_t *p) {
+    typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+    const u32x2 v = __builtin_nontemporal_load(reinterpret_cast<const u32x2 *>(p));
+    return make_uint2(v.x, v.y);
+  }
+  static __device__ __forceinline__ typename Mfma<T>::v8 k_operand(raw r) {
+    typename Mfma<T>::v8 o = {};
+#if __HIP_DEVICE_COMPILE__
+    const uint32_t w[2] = {r.x, r.y};
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      if constexpr (__is_same(T, bf16_t)) {
+        const auto lo = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w[i], 1.0f, false);
+        const auto hi = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w[i], 1.0f, true);
+        o[4 * i] = lo[0];
+        o[4 * i + 1] = lo[1];
+        o[4 * i + 2] = hi[0];
+        o[4 * i + 3] = hi[1];
+      } else {
+        const auto lo = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w[i], 1.0f, false);
+        const auto hi = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w[i], 1.0f, true);
+        o[4 * i] = lo[0];
+        o[4 * i + 1] = lo[1];
+        o[4 * i + 2] = hi[0];
+        o[4 * i + 3] = hi[1];
+      }
+    }
+#else
+    (void)r;
+#endif
+    return o;
+  }
+  static __device__ __forceinline__ void v_floats(raw r, float *f) {
+    fp8x4_to_float(r.x, f);
+    fp8x4_to_float(r.y, f + 4);
+  }
+};
+
+template <typename T, typename KV, int DH, int G>
 __global__ __launch_bounds__(64 * kWaves) void decode_mfma_kernel(DecodeArgs a) {
   using S = DecodeShape<DH, G>;
   constexpr int BS = S::BS, NC = S::NC, LPR = S::LPR, TG = S::TG, HPL = S::HPL;
   using M = Mfma<T>;
+  using IO = PageIO<T, KV>;
+  using raw = typename IO::raw;
   __shared__ __attribute__((aligned(16))) float p_s[kWaves][G][BS];
   __shared__ __attribute__((aligned(16))) float alpha_s[kWaves][G];
   __shared__ __attribute__((aligned(16))) float m_s[kWaves][G];
@@ -95,8 +148,8 @@ __global__ __launch_bounds__(64 * kWaves) void decode_mfma_kernel(DecodeArgs a) 
     for (int c = 0; c < NC; ++c) qa[c] = as_v8<T>(ld16(qp + c * 32));
   }
 
-  const T *kc = static_cast<const T *>(a.kc) + a.pool.layer_base + (int64_t)kvh * a.pool.head_stride;
-  const T *vc = static_cast<const T *>(a.vc) + a.pool.layer_base + (int64_t)kvh * a.pool.head_stride;
+  const KV *kc = static_cast<const KV *>(a.kc) + a.pool.layer_base + (int64_t)kvh * a.pool.head_stride;
+  const KV *vc = static_cast<const KV *>(a.vc) + a.pool.layer_base + (int64_t)kvh * a.pool.head_stride;
   const int k_off = r * DH + grp * 8;
   const int v_off = tg * 4 * DH + dc * 8;
   const int32_t *bt_row = a.bt + (int64_t)b * a.bt_stride;
@@ -114,20 +167,20 @@ __global__ __launch_bounds__(64 * kWaves) void decode_mfma_kernel(DecodeArgs a) 
   }
 
   // Every page is read once: non-temporal loads.
-  auto load_page = [&](int blk_reg, int idx, uint4 (&kr)[NC], uint4 (&vr)[4]) {
+  auto load_page = [&](int blk_reg, int idx, raw (&kr)[NC], raw (&vr)[4]) {
     const int64_t blk = clamp_block(__builtin_amdgcn_readlane(blk_reg, idx), a.pool.num_blocks);
-    const T *kp = kc + blk * a.pool.block_stride + k_off;
-    const T *vp = vc + blk * a.pool.block_stride + v_off;
+    const KV *kp = kc + blk * a.pool.block_stride + k_off;
+    const KV *vp = vc + blk * a.pool.block_stride + v_off;
 #pragma unroll
-    for (int c = 0; c < NC; ++c) kr[c] = ld16_stream(kp + c * 32);
+    for (int c = 0; c < NC; ++c) kr[c] = IO::load(kp + c * 32);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) vr[j] = ld16_stream(vp + j * DH);
+    for (int j = 0; j < 4; ++j) vr[j] = IO::load(vp + j * DH);
   };
 
-  auto consume = [&](const uint4 (&kr)[NC], const uint4 (&vr)[4], int p) {
+  auto consume = [&](const raw (&kr)[NC], const raw (&vr)[4], int p) {
     typename M::f4 s4 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int c = 0; c < NC; ++c) s4 = M::run(qa[c], as_v8<T>(kr[c]), s4);
+    for (int c = 0; c < NC; ++c) s4 = M::run(qa[c], IO::k_operand(kr[c]), s4);
     const bool valid = p * BS + r < len;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -146,7 +199,7 @@ __global__ __launch_bounds__(64 * kWaves) void decode_mfma_kernel(DecodeArgs a) 
     wave_lds_sync();
     float vf[4][8];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) unpack<T>(vr[j], vf[j]);
+    for (int j = 0; j < 4; ++j) IO::v_floats(vr[j], vf[j]);
 #pragma unroll
     for (int j = 0; j < HPL; ++j) {
       const int h = hg * HPL + j;
@@ -167,7 +220,7 @@ __global__ __launch_bounds__(64 * kWaves) void decode_mfma_kernel(DecodeArgs a) 
   for (int c0 = w_begin; c0 < w_end; c0 += 64) {
     const int n = min(w_end, c0 + 64) - c0;
     const int blk_reg = lane < n ? bt_row[c0 + lane] : 0;
-    uint4 kA[NC], vA[4], kB[NC], vB[4];
+    raw kA[NC], vA[4], kB[NC], vB[4];
     load_page(blk_reg, 0, kA, vA);
     int i = 0;
     for (; i + 2 < n; i += 2) {
@@ -227,27 +280,28 @@ __global__ __launch_bounds__(64 * kWaves) void decode_mfma_kernel(DecodeArgs a) 
       L += e * l_s[w][h];
       o += e * acc_s[w][h][d];
     }
+    // v_scale (1 for pools in the model dtype, an exact no-op) decodes V.
     if (single) {
-      out[b * a.o_ss + (int64_t)(kvh * G + h) * a.o_hs + d] = from_float<T>(o / L);
+      out[b * a.o_ss + (int64_t)(kvh * G + h) * a.o_hs + d] = from_float<T>(o / L * a.v_scale);
     } else {
       const int64_t w = ((int64_t)b * a.num_q_heads + kvh * G + h) * a.max_splits + split;
       if (d == 0) {
         a.ws_m[w] = M_;
         a.ws_l[w] = L;
       }
-      a.ws_acc[w * DH + d] = o;
+      a.ws_acc[w * DH + d] = o * a.v_scale;
     }
   }
 }
 
-template <typename T>
+template <typename T, typename KV>
 int32_t launch_typed(const DecodeArgs &a, int32_t num_seqs, int32_t num_kv_heads, int32_t G,
                      int32_t head_dim, hipStream_t s) {
   const dim3 grid(a.max_splits, num_kv_heads, num_seqs);
-#define TKS_DECODE(DH, GG)                                           \
-  if (head_dim == DH && G == GG) {                                   \
-    decode_mfma_kernel<T, DH, GG><<<grid, 64 * kWaves, 0, s>>>(a);   \
-    return check_launch();                                           \
+#define TKS_DECODE(DH, GG)                                              \
+  if (head_dim == DH && G == GG) {                                      \
+    decode_mfma_kernel<T, KV, DH, GG><<<grid, 64 * kWaves, 0, s>>>(a);  \
+    return check_launch();                                              \
   }
   TKS_DECODE(128, 4)
   TKS_DECODE(128, 8)
@@ -272,10 +326,16 @@ bool decode_mfma_supported(int32_t dtype, int32_t head_dim, int32_t group) {
 
 int32_t launch_decode_mfma(const DecodeArgs &a, int32_t dtype, int32_t num_seqs,
                            int32_t num_kv_heads, int32_t group, int32_t head_dim,
-                           hipStream_t stream) {
+                           hipStream_t stream, bool fp8_pools) {
+  if (fp8_pools)
+    return dtype == TKS_BFLOAT16
+               ? launch_typed<bf16_t, fp8e4m3_t>(a, num_seqs, num_kv_heads, group, head_dim, stream)
+               : launch_typed<_Float16, fp8e4m3_t>(a, num_seqs, num_kv_heads, group, head_dim,
+                                                   stream);
   return dtype == TKS_BFLOAT16
-             ? launch_typed<bf16_t>(a, num_seqs, num_kv_heads, group, head_dim, stream)
-             : launch_typed<_Float16>(a, num_seqs, num_kv_heads, group, head_dim, stream);
+             ? launch_typed<bf16_t, bf16_t>(a, num_seqs, num_kv_heads, group, head_dim, stream)
+             : launch_typed<_Float16, _Float16>(a, num_seqs, num_kv_heads, group, head_dim,
+                                                stream);
 }
 
 }  // namespace tks

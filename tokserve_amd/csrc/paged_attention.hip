@@ -55,6 +55,7 @@ struct GenericArgs {
   int64_t o_rs, o_hs;
   float *ws_m, *ws_l, *ws_acc;
   int32_t vec_rows;  // K/V rows are 16-byte aligned and head_dim is a multiple of 16 bytes
+  float v_scale;     // V decode factor of fp8 pools (1 otherwise)
 };
 
 // The split's keys are dealt to the four waves 64 at a time (wave w takes keys
@@ -68,9 +69,9 @@ struct GenericArgs {
 // a zero row offset (an in-bounds read whose score is masked and whose V is
 // zeroed). The waves' (m, l, acc) are combined through LDS at the end.
 // DHMAX (64 or 128) bounds head_dim; dims past head_dim are zero in q and K.
-template <typename T, int DHMAX>
+template <typename T, typename KV, int DHMAX>
 __global__ __launch_bounds__(kGenThreads) void attn_generic_kernel(GenericArgs a) {
-  constexpr int V = Vec<T>::N;
+  constexpr int V = Vec<KV>::N;
   constexpr int DPL = DHMAX / 64;  // dims per lane in P.V
   __shared__ __align__(16) float q_s[kGenMaxG][DHMAX];
   __shared__ float part_m[kGenWaves][kGenMaxG];
@@ -118,8 +119,8 @@ __global__ __launch_bounds__(kGenThreads) void attn_generic_kernel(GenericArgs a
   }
   const int t_end = min(kv_len, t_begin + tok_per_split);
 
-  const T *kc = static_cast<const T *>(a.kc);
-  const T *vc = static_cast<const T *>(a.vc);
+  const KV *kc = static_cast<const KV *>(a.kc);
+  const KV *vc = static_cast<const KV *>(a.vc);
   const int32_t *bt_row = a.bt + (int64_t)seq * a.bt_stride;
 
   // Row offset of key t0 + lane (0 past the step's range) and the step's K row
@@ -138,7 +139,7 @@ __global__ __launch_bounds__(kGenThreads) void attn_generic_kernel(GenericArgs a
 #pragma unroll
       for (int d = 0; d < DHMAX; d += V) {
         if (d < DH) {
-          unpack<T>(ld16(kc + rb + d), kv + d);
+          unpack<KV>(ld16(kc + rb + d), kv + d);
         } else {
 #pragma unroll
           for (int i = 0; i < V; ++i) kv[d + i] = 0.f;
@@ -258,14 +259,15 @@ __global__ __launch_bounds__(kGenThreads) void attn_generic_kernel(GenericArgs a
     }
     const int qh = kvh * G + g;
     if (a.max_splits == 1) {
-      out[(int64_t)row * a.o_rs + (int64_t)qh * a.o_hs + d] = from_float<T>(o / lsum);
+      out[(int64_t)row * a.o_rs + (int64_t)qh * a.o_hs + d] =
+          from_float<T>(o / lsum * a.v_scale);
     } else {
       const int64_t w = ((int64_t)row * a.num_q_heads + qh) * a.max_splits + split;
       if (d == 0) {
         a.ws_m[w] = mx;
         a.ws_l[w] = lsum;
       }
-      a.ws_acc[w * DH + d] = o;
+      a.ws_acc[w * DH + d] = o * a.v_scale;
     }
   }
 }
@@ -355,16 +357,31 @@ PoolView make_pool(int32_t layer_index, int64_t num_blocks, int32_t num_kv_heads
   return p;
 }
 
-template <typename T>
-int32_t launch_generic(const GenericArgs &a, int32_t rows, int32_t num_kv_heads,
-                       hipStream_t s) {
+template <typename T, typename KV>
+int32_t launch_generic_kv(const GenericArgs &a, int32_t rows, int32_t num_kv_heads,
+                          hipStream_t s) {
   const dim3 grid(static_cast<unsigned>(static_cast<int64_t>(rows) * a.max_splits),
                   num_kv_heads);
   if (a.pool.head_dim <= 64)
-    attn_generic_kernel<T, 64><<<grid, kGenThreads, 0, s>>>(a);
+    attn_generic_kernel<T, KV, 64><<<grid, kGenThreads, 0, s>>>(a);
   else
-    attn_generic_kernel<T, 128><<<grid, kGenThreads, 0, s>>>(a);
+    attn_generic_kernel<T, KV, 128><<<grid, kGenThreads, 0, s>>>(a);
   return check_launch();
+}
+
+int32_t launch_generic(const GenericArgs &a, int32_t dtype, int32_t rows, int32_t num_kv_heads,
+                       bool fp8_pools, hipStream_t s) {
+  switch (dtype) {
+    case TKS_FLOAT32:
+      return fp8_pools ? launch_generic_kv<float, fp8e4m3_t>(a, rows, num_kv_heads, s)
+                       : launch_generic_kv<float, float>(a, rows, num_kv_heads, s);
+    case TKS_FLOAT16:
+      return fp8_pools ? launch_generic_kv<_Float16, fp8e4m3_t>(a, rows, num_kv_heads, s)
+                       : launch_generic_kv<_Float16, _Float16>(a, rows, num_kv_heads, s);
+    default:
+      return fp8_pools ? launch_generic_kv<bf16_t, fp8e4m3_t>(a, rows, num_kv_heads, s)
+                       : launch_generic_kv<bf16_t, bf16_t>(a, rows, num_kv_heads, s);
+  }
 }
 
 // K/V rows can be read 16 bytes at a time: pools aligned, rows a multiple of 16 bytes.
@@ -402,19 +419,22 @@ extern "C" int64_t tks_paged_attention_decode_workspace_bytes(int32_t num_seqs,
   return carve(nullptr, num_seqs, num_q_heads, max_splits, head_dim).bytes;
 }
 
-extern "C" int32_t tks_paged_attention_decode(
-    const void *query, int64_t q_seq_stride, int64_t q_head_stride, const void *key_cache,
-    const void *value_cache, int32_t num_layers, int64_t num_blocks, int32_t num_kv_heads,
-    int32_t block_size, int32_t head_dim, int32_t layer_index, const int32_t *block_tables,
-    int32_t block_table_stride, const int32_t *seq_lens, const int32_t *seq_order, int32_t num_seqs,
-    int32_t num_q_heads,
-    int32_t max_seq_len, float scale, int32_t pages_per_split, void *out,
-    int64_t out_seq_stride, int64_t out_head_stride, void *workspace, int64_t workspace_bytes,
-    int32_t dtype, tks_stream_t stream) {
+namespace {
+
+int32_t decode_impl(const void *query, int64_t q_seq_stride, int64_t q_head_stride,
+                    const void *key_cache, const void *value_cache, int32_t num_layers,
+                    int64_t num_blocks, int32_t num_kv_heads, int32_t block_size,
+                    int32_t head_dim, int32_t layer_index, const int32_t *block_tables,
+                    int32_t block_table_stride, const int32_t *seq_lens,
+                    const int32_t *seq_order, int32_t num_seqs, int32_t num_q_heads,
+                    int32_t max_seq_len, float scale, int32_t pages_per_split, void *out,
+                    int64_t out_seq_stride, int64_t out_head_stride, void *workspace,
+                    int64_t workspace_bytes, bool fp8_pools, float k_scale, float v_scale,
+                    int32_t dtype, tks_stream_t stream) {
   if (!valid_dtype(dtype)) return TKS_ERR_TYPE;
   if (!pool_ok(num_layers, num_blocks, num_kv_heads, block_size, head_dim) || num_seqs < 0 ||
       num_q_heads <= 0 || num_q_heads % num_kv_heads != 0 || max_seq_len < 0 ||
-      pages_per_split < 0)
+      pages_per_split < 0 || !valid_scale(k_scale) || !valid_scale(v_scale))
     return TKS_ERR_VALUE;
   const int32_t G = num_q_heads / num_kv_heads;
   if (G > kGenMaxG) return TKS_ERR_VALUE;
@@ -436,7 +456,7 @@ extern "C" int32_t tks_paged_attention_decode(
 
   const PoolView pool = make_pool(layer_index, num_blocks, num_kv_heads, block_size, head_dim);
   hipStream_t s = static_cast<hipStream_t>(stream);
-  const float scale_log2 = scale * kLog2e;
+  const float scale_log2 = scale * kLog2e * k_scale;
 
   int32_t st;
   if (mfma_eligible(dtype, block_size, head_dim, G, query, q_seq_stride, q_head_stride,
@@ -444,19 +464,17 @@ extern "C" int32_t tks_paged_attention_decode(
     DecodeArgs a{query,      q_seq_stride, q_head_stride, key_cache,   value_cache,
                  pool,       block_tables, block_table_stride, seq_lens, seq_order, num_q_heads,
                  scale_log2, pps,          max_splits,    key_cap,     out,
-                 out_seq_stride, out_head_stride, w.m,    w.l,         w.acc};
-    st = launch_decode_mfma(a, dtype, num_seqs, num_kv_heads, G, head_dim, s);
+                 out_seq_stride, out_head_stride, w.m,    w.l,         w.acc,
+                 v_scale};
+    st = launch_decode_mfma(a, dtype, num_seqs, num_kv_heads, G, head_dim, s, fp8_pools);
   } else {
+    const int kv_elem = fp8_pools ? 1 : elem_bytes(dtype);
     GenericArgs a{query,     q_seq_stride, q_head_stride, key_cache, value_cache, pool,
                   block_tables, block_table_stride, seq_lens, seq_order, nullptr, num_seqs, num_q_heads,
                   G,         scale_log2,   pps,           max_splits, key_cap,  out,
                   out_seq_stride, out_head_stride, w.m,   w.l,        w.acc,
-                  vec_rows_ok(key_cache, value_cache, head_dim, elem_bytes(dtype))};
-    switch (dtype) {
-      case TKS_FLOAT32: st = launch_generic<float>(a, num_seqs, num_kv_heads, s); break;
-      case TKS_FLOAT16: st = launch_generic<_Float16>(a, num_seqs, num_kv_heads, s); break;
-      default: st = launch_generic<bf16_t>(a, num_seqs, num_kv_heads, s); break;
-    }
+                  vec_rows_ok(key_cache, value_cache, head_dim, kv_elem), v_scale};
+    st = launch_generic(a, dtype, num_seqs, num_kv_heads, fp8_pools, s);
   }
   if (st != TKS_OK || max_splits == 1) return st;
   const dim3 grid(num_q_heads, num_seqs);
@@ -474,18 +492,21 @@ extern "C" int32_t tks_paged_attention_decode(
   return check_launch();
 }
 
-extern "C" int32_t tks_paged_attention_prefill(
-    const void *query, int64_t q_token_stride, int64_t q_head_stride, const void *key_cache,
-    const void *value_cache, int32_t num_layers, int64_t num_blocks, int32_t num_kv_heads,
-    int32_t block_size, int32_t head_dim, int32_t layer_index, const int32_t *block_tables,
-    int32_t block_table_stride, const int32_t *seq_lens, const int32_t *cu_seqlens_q,
-    int32_t num_seqs, int64_t num_tokens, int32_t num_q_heads, int32_t max_query_len,
-    int32_t max_seq_len, float scale, void *out, int64_t out_token_stride,
-    int64_t out_head_stride, int32_t dtype, tks_stream_t stream) {
+int32_t prefill_impl(const void *query, int64_t q_token_stride, int64_t q_head_stride,
+                     const void *key_cache, const void *value_cache, int32_t num_layers,
+                     int64_t num_blocks, int32_t num_kv_heads, int32_t block_size,
+                     int32_t head_dim, int32_t layer_index, const int32_t *block_tables,
+                     int32_t block_table_stride, const int32_t *seq_lens,
+                     const int32_t *cu_seqlens_q, int32_t num_seqs, int64_t num_tokens,
+                     int32_t num_q_heads, int32_t max_query_len, int32_t max_seq_len,
+                     float scale, void *out, int64_t out_token_stride, int64_t out_head_stride,
+                     bool fp8_pools, float k_scale, float v_scale, int32_t dtype,
+                     tks_stream_t stream) {
   if (!valid_dtype(dtype)) return TKS_ERR_TYPE;
   if (!pool_ok(num_layers, num_blocks, num_kv_heads, block_size, head_dim) || num_seqs < 0 ||
       num_tokens < 0 || num_q_heads <= 0 || num_q_heads % num_kv_heads != 0 ||
-      max_query_len < 0 || max_seq_len < 0 || max_query_len > max_seq_len)
+      max_query_len < 0 || max_seq_len < 0 || max_query_len > max_seq_len ||
+      !valid_scale(k_scale) || !valid_scale(v_scale))
     return TKS_ERR_VALUE;
   const int32_t G = num_q_heads / num_kv_heads;
   if (G > kGenMaxG) return TKS_ERR_VALUE;
@@ -498,11 +519,12 @@ extern "C" int32_t tks_paged_attention_prefill(
     return TKS_ERR_VALUE;
   const PoolView pool = make_pool(layer_index, num_blocks, num_kv_heads, block_size, head_dim);
   hipStream_t s = static_cast<hipStream_t>(stream);
-  const float scale_log2 = scale * kLog2e;
+  const float scale_log2 = scale * kLog2e * k_scale;
   // One split covering the whole key range: no partials, no workspace.
   const int32_t pps = static_cast<int32_t>(ceil_div(max_seq_len > 0 ? max_seq_len : 1, block_size));
   const int32_t key_cap = std::min(block_table_stride, pps) * block_size;
-  if (prefill_mfma_supported(dtype, head_dim, G, key_cap, block_size, num_blocks, num_kv_heads) &&
+  if (!fp8_pools &&
+      prefill_mfma_supported(dtype, head_dim, G, key_cap, block_size, num_blocks, num_kv_heads) &&
       aligned16(query) &&
       aligned16(key_cache) && aligned16(value_cache) && q_token_stride % 8 == 0 &&
       q_head_stride % 8 == 0) {
@@ -511,15 +533,75 @@ extern "C" int32_t tks_paged_attention_prefill(
                   scale_log2, key_cap,      out,           out_token_stride, out_head_stride};
     return launch_prefill_mfma(p, dtype, num_seqs, num_kv_heads, G, head_dim, max_query_len, s);
   }
+  const int kv_elem = fp8_pools ? 1 : elem_bytes(dtype);
   GenericArgs a{query,     q_token_stride, q_head_stride, key_cache,  value_cache, pool,
                 block_tables, block_table_stride, seq_lens, nullptr, cu_seqlens_q, num_seqs, num_q_heads,
                 G,         scale_log2,     pps,           1,          key_cap,     out,         out_token_stride,
                 out_head_stride, nullptr,  nullptr,       nullptr,
-                vec_rows_ok(key_cache, value_cache, head_dim, elem_bytes(dtype))};
-  const int32_t rows = static_cast<int32_t>(num_tokens);
-  switch (dtype) {
-    case TKS_FLOAT32: return launch_generic<float>(a, rows, num_kv_heads, s);
-    case TKS_FLOAT16: return launch_generic<_Float16>(a, rows, num_kv_heads, s);
-    default: return launch_generic<bf16_t>(a, rows, num_kv_heads, s);
-  }
+                vec_rows_ok(key_cache, value_cache, head_dim, kv_elem), v_scale};
+  return launch_generic(a, dtype, static_cast<int32_t>(num_tokens), num_kv_heads, fp8_pools, s);
+}
+
+}  // namespace
+
+extern "C" int32_t tks_paged_attention_decode(
+    const void *query, int64_t q_seq_stride, int64_t q_head_stride, const void *key_cache,
+    const void *value_cache, int32_t num_layers, int64_t num_blocks, int32_t num_kv_heads,
+    int32_t block_size, int32_t head_dim, int32_t layer_index, const int32_t *block_tables,
+    int32_t block_table_stride, const int32_t *seq_lens, const int32_t *seq_order, int32_t num_seqs,
+    int32_t num_q_heads,
+    int32_t max_seq_len, float scale, int32_t pages_per_split, void *out,
+    int64_t out_seq_stride, int64_t out_head_stride, void *workspace, int64_t workspace_bytes,
+    int32_t dtype, tks_stream_t stream) {
+  return decode_impl(query, q_seq_stride, q_head_stride, key_cache, value_cache, num_layers,
+                     num_blocks, num_kv_heads, block_size, head_dim, layer_index, block_tables,
+                     block_table_stride, seq_lens, seq_order, num_seqs, num_q_heads, max_seq_len,
+                     scale, pages_per_split, out, out_seq_stride, out_head_stride, workspace,
+                     workspace_bytes, false, 1.f, 1.f, dtype, stream);
+}
+
+extern "C" int32_t tks_paged_attention_decode_fp8(
+    const void *query, int64_t q_seq_stride, int64_t q_head_stride, const void *key_cache,
+    const void *value_cache, int32_t num_layers, int64_t num_blocks, int32_t num_kv_heads,
+    int32_t block_size, int32_t head_dim, int32_t layer_index, const int32_t *block_tables,
+    int32_t block_table_stride, const int32_t *seq_lens, const int32_t *seq_order,
+    int32_t num_seqs, int32_t num_q_heads, int32_t max_seq_len, float scale,
+    int32_t pages_per_split, void *out, int64_t out_seq_stride, int64_t out_head_stride,
+    void *workspace, int64_t workspace_bytes, float k_scale, float v_scale, int32_t dtype,
+    tks_stream_t stream) {
+  return decode_impl(query, q_seq_stride, q_head_stride, key_cache, value_cache, num_layers,
+                     num_blocks, num_kv_heads, block_size, head_dim, layer_index, block_tables,
+                     block_table_stride, seq_lens, seq_order, num_seqs, num_q_heads, max_seq_len,
+                     scale, pages_per_split, out, out_seq_stride, out_head_stride, workspace,
+                     workspace_bytes, true, k_scale, v_scale, dtype, stream);
+}
+
+extern "C" int32_t tks_paged_attention_prefill(
+    const void *query, int64_t q_token_stride, int64_t q_head_stride, const void *key_cache,
+    const void *value_cache, int32_t num_layers, int64_t num_blocks, int32_t num_kv_heads,
+    int32_t block_size, int32_t head_dim, int32_t layer_index, const int32_t *block_tables,
+    int32_t block_table_stride, const int32_t *seq_lens, const int32_t *cu_seqlens_q,
+    int32_t num_seqs, int64_t num_tokens, int32_t num_q_heads, int32_t max_query_len,
+    int32_t max_seq_len, float scale, void *out, int64_t out_token_stride,
+    int64_t out_head_stride, int32_t dtype, tks_stream_t stream) {
+  return prefill_impl(query, q_token_stride, q_head_stride, key_cache, value_cache, num_layers,
+                      num_blocks, num_kv_heads, block_size, head_dim, layer_index, block_tables,
+                      block_table_stride, seq_lens, cu_seqlens_q, num_seqs, num_tokens,
+                      num_q_heads, max_query_len, max_seq_len, scale, out, out_token_stride,
+                      out_head_stride, false, 1.f, 1.f, dtype, stream);
+}
+
+extern "C" int32_t tks_paged_attention_prefill_fp8(
+    const void *query, int64_t q_token_stride, int64_t q_head_stride, const void *key_cache,
+    const void *value_cache, int32_t num_layers, int64_t num_blocks, int32_t num_kv_heads,
+    int32_t block_size, int32_t head_dim, int32_t layer_index, const int32_t *block_tables,
+    int32_t block_table_stride, const int32_t *seq_lens, const int32_t *cu_seqlens_q,
+    int32_t num_seqs, int64_t num_tokens, int32_t num_q_heads, int32_t max_query_len,
+    int32_t max_seq_len, float scale, void *out, int64_t out_token_stride,
+    int64_t out_head_stride, float k_scale, float v_scale, int32_t dtype, tks_stream_t stream) {
+  return prefill_impl(query, q_token_stride, q_head_stride, key_cache, value_cache, num_layers,
+                      num_blocks, num_kv_heads, block_size, head_dim, layer_index, block_tables,
+                      block_table_stride, seq_lens, cu_seqlens_q, num_seqs, num_tokens,
+                      num_q_heads, max_query_len, max_seq_len, scale, out, out_token_stride,
+                      out_head_stride, true, k_scale, v_scale, dtype, stream);
 }

@@ -139,13 +139,13 @@ class GroupedQueryAttention(nn.Module):
                 query[:split], storage.key_storage, storage.value_storage,
                 batch.prefill_block_tables, batch.prefill_seq_lens, batch.prefill_cu_seqlens_q,
                 layer_index=layer_index, max_query_len=batch.prefill_max_query_len,
-                max_seq_len=batch.prefill_max_seq_len, out=attended[:split],
+                max_seq_len=batch.prefill_max_seq_len, out=attended[:split], **storage.scales,
             )
         if split < tokens:
             ops.paged_attention_decode(
                 query[split:], storage.key_storage, storage.value_storage,
                 batch.decode_block_tables, batch.decode_seq_lens, layer_index=layer_index,
                 max_seq_len=batch.decode_max_seq_len, out=attended[split:],
-                seq_order=batch.decode_seq_order,
+                seq_order=batch.decode_seq_order, **storage.scales,
             )
         return self.o_proj(attended.view(tokens, self.hidden_size))

@@ -24,6 +24,9 @@ class PagedKVCacheManager:
         head_dim: int,
         device: torch.device,
         dtype: torch.dtype,
+        kv_dtype: torch.dtype | None = None,
+        k_scale: float = 1.0,
+        v_scale: float = 1.0,
     ) -> None:
         self.allocator = PhysicalBlockAllocator(num_blocks)
         self.storage = PagedKVStorage(
@@ -34,6 +37,9 @@ class PagedKVCacheManager:
             head_dim=head_dim,
             device=device,
             dtype=dtype,
+            kv_dtype=kv_dtype,
+            k_scale=k_scale,
+            v_scale=v_scale,
         )
         self._sequences: dict[str, SequencePagedKVCache] = {}
 

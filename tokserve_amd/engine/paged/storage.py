@@ -5,6 +5,12 @@ storage.py:40-56), allocated uninitialised like the reference's torch.empty.
 Writes go through the KV-append kernel (tks_kv_append), reads through the
 block-table gather kernel (tks_paged_gather); the kernels run on HIP devices
 only, and a storage on another device rejects them.
+
+A pool variant the reference lacks: `kv_dtype=torch.float8_e4m3fn` stores
+K and V as OCP fp8 e4m3 with one fp32 scale per pool (stored =
+e4m3(clamp(x / scale, -448, 448)), decoded = float(stored) * scale), half the
+bytes of bf16 pools. The API is unchanged: writes take rows in `dtype`, reads
+and attention see the decoded values.
 """
 
 from __future__ import annotations
@@ -29,6 +35,9 @@ class PagedKVStorage:
         head_dim: int,
         device: torch.device,
         dtype: torch.dtype,
+        kv_dtype: torch.dtype | None = None,
+        k_scale: float = 1.0,
+        v_scale: float = 1.0,
     ) -> None:
         for name, size in (
             ("num_layers", num_layers),
@@ -46,9 +55,19 @@ class PagedKVStorage:
         self.head_dim = head_dim
         self.device = torch.device(device)
         self.dtype = dtype
+        self.kv_dtype = dtype if kv_dtype is None else kv_dtype
+        if self.kv_dtype not in (dtype, ops.FP8_POOL_DTYPE):
+            raise ValueError("kv_dtype must be the model dtype or torch.float8_e4m3fn")
+        self.k_scale = float(k_scale)
+        self.v_scale = float(v_scale)
+        if self.kv_dtype == ops.FP8_POOL_DTYPE:
+            if not (0.0 < self.k_scale < float("inf") and 0.0 < self.v_scale < float("inf")):
+                raise ValueError("k_scale and v_scale must be positive finite floats")
+        elif self.k_scale != 1.0 or self.v_scale != 1.0:
+            raise ValueError("k_scale and v_scale apply to fp8 pools only")
         shape = (num_layers, num_blocks, num_key_value_heads, block_size, head_dim)
-        self._key_storage = torch.empty(shape, device=self.device, dtype=dtype)
-        self._value_storage = torch.empty(shape, device=self.device, dtype=dtype)
+        self._key_storage = torch.empty(shape, device=self.device, dtype=self.kv_dtype)
+        self._value_storage = torch.empty(shape, device=self.device, dtype=self.kv_dtype)
 
     @property
     def storage_shape(self) -> tuple[int, ...]:
@@ -65,6 +84,12 @@ class PagedKVStorage:
         """The physical V pool, for kernels."""
 
         return self._value_storage
+
+    @property
+    def scales(self) -> dict[str, float]:
+        """Pool decode factors as the kernels' keyword arguments."""
+
+        return {"k_scale": self.k_scale, "v_scale": self.v_scale}
 
     # ------------------------------------------------------------- single slot
 
@@ -117,7 +142,7 @@ class PagedKVStorage:
         if layer_index < 0 or layer_index >= self.num_layers:
             raise IndexError("layer_index is out of range")
         ops.kv_append(keys, values, self._key_storage, self._value_storage, slot_mapping,
-                      layer_index)
+                      layer_index, **self.scales)
 
     def gather(
         self, layer_index: int, block_ids: tuple[int, ...] | list[int], length: int
@@ -138,6 +163,7 @@ class PagedKVStorage:
         ops.paged_gather(
             self._key_storage, self._value_storage, meta[:needed].view(1, needed),
             meta[needed : needed + 1], meta[needed + 1 :], layer_index, length, keys, values,
+            **self.scales,
         )
         return keys, values
 

@@ -15,7 +15,7 @@ from pathlib import Path
 import torch
 
 LIBRARY_NAME = "libtokserve_hip.so"
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 TKS_OK = 0
 TKS_ERR_VALUE = -1
@@ -77,6 +77,30 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "tks_argmax": (_i32, [_c_void_p, _i64, _i64, _i64, _c_void_p, _i32, _c_void_p]),
     "tks_vector_add": (_i32, [_c_void_p, _c_void_p, _c_void_p, _i64, _i32, _c_void_p]),
     "tks_silu_mul": (_i32, [_c_void_p, _i64, _i64, _i64, _c_void_p, _i64, _i32, _c_void_p]),
+    "tks_kv_append_fp8": (
+        _i32,
+        [_c_void_p, _i64, _i64, _c_void_p, _i64, _i64, _i64, _c_void_p, _c_void_p,
+         _i32, _i64, _i32, _i32, _i32, _i32, _c_void_p, _f32, _f32, _i32, _c_void_p],
+    ),
+    "tks_paged_gather_fp8": (
+        _i32,
+        [_c_void_p, _c_void_p, _i32, _i64, _i32, _i32, _i32, _i32, _c_void_p, _i32,
+         _c_void_p, _c_void_p, _i32, _i32, _c_void_p, _c_void_p, _i64, _i64, _f32, _f32,
+         _i32, _c_void_p],
+    ),
+    "tks_paged_attention_decode_fp8": (
+        _i32,
+        [_c_void_p, _i64, _i64, _c_void_p, _c_void_p, _i32, _i64, _i32, _i32, _i32, _i32,
+         _c_void_p, _i32, _c_void_p, _c_void_p, _i32, _i32, _i32, _f32, _i32, _c_void_p,
+         _i64, _i64,
+         _c_void_p, _i64, _f32, _f32, _i32, _c_void_p],
+    ),
+    "tks_paged_attention_prefill_fp8": (
+        _i32,
+        [_c_void_p, _i64, _i64, _c_void_p, _c_void_p, _i32, _i64, _i32, _i32, _i32, _i32,
+         _c_void_p, _i32, _c_void_p, _c_void_p, _i32, _i64, _i32, _i32, _i32, _f32,
+         _c_void_p, _i64, _i64, _f32, _f32, _i32, _c_void_p],
+    ),
 }
 
 _lib: ctypes.CDLL | None = None

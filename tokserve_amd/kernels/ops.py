@@ -38,6 +38,28 @@ def _pool_shape(key_cache: torch.Tensor, value_cache: torch.Tensor) -> tuple[int
     return tuple(key_cache.shape)
 
 
+# K/V pools may hold OCP fp8 e4m3 with one fp32 scale per pool (stored =
+# e4m3(clamp(x / scale, -448, 448)), decoded = float(stored) * scale); every
+# other tensor of the call keeps a float dtype.
+FP8_POOL_DTYPE = torch.float8_e4m3fn
+
+
+def is_fp8_pool(pool: torch.Tensor) -> bool:
+    return pool.dtype == FP8_POOL_DTYPE
+
+
+def _pool_scales(pool: torch.Tensor, k_scale: float, v_scale: float) -> tuple[float, float]:
+    k_scale, v_scale = float(k_scale), float(v_scale)
+    if not is_fp8_pool(pool):
+        if k_scale != 1.0 or v_scale != 1.0:
+            raise ValueError("k_scale and v_scale apply to fp8 KV pools only")
+        return k_scale, v_scale
+    for name, value in (("k_scale", k_scale), ("v_scale", v_scale)):
+        if not (0.0 < value < float("inf")):
+            raise ValueError(f"{name} must be a positive finite float")
+    return k_scale, v_scale
+
+
 def _last_dim_contiguous(tensor: torch.Tensor, name: str) -> torch.Tensor:
     return tensor if tensor.stride(-1) == 1 else tensor.contiguous()
 
@@ -59,8 +81,15 @@ def kv_append(
     value_cache: torch.Tensor,
     slot_mapping: torch.Tensor,
     layer_index: int,
+    *,
+    k_scale: float = 1.0,
+    v_scale: float = 1.0,
 ) -> None:
-    """Scatter K/V rows (N, Hkv, Dh) into the pools at slot_mapping (int64, N)."""
+    """Scatter K/V rows (N, Hkv, Dh) into the pools at slot_mapping (int64, N).
+
+    fp8 pools quantize the rows with the pool scales (k_scale, v_scale); pools
+    in a float dtype take rows of that dtype, copied bit for bit.
+    """
 
     require_hip("kv_append", key, value, key_cache, value_cache, slot_mapping)
     num_layers, num_blocks, num_kv_heads, block_size, head_dim = _pool_shape(
@@ -70,13 +99,25 @@ def kv_append(
         raise ValueError("key and value must have shape (N, Hkv, Dh)")
     if key.shape[1:] != (num_kv_heads, head_dim):
         raise ValueError("key rows must match the pool's (Hkv, Dh)")
-    if key.dtype != key_cache.dtype or value.dtype != key_cache.dtype:
+    fp8 = is_fp8_pool(key_cache)
+    k_scale, v_scale = _pool_scales(key_cache, k_scale, v_scale)
+    if value.dtype != key.dtype or (not fp8 and key.dtype != key_cache.dtype):
         raise ValueError("keys and values must match the storage dtype")
     if slot_mapping.shape != (key.shape[0],):
         raise ValueError("slot_mapping must have shape (N,)")
     slots = _int_tensor(slot_mapping, torch.int64, "slot_mapping")
     key = _last_dim_contiguous(key, "key")
     value = _last_dim_contiguous(value, "value")
+    if fp8:
+        status = _lib.load().tks_kv_append_fp8(
+            key.data_ptr(), key.stride(0), key.stride(1),
+            value.data_ptr(), value.stride(0), value.stride(1),
+            key.shape[0], key_cache.data_ptr(), value_cache.data_ptr(),
+            num_layers, num_blocks, num_kv_heads, block_size, head_dim, layer_index,
+            slots.data_ptr(), k_scale, v_scale, _lib.dtype_code(key.dtype), _lib.stream_of(key),
+        )
+        _lib.check(status, "kv_append")
+        return
     status = _lib.load().tks_kv_append(
         key.data_ptr(), key.stride(0), key.stride(1),
         value.data_ptr(), value.stride(0), value.stride(1),
@@ -97,11 +138,15 @@ def paged_gather(
     max_seq_len: int,
     key_out: torch.Tensor,
     value_out: torch.Tensor,
+    *,
+    k_scale: float = 1.0,
+    v_scale: float = 1.0,
 ) -> None:
     """Copy each sequence's K/V in logical order into key_out/value_out.
 
     key_out/value_out are (S_total, Hkv, Dh) views (any token/head strides, Dh
     contiguous); sequence b fills rows cu_seqlens[b] .. cu_seqlens[b]+seq_lens[b]-1.
+    fp8 pools are decoded with their scales into the outputs' float dtype.
     """
 
     require_hip(
@@ -122,6 +167,20 @@ def paged_gather(
         raise ValueError("key_out and value_out must share shape and strides")
     if key_out.stride(-1) != 1:
         raise ValueError("outputs must be contiguous in head_dim")
+    fp8 = is_fp8_pool(key_cache)
+    k_scale, v_scale = _pool_scales(key_cache, k_scale, v_scale)
+    if value_out.dtype != key_out.dtype or (not fp8 and key_out.dtype != key_cache.dtype):
+        raise ValueError("outputs must match the storage dtype")
+    if fp8:
+        status = _lib.load().tks_paged_gather_fp8(
+            key_cache.data_ptr(), value_cache.data_ptr(), num_layers, num_blocks, num_kv_heads,
+            block_size, head_dim, layer_index, tables.data_ptr(), tables.shape[1],
+            lens.data_ptr(), cu.data_ptr(), tables.shape[0], max_seq_len,
+            key_out.data_ptr(), value_out.data_ptr(), key_out.stride(0), key_out.stride(1),
+            k_scale, v_scale, _lib.dtype_code(key_out.dtype), _lib.stream_of(key_cache),
+        )
+        _lib.check(status, "paged_gather")
+        return
     status = _lib.load().tks_paged_gather(
         key_cache.data_ptr(), value_cache.data_ptr(), num_layers, num_blocks, num_kv_heads,
         block_size, head_dim, layer_index, tables.data_ptr(), tables.shape[1],
@@ -194,6 +253,8 @@ def paged_attention_decode(
     workspace: torch.Tensor | None = None,
     pages_per_split: int = 0,
     seq_order: torch.Tensor | None = None,
+    k_scale: float = 1.0,
+    v_scale: float = 1.0,
 ) -> torch.Tensor:
     """One query token per sequence: query (B, Hq, Dh) -> out (B, Hq, Dh).
 
@@ -204,7 +265,8 @@ def paged_attention_decode(
     Launches that share a workspace must be ordered on one stream.
     `seq_order` (int32 permutation of 0..B-1, see longest_first) is the order in
     which sequences reach workgroups; longest-first avoids a tail of long
-    sequences. Results do not depend on it.
+    sequences. Results do not depend on it. fp8 pools are decoded with
+    (k_scale, v_scale).
     """
 
     require_hip("paged_attention_decode", query, key_cache, value_cache, block_tables, seq_lens)
@@ -213,7 +275,9 @@ def paged_attention_decode(
     )
     if query.ndim != 3 or query.shape[2] != head_dim:
         raise ValueError("query must have shape (B, Hq, Dh) with the pool's Dh")
-    if query.dtype != key_cache.dtype:
+    fp8 = is_fp8_pool(key_cache)
+    k_scale, v_scale = _pool_scales(key_cache, k_scale, v_scale)
+    if not fp8 and query.dtype != key_cache.dtype:
         raise ValueError("query and paged storage must use the same dtype")
     num_seqs, num_q_heads, _ = query.shape
     if num_q_heads % num_kv_heads != 0:
@@ -239,7 +303,7 @@ def paged_attention_decode(
     )
     if workspace is None:
         workspace = _workspace(query.device, nbytes)
-    status = library.tks_paged_attention_decode(
+    common = (
         query.data_ptr(), query.stride(0), query.stride(1),
         key_cache.data_ptr(), value_cache.data_ptr(), num_layers, num_blocks, num_kv_heads,
         block_size, head_dim, layer_index, tables.data_ptr(), tables.shape[1],
@@ -247,8 +311,15 @@ def paged_attention_decode(
         pages_per_split,
         out.data_ptr(), out.stride(0), out.stride(1),
         _lib.ptr(workspace), 0 if workspace is None else workspace.numel(),
-        _lib.dtype_code(query.dtype), _lib.stream_of(query),
     )
+    if fp8:
+        status = library.tks_paged_attention_decode_fp8(
+            *common, k_scale, v_scale, _lib.dtype_code(query.dtype), _lib.stream_of(query)
+        )
+    else:
+        status = library.tks_paged_attention_decode(
+            *common, _lib.dtype_code(query.dtype), _lib.stream_of(query)
+        )
     _lib.check(status, "paged_attention_decode")
     return out
 
@@ -266,12 +337,15 @@ def paged_attention_prefill(
     max_seq_len: int,
     scale: float | None = None,
     out: torch.Tensor | None = None,
+    k_scale: float = 1.0,
+    v_scale: float = 1.0,
 ) -> torch.Tensor:
     """Causal attention of packed query chunks (N, Hq, Dh) over their paged KV.
 
     Sequence b owns query rows cu_seqlens_q[b] .. cu_seqlens_q[b+1]-1; its
     seq_lens[b] keys already include those rows, so query i sits at absolute
-    position seq_lens[b] - q_len_b + i.
+    position seq_lens[b] - q_len_b + i. fp8 pools are decoded with
+    (k_scale, v_scale).
     """
 
     require_hip(
@@ -283,7 +357,9 @@ def paged_attention_prefill(
     )
     if query.ndim != 3 or query.shape[2] != head_dim:
         raise ValueError("query must have shape (N, Hq, Dh) with the pool's Dh")
-    if query.dtype != key_cache.dtype:
+    fp8 = is_fp8_pool(key_cache)
+    k_scale, v_scale = _pool_scales(key_cache, k_scale, v_scale)
+    if not fp8 and query.dtype != key_cache.dtype:
         raise ValueError("query and paged storage must use the same dtype")
     num_q_heads = query.shape[1]
     if num_q_heads % num_kv_heads != 0:
@@ -299,14 +375,21 @@ def paged_attention_prefill(
         out = torch.empty(query.shape, dtype=query.dtype, device=query.device)
     if scale is None:
         scale = 1.0 / sqrt(head_dim)
-    status = _lib.load().tks_paged_attention_prefill(
+    common = (
         query.data_ptr(), query.stride(0), query.stride(1),
         key_cache.data_ptr(), value_cache.data_ptr(), num_layers, num_blocks, num_kv_heads,
         block_size, head_dim, layer_index, tables.data_ptr(), tables.shape[1],
         lens.data_ptr(), cu.data_ptr(), num_seqs, query.shape[0], num_q_heads,
         max_query_len, max_seq_len, scale, out.data_ptr(), out.stride(0), out.stride(1),
-        _lib.dtype_code(query.dtype), _lib.stream_of(query),
     )
+    if fp8:
+        status = _lib.load().tks_paged_attention_prefill_fp8(
+            *common, k_scale, v_scale, _lib.dtype_code(query.dtype), _lib.stream_of(query)
+        )
+    else:
+        status = _lib.load().tks_paged_attention_prefill(
+            *common, _lib.dtype_code(query.dtype), _lib.stream_of(query)
+        )
     _lib.check(status, "paged_attention_prefill")
     return out
 

@@ -80,13 +80,13 @@ def hip_paged_attention(
     if query_length == 1:
         ops.paged_attention_decode(
             packed_query, storage.key_storage, storage.value_storage, block_table, seq_lens,
-            layer_index=layer_index, max_seq_len=visible, out=packed_out,
+            layer_index=layer_index, max_seq_len=visible, out=packed_out, **storage.scales,
         )
     else:
         ops.paged_attention_prefill(
             packed_query, storage.key_storage, storage.value_storage, block_table, seq_lens,
             cu_seqlens_q, layer_index=layer_index, max_query_len=query_length,
-            max_seq_len=visible, out=packed_out,
+            max_seq_len=visible, out=packed_out, **storage.scales,
         )
     return out
 

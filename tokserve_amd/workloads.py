@@ -37,6 +37,8 @@ class PagedBatch:
     cu_seqlens_q: torch.Tensor    # (B+1,) int32
     contexts: list[int]           # host copy of seq_lens
     query_lens: list[int]         # host copy of per-sequence query counts
+    k_scale: float = 1.0          # pool decode factors (fp8 pools)
+    v_scale: float = 1.0
 
     @property
     def num_seqs(self) -> int:
@@ -88,8 +90,15 @@ def paged_batch(
     seed: int,
     num_blocks: int | None = None,
     pool_on_device_rng: bool = False,
+    kv_dtype: torch.dtype | None = None,
+    k_scale: float = 1.0,
+    v_scale: float = 1.0,
 ) -> PagedBatch:
-    """Build a batch where sequence b has contexts[b] keys, the last query_lens[b] of them queried."""
+    """Build a batch where sequence b has contexts[b] keys, the last query_lens[b] of them queried.
+
+    kv_dtype=torch.float8_e4m3fn stores the (same) pools as fp8:
+    e4m3(clamp(x / scale, -448, 448)) with the given per-pool scales.
+    """
 
     device = torch.device(device)
     generator = torch.Generator().manual_seed(seed)
@@ -106,6 +115,13 @@ def paged_batch(
     else:
         key_cache = torch.randn(shape, generator=generator).to(dtype).to(device)
         value_cache = torch.randn(shape, generator=generator).to(dtype).to(device)
+    if kv_dtype is not None and kv_dtype != dtype:
+        if kv_dtype != torch.float8_e4m3fn:
+            raise ValueError("kv_dtype must be the batch dtype or torch.float8_e4m3fn")
+        key_cache = (key_cache.float() / k_scale).clamp(-448.0, 448.0).to(kv_dtype)
+        value_cache = (value_cache.float() / v_scale).clamp(-448.0, 448.0).to(kv_dtype)
+    else:
+        k_scale = v_scale = 1.0
     n_tokens = sum(query_lens)
     query = torch.randn((n_tokens, num_q_heads, head_dim), generator=generator).to(dtype)
     cu = torch.zeros(len(query_lens) + 1, dtype=torch.int32)
@@ -119,6 +135,8 @@ def paged_batch(
         cu_seqlens_q=cu.to(device),
         contexts=list(contexts),
         query_lens=list(query_lens),
+        k_scale=float(k_scale),
+        v_scale=float(v_scale),
     )
 
 
@@ -146,6 +164,20 @@ def decode_llama3_8b(
         contexts, [1] * num_seqs, num_q_heads=32, num_kv_heads=8, head_dim=128,
         block_size=16, dtype=torch.bfloat16, device=device, seed=seed + 7,
         pool_on_device_rng=torch.device(device).type == "cuda",
+    )
+
+
+def decode_llama3_8b_fp8(
+    device: torch.device | str, *, seed: int = 0, num_seqs: int = 256
+) -> PagedBatch:
+    """The Llama-3-8B decode workload with fp8 e4m3 K/V pools (scale 1: N(0, 1) values)."""
+
+    gen = torch.Generator().manual_seed(seed)
+    contexts = log_uniform_contexts(num_seqs, 128, 8192, gen)
+    return paged_batch(
+        contexts, [1] * num_seqs, num_q_heads=32, num_kv_heads=8, head_dim=128,
+        block_size=16, dtype=torch.bfloat16, device=device, seed=seed + 7,
+        pool_on_device_rng=torch.device(device).type == "cuda", kv_dtype=torch.float8_e4m3fn,
     )
 
 
