@@ -30,10 +30,11 @@ TRAFFIC_FILE = ROOT / "profiles" / "decode_llama3_8b_traffic.txt"
 
 
 def algorithmic_bytes(batch) -> int:
+    """Every visible K/V byte once, Q in and O out, block ids and lengths."""
+
     _, _, hkv, _, dh = batch.key_cache.shape
-    elem = batch.key_cache.element_size()
-    kv = sum(batch.contexts) * hkv * dh * 2 * elem
-    qo = 2 * batch.query.numel() * elem
+    kv = sum(batch.contexts) * hkv * dh * 2 * batch.key_cache.element_size()
+    qo = 2 * batch.query.numel() * batch.query.element_size()
     tables = sum((c + 15) // 16 for c in batch.contexts) * 4
     return kv + qo + tables + 4 * batch.num_seqs
 
@@ -188,6 +189,7 @@ def main() -> int:
             "mixed_step": measure_mixed(device, 20, 5),
             "norm_rope": measure_norm_rope(device, 20, 5),
             "small_fp32_step": measure_small_fp32_step(device, 50, 10),
+            "decode_fp8_kv": measure_decode_fp8(device, args.seed, 50, 10),
         }
     if not args.no_e2e:
         e2e = measure_e2e(device, args.seed,
@@ -268,6 +270,38 @@ def measure_mixed(device, steps: int, warmup: int) -> dict:
         "prefill_mfma_frac_of_2500_tflops": round(flops / (ms_pre * 1e-3) / 2.5e15, 4),
         "decode_ms": round(ms_dec, 5),
         "decode_gbps": round(dec_bytes / (ms_dec * 1e-3) / 1e9, 1),
+    }
+
+
+def measure_decode_fp8(device, seed: int, steps: int, warmup: int) -> dict:
+    """The headline decode workload with fp8 e4m3 K/V pools (bf16 queries and output):
+    half the K/V bytes per decode token."""
+
+    import torch
+
+    from tokserve_amd import workloads
+    from tokserve_amd.kernels import ops
+
+    batch = workloads.decode_llama3_8b_fp8(device, seed=seed)
+    out = torch.empty_like(batch.query)
+    order = ops.longest_first(batch.contexts, device)
+
+    def step() -> None:
+        ops.paged_attention_decode(
+            batch.query, batch.key_cache, batch.value_cache, batch.block_tables,
+            batch.seq_lens, layer_index=0, max_seq_len=batch.max_seq_len, out=out,
+            seq_order=order, k_scale=batch.k_scale, v_scale=batch.v_scale)
+
+    ms = _time_ms(step, steps, warmup)
+    nbytes = algorithmic_bytes(batch)
+    return {
+        "workload": "decode_llama3_8b_fp8: the headline decode batch (256 seqs, ctx "
+                    "log-uniform [128, 8192], Hq 32 / Hkv 8, Dh 128, block 16) with e4m3 K/V "
+                    "pools, bf16 queries",
+        "ms_per_step": round(ms, 5),
+        "algorithmic_bytes": nbytes,
+        "gbps": round(nbytes / (ms * 1e-3) / 1e9, 1),
+        "decode_tokens_per_s_one_layer": round(batch.num_seqs / (ms * 1e-3), 1),
     }
 
 

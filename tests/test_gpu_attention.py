@@ -241,3 +241,45 @@ def test_mixed_step_subset_matches_oracle(device) -> None:
     torch.cuda.synchronize()
     _assert_parity(out_p, _prefill_oracle, prefill)
     _assert_parity(out_d, _decode_oracle, decode)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize(("hq", "hkv", "dh"), [(32, 8, 128), (32, 4, 64), (4, 2, 16)])
+@pytest.mark.parametrize("pages_per_split", [0, 1])
+def test_nan_in_unwritten_pool_rows_never_reaches_the_output(device, dtype, hq, hkv, dh,
+                                                             pages_per_split) -> None:
+    """Pool rows no sequence has written (the tail of each last page, other blocks) hold
+    NaN: the reference reads only the valid keys (masked loads,
+    tokserve/kernels/_triton_paged_attention.py:76-99), so decode and prefill stay finite
+    and equal the oracle on the written rows."""
+
+    contexts, query_lens = [1, 17, 35, 100], [1, 5, 35, 16]
+    batch = workloads.paged_batch(contexts, query_lens, num_q_heads=hq, num_kv_heads=hkv,
+                                  head_dim=dh, block_size=16, dtype=dtype, device=device,
+                                  seed=dh + hq)
+    tables = batch.block_tables.cpu()
+    valid = torch.zeros(batch.key_cache.shape[1], 16, dtype=torch.bool)
+    for b, ctx in enumerate(contexts):
+        for pos in range(ctx):
+            valid[int(tables[b, pos // 16]), pos % 16] = True
+    mask = valid.view(1, -1, 1, 16, 1).to(device)
+    nan = torch.tensor(float("nan"), dtype=dtype, device=device)
+    batch.key_cache.copy_(torch.where(mask, batch.key_cache, nan))
+    batch.value_cache.copy_(torch.where(mask, batch.value_cache, nan))
+    q_rows = torch.tensor([sum(query_lens[: b + 1]) - 1 for b in range(4)], device=device)
+    decode = ops.paged_attention_decode(
+        batch.query[q_rows], batch.key_cache, batch.value_cache, batch.block_tables,
+        batch.seq_lens, layer_index=0, max_seq_len=batch.max_seq_len,
+        pages_per_split=pages_per_split)
+    prefill = ops.paged_attention_prefill(
+        batch.query, batch.key_cache, batch.value_cache, batch.block_tables, batch.seq_lens,
+        batch.cu_seqlens_q, layer_index=0, max_query_len=batch.max_query_len,
+        max_seq_len=batch.max_seq_len)
+    torch.cuda.synchronize()
+    assert torch.isfinite(decode.float()).all() and torch.isfinite(prefill.float()).all()
+    q, kc, vc, bt, lens, cu = _cpu(batch)
+    tol = TOL[torch.float32] if dtype == torch.float32 else dict(rtol=0, atol=2e-2)
+    compute = None if dtype == torch.float32 else torch.float32
+    assert_close(decode.cpu(), paged.decode_batch(q[q_rows.cpu()], kc, vc, bt, lens, 0, compute),
+                 **tol)
+    assert_close(prefill.cpu(), paged.prefill_batch(q, kc, vc, bt, lens, cu, 0, compute), **tol)

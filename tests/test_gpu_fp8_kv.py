@@ -212,3 +212,42 @@ def test_fp8_storage_round_trip_and_scale_checks(device) -> None:
                       torch.empty(1, 1, 2, 4, 32, dtype=torch.bfloat16, device=device),
                       torch.empty(1, 1, 2, 4, 32, dtype=torch.bfloat16, device=device),
                       torch.zeros(1, dtype=torch.int64, device=device), 0, k_scale=2.0)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_fp8_nan_codes_in_unwritten_rows_are_never_read(device, dtype) -> None:
+    """Tail rows of the last pages hold the e4m3 NaN code: decode (MFMA and split) and
+    prefill stay finite and equal the decoded-pool oracle on the written rows."""
+
+    contexts, query_lens = [1, 17, 35, 100], [1, 5, 35, 16]
+    batch = workloads.paged_batch(contexts, query_lens, num_q_heads=32, num_kv_heads=8,
+                                  head_dim=128, block_size=16, dtype=dtype, device=device,
+                                  seed=5, kv_dtype=FP8, k_scale=0.5, v_scale=2.0)
+    tables = batch.block_tables.cpu()
+    valid = torch.zeros(batch.key_cache.shape[1], 16, dtype=torch.bool)
+    for b, ctx in enumerate(contexts):
+        for pos in range(ctx):
+            valid[int(tables[b, pos // 16]), pos % 16] = True
+    mask = valid.view(1, -1, 1, 16, 1).to(device)
+    for pool in (batch.key_cache, batch.value_cache):
+        raw = pool.view(torch.uint8)
+        raw.copy_(torch.where(mask, raw, torch.tensor(0x7F, dtype=torch.uint8, device=device)))
+    q_rows = torch.tensor([sum(query_lens[: b + 1]) - 1 for b in range(4)], device=device)
+    outs = [ops.paged_attention_decode(
+        batch.query[q_rows], batch.key_cache, batch.value_cache, batch.block_tables,
+        batch.seq_lens, layer_index=0, max_seq_len=batch.max_seq_len, pages_per_split=pps,
+        k_scale=batch.k_scale, v_scale=batch.v_scale) for pps in (0, 1)]
+    prefill = ops.paged_attention_prefill(
+        batch.query, batch.key_cache, batch.value_cache, batch.block_tables, batch.seq_lens,
+        batch.cu_seqlens_q, layer_index=0, max_query_len=batch.max_query_len,
+        max_seq_len=batch.max_seq_len, k_scale=batch.k_scale, v_scale=batch.v_scale)
+    torch.cuda.synchronize()
+    kc, vc = _decoded(batch)
+    q = batch.query.cpu()
+    expected = paged.decode_batch(q[q_rows.cpu()], kc, vc, batch.block_tables.cpu(),
+                                  batch.seq_lens.cpu(), 0, torch.float32)
+    for out in outs:
+        assert torch.isfinite(out.float()).all()
+        assert_close(out.cpu(), expected, **TOL[dtype])
+    assert torch.isfinite(prefill.float()).all()
+    assert_close(prefill.cpu(), _prefill_expected(batch), **TOL[dtype])

@@ -200,6 +200,15 @@ __global__ __launch_bounds__(64 * kWaves) void decode_mfma_kernel(DecodeArgs a) 
     float vf[4][8];
 #pragma unroll
     for (int j = 0; j < 4; ++j) IO::v_floats(vr[j], vf[j]);
+    if ((p + 1) * BS > len) {
+      // The sequence's last page: rows past the last key hold whatever the pool
+      // has there. Their probabilities are 0, and 0 * NaN would not be.
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        if (p * BS + tg * 4 + j >= len)
+#pragma unroll
+          for (int d = 0; d < 8; ++d) vf[j][d] = 0.f;
+    }
 #pragma unroll
     for (int j = 0; j < HPL; ++j) {
       const int h = hg * HPL + j;
