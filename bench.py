@@ -187,6 +187,7 @@ def main() -> int:
     if not args.no_secondary:
         result["secondary"] = {
             "mixed_step": measure_mixed(device, 20, 5),
+            "mixed_step_fp8_kv": measure_mixed(device, 20, 5, kv_dtype=torch.float8_e4m3fn),
             "norm_rope": measure_norm_rope(device, 20, 5),
             "small_fp32_step": measure_small_fp32_step(device, 50, 10),
             "decode_fp8_kv": measure_decode_fp8(device, args.seed, 50, 10),
@@ -196,6 +197,9 @@ def main() -> int:
                           None if args.no_cpu_baseline else args.cpu_seconds)
         result["decode_tokens_per_s_e2e"] = e2e["tokens_per_s"]
         result.setdefault("secondary", {})["e2e_tinyllama"] = e2e
+        if not args.no_secondary:
+            result["secondary"]["e2e_tinyllama_fp8_kv"] = measure_e2e(
+                device, args.seed, None, kv_dtype=torch.float8_e4m3fn)
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(batch, args.cpu_seconds)
     print(json.dumps(result), flush=True)
@@ -222,16 +226,18 @@ def _time_ms(fn, steps: int, warmup: int) -> float:
     return start.elapsed_time(end) / steps
 
 
-def measure_mixed(device, steps: int, warmup: int) -> dict:
+def measure_mixed(device, steps: int, warmup: int, kv_dtype=None) -> dict:
     """Mixed chunked-prefill + decode step (Llama-3-8B layer shape, bf16): 16 chunks of
-    512 tokens on prior contexts U[0, 2048] and 240 decodes on contexts U[256, 4096]."""
+    512 tokens on prior contexts U[0, 2048] and 240 decodes on contexts U[256, 4096].
+    kv_dtype torch.float8_e4m3fn: the same step over fp8 pools (scale 1)."""
 
     import torch
 
     from tokserve_amd import workloads
     from tokserve_amd.kernels import ops
 
-    pre, dec = workloads.mixed_llama3_8b(device, seed=0)
+    pre, dec = workloads.mixed_llama3_8b(device, seed=0, kv_dtype=kv_dtype)
+    scales = {"k_scale": pre.k_scale, "v_scale": pre.v_scale}
     out_p = torch.empty_like(pre.query)
     out_d = torch.empty_like(dec.query)
     order = ops.longest_first(dec.contexts, device)
@@ -240,12 +246,12 @@ def measure_mixed(device, steps: int, warmup: int) -> dict:
         ops.paged_attention_prefill(
             pre.query, pre.key_cache, pre.value_cache, pre.block_tables, pre.seq_lens,
             pre.cu_seqlens_q, layer_index=0, max_query_len=pre.max_query_len,
-            max_seq_len=pre.max_seq_len, out=out_p)
+            max_seq_len=pre.max_seq_len, out=out_p, **scales)
 
     def decode() -> None:
         ops.paged_attention_decode(
             dec.query, dec.key_cache, dec.value_cache, dec.block_tables, dec.seq_lens,
-            layer_index=0, max_seq_len=dec.max_seq_len, out=out_d, seq_order=order)
+            layer_index=0, max_seq_len=dec.max_seq_len, out=out_d, seq_order=order, **scales)
 
     def step() -> None:
         prefill()
@@ -260,10 +266,12 @@ def measure_mixed(device, steps: int, warmup: int) -> dict:
         prior = ctx - ql
         visible = ql * prior + ql * (ql + 1) // 2  # sum over queries of (prior + i + 1)
         flops += 4 * hq * dh * visible
-    dec_bytes = sum(dec.contexts) * 8 * dh * 2 * 2 + 2 * dec.query.numel() * 2
+    dec_bytes = (sum(dec.contexts) * 8 * dh * 2 * dec.key_cache.element_size()
+                 + 2 * dec.query.numel() * 2)
     return {
         "workload": "mixed_llama3_8b: 16 x 512-token prefill chunks (prior U[0,2048]) + 240 "
-                    "decodes (ctx U[256,4096]), Hq 32 / Hkv 8, Dh 128, block 16, bf16",
+                    "decodes (ctx U[256,4096]), Hq 32 / Hkv 8, Dh 128, block 16, bf16"
+                    + ("" if kv_dtype is None else "; fp8 e4m3 K/V pools"),
         "ms_per_step": round(ms_step, 5),
         "prefill_ms": round(ms_pre, 5),
         "prefill_tflops": round(flops / (ms_pre * 1e-3) / 1e12, 2),
@@ -396,7 +404,7 @@ def measure_norm_rope(device, steps: int, warmup: int) -> dict:
     }
 
 
-def _e2e_engine(model, specs, device, block_size: int = 16):
+def _e2e_engine(model, specs, device, block_size: int = 16, kv_dtype=None):
     import torch
 
     from tokserve_amd import workloads
@@ -410,7 +418,8 @@ def _e2e_engine(model, specs, device, block_size: int = 16):
     manager = PagedKVCacheManager(
         num_layers=config.num_hidden_layers, num_blocks=workloads.pool_blocks(specs, block_size),
         num_key_value_heads=config.num_key_value_heads, block_size=block_size,
-        head_dim=config.head_dim, device=device, dtype=model.embed_tokens.weight.dtype)
+        head_dim=config.head_dim, device=device, dtype=model.embed_tokens.weight.dtype,
+        kv_dtype=kv_dtype)
     scheduler = RequestScheduler(max_running_requests=128, cache_manager=manager)
     for spec in specs:
         prompt = torch.tensor([spec.prompt], dtype=torch.int64, device=device)
@@ -419,11 +428,12 @@ def _e2e_engine(model, specs, device, block_size: int = 16):
     return ContinuousBatchEngine(model, scheduler, manager)
 
 
-def measure_e2e(device, seed: int, cpu_seconds: float | None) -> dict:
+def measure_e2e(device, seed: int, cpu_seconds: float | None, kv_dtype=None) -> dict:
     """TinyLlama-1.1B (random init, bf16) serving 128 requests, prompts U[64, 1024],
     128 greedy tokens each, block size 16, max 128 running: the whole run through the
     continuous-batching engine, timed on the host wall clock (each step ends with its
-    tokens on the host). tokens/s = generated tokens / wall time."""
+    tokens on the host). tokens/s = generated tokens / wall time. kv_dtype
+    torch.float8_e4m3fn runs the same workload over fp8 K/V pools (scale 1)."""
 
     import torch
 
@@ -437,10 +447,13 @@ def measure_e2e(device, seed: int, cpu_seconds: float | None) -> dict:
         model = LlamaModel(config)
     model = model.to(torch.bfloat16).eval()
     specs = workloads.tinyllama_requests(seed=seed)
-    warm = workloads.tinyllama_requests(seed=seed + 1, num_requests=8, max_new_tokens=4)
-    _e2e_engine(model, warm, device).run_until_idle()
+    # Warm-up at the timed run's shapes (a full-size prefill iteration and two decode
+    # iterations of another request set): library GEMM kernels for those shapes load
+    # here, not in the timed run.
+    warm = workloads.tinyllama_requests(seed=seed + 1, max_new_tokens=2)
+    _e2e_engine(model, warm, device, kv_dtype=kv_dtype).run_until_idle()
     torch.cuda.synchronize()
-    engine = _e2e_engine(model, specs, device)
+    engine = _e2e_engine(model, specs, device, kv_dtype=kv_dtype)
     step_s = []
     start = time.perf_counter()
     while engine.scheduler.waiting_count or engine.scheduler.running_count:
@@ -457,10 +470,11 @@ def measure_e2e(device, seed: int, cpu_seconds: float | None) -> dict:
     if graphs is not None and graphs._graphs:
         captured = graphs._graphs[max(graphs._graphs)]
         replay_ms = _time_ms(captured.graph.replay, 20, 3)
+    pools = "" if kv_dtype is None else "; fp8 e4m3 K/V pools"
     result = {
         "workload": "e2e_tinyllama: TinyLlama-1.1B shape (22 layers, hidden 2048, 32/4 heads, "
                     "Dh 64, MLP 5632, vocab 32000), random init, bf16; 128 requests, prompts "
-                    "U[64,1024], 128 greedy tokens, block 16, max_running 128",
+                    "U[64,1024], 128 greedy tokens, block 16, max_running 128" + pools,
         "requests": len(specs),
         "prompt_tokens": sum(len(s.prompt) for s in specs),
         "generated_tokens": generated,

@@ -213,7 +213,21 @@ int32_t tks_paged_attention_decode_fp8(
     void *workspace, int64_t workspace_bytes, float k_scale, float v_scale, int32_t dtype,
     tks_stream_t stream);
 
-/* Chunked-prefill attention over fp8 pools (tks_paged_attention_prefill). */
+/* Chunked-prefill attention over fp8 pools (tks_paged_attention_prefill).
+ * For shapes the MFMA prefill kernel serves (bf16/fp16 queries, Dh 64/128,
+ * block size a multiple of 16), the pages the batch reads are first decoded
+ * into a caller-owned workspace (a dense [num_seqs * block_table_stride] page
+ * pool in `dtype` plus its identity block table); its size comes from
+ * tks_paged_attention_prefill_fp8_workspace_bytes with the same shapes (0: no
+ * workspace needed, the VALU kernel reads the fp8 pool directly). The
+ * workspace must be 16-byte aligned; no initial contents are required;
+ * launches sharing it must be stream-ordered. */
+int64_t tks_paged_attention_prefill_fp8_workspace_bytes(int32_t num_seqs, int32_t num_q_heads,
+                                                        int32_t num_kv_heads, int32_t head_dim,
+                                                        int32_t block_size,
+                                                        int32_t block_table_stride,
+                                                        int32_t max_seq_len, int32_t dtype);
+
 int32_t tks_paged_attention_prefill_fp8(
     const void *query, int64_t q_token_stride, int64_t q_head_stride, const void *key_cache,
     const void *value_cache, int32_t num_layers, int64_t num_blocks, int32_t num_kv_heads,
@@ -221,7 +235,8 @@ int32_t tks_paged_attention_prefill_fp8(
     int32_t block_table_stride, const int32_t *seq_lens, const int32_t *cu_seqlens_q,
     int32_t num_seqs, int64_t num_tokens, int32_t num_q_heads, int32_t max_query_len,
     int32_t max_seq_len, float scale, void *out, int64_t out_token_stride,
-    int64_t out_head_stride, float k_scale, float v_scale, int32_t dtype, tks_stream_t stream);
+    int64_t out_head_stride, void *workspace, int64_t workspace_bytes, float k_scale,
+    float v_scale, int32_t dtype, tks_stream_t stream);
 
 /* ------------------------------------------------------------------------
  * RMSNorm over the last dimension.

@@ -167,10 +167,13 @@ def test_fp8_decode_split_k(device, dtype, pages_per_split) -> None:
     assert_close(out.cpu(), _decode_expected(batch), **TOL[dtype])
 
 
-@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
 @pytest.mark.parametrize(("hq", "hkv", "dh", "bs"), [(32, 8, 128, 16), (8, 2, 64, 32),
                                                      (4, 4, 16, 5)])
 def test_fp8_prefill_matches_decoded_pool_oracle(device, dtype, hq, hkv, dh, bs) -> None:
+    """bf16/fp16 at Dh 64/128 with block sizes 16 and 32: pages decoded into the scratch
+    pool, then the MFMA kernel; the rest (fp32, Dh 16, block size 5): the VALU kernel on
+    the fp8 pool."""
     contexts = [7, 64, 300, 33]
     query_lens = [7, 20, 128, 1]
     batch = workloads.paged_batch(contexts, query_lens, num_q_heads=hq, num_kv_heads=hkv,

@@ -37,3 +37,20 @@ def test_rotary_table_matches_reference_formula() -> None:
     assert torch.equal(table.cos[3], (3.0 * inv).cos())
     table.ensure(12)
     assert table.length >= 12
+
+
+def test_workspace_growth_keeps_replaced_buffers_alive() -> None:
+    """A grown workspace never frees the old buffer (a captured graph may still hold its
+    address), and different uses do not share one buffer."""
+
+    cpu = torch.device("cpu")
+    key = "test-growth"
+    first = ops._workspace(cpu, 100, key)
+    assert first is not None and first.numel() >= 100
+    assert ops._workspace(cpu, 50, key) is first
+    grown = ops._workspace(cpu, first.numel() + 1, key)
+    assert grown is not first and grown.numel() >= 2 * first.numel()
+    assert any(t is first for t in ops._retired)
+    other = ops._workspace(cpu, 10, key + "-other")
+    assert other is not grown
+    assert ops._workspace(cpu, 0, key) is None

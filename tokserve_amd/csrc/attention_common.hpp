@@ -101,7 +101,7 @@ struct DecodeArgs {
   void *out;
   int64_t o_ss, o_hs;
   float *ws_m, *ws_l, *ws_acc;
-  float v_scale;  // V decode factor of fp8 pools (1 otherwise)
+  float v_scale = 1.f;  // V decode factor of fp8 pools (1 otherwise)
 };
 
 struct PrefillArgs {
@@ -120,6 +120,7 @@ struct PrefillArgs {
   int32_t num_kv_heads;
   int32_t num_pairs;  // sequences * KV heads
   int32_t tiles;      // query tiles per (sequence, KV head): ceil(max_query_len / tile)
+  float v_scale = 1.f;  // V decode factor (pages decoded from fp8 pools; 1 otherwise)
 };
 
 // 16-key pages of one sequence the MFMA prefill kernel holds in LDS: it serves

@@ -55,7 +55,7 @@ struct GenericArgs {
   int64_t o_rs, o_hs;
   float *ws_m, *ws_l, *ws_acc;
   int32_t vec_rows;  // K/V rows are 16-byte aligned and head_dim is a multiple of 16 bytes
-  float v_scale;     // V decode factor of fp8 pools (1 otherwise)
+  float v_scale = 1.f;  // V decode factor of fp8 pools (1 otherwise)
 };
 
 // The split's keys are dealt to the four waves 64 at a time (wave w takes keys
@@ -270,6 +270,67 @@ __global__ __launch_bounds__(kGenThreads) void attn_generic_kernel(GenericArgs a
       a.ws_acc[w * DH + d] = o * a.v_scale;
     }
   }
+}
+
+// ------------------------------------------------------------------------
+// fp8 pools under the MFMA prefill: the pages a batch reads are decoded once
+// into a dense scratch pool, page (b, p) at block b * W + p (W = the table
+// width), with the identity table beside it. The scales are not applied here
+// (k_scale rides on the score scale, v_scale on the output), so the scratch
+// holds the exact e4m3 values in T.
+// ------------------------------------------------------------------------
+
+struct ScratchPages {
+  void *k, *v;
+  int32_t *table;
+  int64_t bytes;
+};
+
+ScratchPages carve_pages(void *ws, int32_t num_seqs, int32_t table_width, int32_t num_kv_heads,
+                         int32_t block_size, int32_t head_dim) {
+  const int64_t pages = static_cast<int64_t>(num_seqs) * table_width;
+  const int64_t pool = ceil_div(pages * num_kv_heads * block_size * head_dim * 2, 256) * 256;
+  const int64_t table = ceil_div(pages * 4, 256) * 256;
+  char *base = static_cast<char *>(ws);
+  ScratchPages s;
+  s.k = base;
+  s.v = base ? base + pool : nullptr;
+  s.table = base ? reinterpret_cast<int32_t *>(base + 2 * pool) : nullptr;
+  s.bytes = 2 * pool + table;
+  return s;
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void decode_pages_kernel(
+    const fp8e4m3_t *__restrict__ kc, const fp8e4m3_t *__restrict__ vc, PoolView pool,
+    int32_t num_kv_heads, const int32_t *__restrict__ bt, int32_t bt_stride,
+    const int32_t *__restrict__ seq_lens, int32_t num_seqs, T *__restrict__ k_out,
+    T *__restrict__ v_out, int32_t *__restrict__ table_out) {
+  const int64_t chunks = static_cast<int64_t>(pool.block_size) * pool.head_dim / 16;
+  const int64_t per_page = chunks * num_kv_heads;
+  const int64_t item = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  const int64_t slot = item / per_page;  // b * W + p
+  if (slot >= static_cast<int64_t>(num_seqs) * bt_stride) return;
+  const int b = static_cast<int>(slot / bt_stride);
+  const int p = static_cast<int>(slot - static_cast<int64_t>(b) * bt_stride);
+  const int64_t rem = item - slot * per_page;
+  const int h = static_cast<int>(rem / chunks);
+  const int64_t c = (rem - h * chunks) * 16;
+  if (rem == 0) table_out[slot] = static_cast<int32_t>(slot);
+  const int64_t len = min(static_cast<int64_t>(max(seq_lens[b], 0)),
+                          static_cast<int64_t>(bt_stride) * pool.block_size);
+  if (p * static_cast<int64_t>(pool.block_size) >= len) return;
+  const int64_t blk = block_of(bt + static_cast<int64_t>(b) * bt_stride, p, pool.num_blocks);
+  const int64_t src = pool.layer_base + blk * pool.block_stride + h * pool.head_stride + c;
+  const int64_t dst = slot * pool.block_stride + h * pool.head_stride + c;
+  float f[16];
+  constexpr int N = Vec<T>::N;
+  unpack<fp8e4m3_t>(ld16(kc + src), f);
+#pragma unroll
+  for (int i = 0; i < 16; i += N) st16(k_out + dst + i, pack<T>(f + i));
+  unpack<fp8e4m3_t>(ld16(vc + src), f);
+#pragma unroll
+  for (int i = 0; i < 16; i += N) st16(v_out + dst + i, pack<T>(f + i));
 }
 
 // ------------------------------------------------------------------------
@@ -500,8 +561,8 @@ int32_t prefill_impl(const void *query, int64_t q_token_stride, int64_t q_head_s
                      const int32_t *cu_seqlens_q, int32_t num_seqs, int64_t num_tokens,
                      int32_t num_q_heads, int32_t max_query_len, int32_t max_seq_len,
                      float scale, void *out, int64_t out_token_stride, int64_t out_head_stride,
-                     bool fp8_pools, float k_scale, float v_scale, int32_t dtype,
-                     tks_stream_t stream) {
+                     bool fp8_pools, void *workspace, int64_t workspace_bytes, float k_scale,
+                     float v_scale, int32_t dtype, tks_stream_t stream) {
   if (!valid_dtype(dtype)) return TKS_ERR_TYPE;
   if (!pool_ok(num_layers, num_blocks, num_kv_heads, block_size, head_dim) || num_seqs < 0 ||
       num_tokens < 0 || num_q_heads <= 0 || num_q_heads % num_kv_heads != 0 ||
@@ -523,14 +584,44 @@ int32_t prefill_impl(const void *query, int64_t q_token_stride, int64_t q_head_s
   // One split covering the whole key range: no partials, no workspace.
   const int32_t pps = static_cast<int32_t>(ceil_div(max_seq_len > 0 ? max_seq_len : 1, block_size));
   const int32_t key_cap = std::min(block_table_stride, pps) * block_size;
-  if (!fp8_pools &&
-      prefill_mfma_supported(dtype, head_dim, G, key_cap, block_size, num_blocks, num_kv_heads) &&
-      aligned16(query) &&
-      aligned16(key_cache) && aligned16(value_cache) && q_token_stride % 8 == 0 &&
-      q_head_stride % 8 == 0) {
+  const int64_t scratch_blocks = static_cast<int64_t>(num_seqs) * block_table_stride;
+  const bool mfma_shape =
+      prefill_mfma_supported(dtype, head_dim, G, key_cap, block_size,
+                             fp8_pools ? scratch_blocks : num_blocks, num_kv_heads) &&
+      aligned16(query) && aligned16(key_cache) && aligned16(value_cache) &&
+      q_token_stride % 8 == 0 && q_head_stride % 8 == 0;
+  if (mfma_shape && !fp8_pools) {
     PrefillArgs p{query,    q_token_stride, q_head_stride, key_cache,    value_cache,
                   pool,     block_tables,   block_table_stride, seq_lens, cu_seqlens_q,
                   scale_log2, key_cap,      out,           out_token_stride, out_head_stride};
+    return launch_prefill_mfma(p, dtype, num_seqs, num_kv_heads, G, head_dim, max_query_len, s);
+  }
+  if (mfma_shape) {
+    // fp8 pools: decode the batch's pages into the scratch pool, then the MFMA
+    // kernel reads it through the identity table.
+    const ScratchPages sp =
+        carve_pages(workspace, num_seqs, block_table_stride, num_kv_heads, block_size, head_dim);
+    if (workspace == nullptr || workspace_bytes < sp.bytes || !aligned16(workspace))
+      return TKS_ERR_WORKSPACE;
+    const int64_t items = scratch_blocks * num_kv_heads * block_size * head_dim / 16;
+    const dim3 grid(static_cast<unsigned>(ceil_div(items, 256)));
+    const fp8e4m3_t *k8 = static_cast<const fp8e4m3_t *>(key_cache);
+    const fp8e4m3_t *v8 = static_cast<const fp8e4m3_t *>(value_cache);
+    if (dtype == TKS_BFLOAT16)
+      decode_pages_kernel<bf16_t><<<grid, 256, 0, s>>>(
+          k8, v8, pool, num_kv_heads, block_tables, block_table_stride, seq_lens, num_seqs,
+          static_cast<bf16_t *>(sp.k), static_cast<bf16_t *>(sp.v), sp.table);
+    else
+      decode_pages_kernel<_Float16><<<grid, 256, 0, s>>>(
+          k8, v8, pool, num_kv_heads, block_tables, block_table_stride, seq_lens, num_seqs,
+          static_cast<_Float16 *>(sp.k), static_cast<_Float16 *>(sp.v), sp.table);
+    const int32_t st = check_launch();
+    if (st != TKS_OK) return st;
+    const PoolView scratch = make_pool(0, scratch_blocks, num_kv_heads, block_size, head_dim);
+    PrefillArgs p{query,    q_token_stride, q_head_stride, sp.k,        sp.v,
+                  scratch,  sp.table,       block_table_stride, seq_lens, cu_seqlens_q,
+                  scale_log2, key_cap,      out,           out_token_stride, out_head_stride};
+    p.v_scale = v_scale;
     return launch_prefill_mfma(p, dtype, num_seqs, num_kv_heads, G, head_dim, max_query_len, s);
   }
   const int kv_elem = fp8_pools ? 1 : elem_bytes(dtype);
@@ -588,7 +679,24 @@ extern "C" int32_t tks_paged_attention_prefill(
                       num_blocks, num_kv_heads, block_size, head_dim, layer_index, block_tables,
                       block_table_stride, seq_lens, cu_seqlens_q, num_seqs, num_tokens,
                       num_q_heads, max_query_len, max_seq_len, scale, out, out_token_stride,
-                      out_head_stride, false, 1.f, 1.f, dtype, stream);
+                      out_head_stride, false, nullptr, 0, 1.f, 1.f, dtype, stream);
+}
+
+extern "C" int64_t tks_paged_attention_prefill_fp8_workspace_bytes(
+    int32_t num_seqs, int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+    int32_t block_size, int32_t block_table_stride, int32_t max_seq_len, int32_t dtype) {
+  if (num_seqs < 0 || num_q_heads <= 0 || num_kv_heads <= 0 || head_dim <= 0 ||
+      block_size <= 0 || block_table_stride < 0 || max_seq_len < 0 ||
+      num_q_heads % num_kv_heads != 0 || !valid_dtype(dtype))
+    return -1;
+  const int32_t pps = static_cast<int32_t>(ceil_div(max_seq_len > 0 ? max_seq_len : 1, block_size));
+  const int32_t key_cap = std::min(block_table_stride, pps) * block_size;
+  const int64_t scratch_blocks = static_cast<int64_t>(num_seqs) * block_table_stride;
+  if (!prefill_mfma_supported(dtype, head_dim, num_q_heads / num_kv_heads, key_cap, block_size,
+                              scratch_blocks, num_kv_heads))
+    return 0;
+  return carve_pages(nullptr, num_seqs, block_table_stride, num_kv_heads, block_size, head_dim)
+      .bytes;
 }
 
 extern "C" int32_t tks_paged_attention_prefill_fp8(
@@ -598,10 +706,12 @@ extern "C" int32_t tks_paged_attention_prefill_fp8(
     int32_t block_table_stride, const int32_t *seq_lens, const int32_t *cu_seqlens_q,
     int32_t num_seqs, int64_t num_tokens, int32_t num_q_heads, int32_t max_query_len,
     int32_t max_seq_len, float scale, void *out, int64_t out_token_stride,
-    int64_t out_head_stride, float k_scale, float v_scale, int32_t dtype, tks_stream_t stream) {
+    int64_t out_head_stride, void *workspace, int64_t workspace_bytes, float k_scale,
+    float v_scale, int32_t dtype, tks_stream_t stream) {
   return prefill_impl(query, q_token_stride, q_head_stride, key_cache, value_cache, num_layers,
                       num_blocks, num_kv_heads, block_size, head_dim, layer_index, block_tables,
                       block_table_stride, seq_lens, cu_seqlens_q, num_seqs, num_tokens,
                       num_q_heads, max_query_len, max_seq_len, scale, out, out_token_stride,
-                      out_head_stride, true, k_scale, v_scale, dtype, stream);
+                      out_head_stride, true, workspace, workspace_bytes, k_scale, v_scale, dtype,
+                      stream);
 }

@@ -555,7 +555,7 @@ __global__ __launch_bounds__(64 * kPWaves) __attribute__((amdgpu_waves_per_eu(2,
     const int t = t0 + row / G;
     const int h = row % G;
     if (t >= t_end) continue;
-    const float inv = lj > 0.f ? 1.f / lj : 0.f;
+    const float inv = (lj > 0.f ? 1.f / lj : 0.f) * a.v_scale;  // v_scale 1: exact no-op
     T *op = out + (int64_t)(q0 + t) * a.o_ts + (int64_t)(kvh * G + h) * a.o_hs + g * 4;
 #pragma unroll
     for (int d = 0; d < DT; ++d) {

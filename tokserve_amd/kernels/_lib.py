@@ -95,11 +95,14 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
          _i64, _i64,
          _c_void_p, _i64, _f32, _f32, _i32, _c_void_p],
     ),
+    "tks_paged_attention_prefill_fp8_workspace_bytes": (
+        _i64, [_i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32],
+    ),
     "tks_paged_attention_prefill_fp8": (
         _i32,
         [_c_void_p, _i64, _i64, _c_void_p, _c_void_p, _i32, _i64, _i32, _i32, _i32, _i32,
          _c_void_p, _i32, _c_void_p, _c_void_p, _i32, _i64, _i32, _i32, _i32, _f32,
-         _c_void_p, _i64, _i64, _f32, _f32, _i32, _c_void_p],
+         _c_void_p, _i64, _i64, _c_void_p, _i64, _f32, _f32, _i32, _c_void_p],
     ),
 }
 

@@ -215,16 +215,30 @@ def decode_workspace_bytes(
     return int(size)
 
 
-_workspaces: dict[torch.device, torch.Tensor] = {}
+_workspaces: dict[tuple[torch.device, str], torch.Tensor] = {}
+# Buffers replaced by larger ones stay allocated: a captured HIP graph keeps the
+# device address it was recorded with, and a freed buffer could be handed to
+# another tensor while such a graph still writes into it.
+_retired: list[torch.Tensor] = []
 
 
-def _workspace(device: torch.device, nbytes: int) -> torch.Tensor | None:
+def _workspace(device: torch.device, nbytes: int, key: str) -> torch.Tensor | None:
+    """A per-(device, use) scratch buffer of at least nbytes (None for 0 bytes).
+
+    Growth doubles the buffer; the old one is kept alive (see _retired). Calls
+    that share a buffer must be ordered on one stream, as the kernels require.
+    """
+
     if nbytes == 0:
         return None
-    buffer = _workspaces.get(device)
+    slot = (torch.device(device), key)
+    buffer = _workspaces.get(slot)
     if buffer is None or buffer.numel() < nbytes:
-        buffer = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
-        _workspaces[device] = buffer
+        size = max(nbytes, 1 << 20, 0 if buffer is None else 2 * buffer.numel())
+        if buffer is not None:
+            _retired.append(buffer)
+        buffer = torch.empty(size, dtype=torch.uint8, device=device)
+        _workspaces[slot] = buffer
     return buffer
 
 
@@ -302,7 +316,7 @@ def paged_attention_decode(
         num_seqs, num_q_heads, num_kv_heads, head_dim, block_size, max_seq_len, pages_per_split
     )
     if workspace is None:
-        workspace = _workspace(query.device, nbytes)
+        workspace = _workspace(query.device, nbytes, "decode")
     common = (
         query.data_ptr(), query.stride(0), query.stride(1),
         key_cache.data_ptr(), value_cache.data_ptr(), num_layers, num_blocks, num_kv_heads,
@@ -383,8 +397,17 @@ def paged_attention_prefill(
         max_query_len, max_seq_len, scale, out.data_ptr(), out.stride(0), out.stride(1),
     )
     if fp8:
-        status = _lib.load().tks_paged_attention_prefill_fp8(
-            *common, k_scale, v_scale, _lib.dtype_code(query.dtype), _lib.stream_of(query)
+        library = _lib.load()
+        nbytes = library.tks_paged_attention_prefill_fp8_workspace_bytes(
+            num_seqs, num_q_heads, num_kv_heads, head_dim, block_size, tables.shape[1],
+            max_seq_len, _lib.dtype_code(query.dtype),
+        )
+        if nbytes < 0:
+            raise ValueError("invalid fp8 prefill workspace query")
+        workspace = _workspace(query.device, nbytes, "prefill_fp8_pages")
+        status = library.tks_paged_attention_prefill_fp8(
+            *common, _lib.ptr(workspace), 0 if workspace is None else workspace.numel(),
+            k_scale, v_scale, _lib.dtype_code(query.dtype), _lib.stream_of(query)
         )
     else:
         status = _lib.load().tks_paged_attention_prefill(

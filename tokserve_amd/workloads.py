@@ -193,13 +193,14 @@ def decode_fp32_small(device: torch.device | str, *, seed: int = 0) -> PagedBatc
 
 
 def mixed_llama3_8b(
-    device: torch.device | str, *, seed: int = 0, chunks: int = 16, decodes: int = 240
+    device: torch.device | str, *, seed: int = 0, chunks: int = 16, decodes: int = 240,
+    kv_dtype: torch.dtype | None = None,
 ) -> tuple[PagedBatch, PagedBatch]:
     """(prefill part, decode part) of the mixed chunked-prefill + decode step.
 
     Both parts share one KV pool. Prefill chunk c has 512 query tokens on a prior
     context P_c ~ U[0, 2048] (so it sees P_c + 512 keys); decode d sees
-    ctx_d ~ U[256, 4096] keys.
+    ctx_d ~ U[256, 4096] keys. kv_dtype torch.float8_e4m3fn: fp8 pools, scale 1.
     """
 
     gen = torch.Generator().manual_seed(seed)
@@ -210,7 +211,7 @@ def mixed_llama3_8b(
     full = paged_batch(
         contexts, qlens, num_q_heads=32, num_kv_heads=8, head_dim=128, block_size=16,
         dtype=torch.bfloat16, device=device, seed=seed + 7,
-        pool_on_device_rng=torch.device(device).type == "cuda",
+        pool_on_device_rng=torch.device(device).type == "cuda", kv_dtype=kv_dtype,
     )
     n_pre = chunks * 512
     cu_pre = full.cu_seqlens_q[: chunks + 1]
