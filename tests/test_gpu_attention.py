@@ -283,3 +283,35 @@ def test_nan_in_unwritten_pool_rows_never_reaches_the_output(device, dtype, hq, 
     assert_close(decode.cpu(), paged.decode_batch(q[q_rows.cpu()], kc, vc, bt, lens, 0, compute),
                  **tol)
     assert_close(prefill.cpu(), paged.prefill_batch(q, kc, vc, bt, lens, cu, 0, compute), **tol)
+
+
+def test_decode_200k_token_context(device) -> None:
+    """One 200,000-key sequence beside short ones (12,500 pages, split across workgroups
+    and merged) against the oracle; the long context's output is not the short ones'."""
+
+    contexts = [200_000, 7, 1500]
+    batch = workloads.paged_batch(contexts, [1] * 3, num_q_heads=8, num_kv_heads=2,
+                                  head_dim=128, block_size=16, dtype=torch.bfloat16,
+                                  device=device, seed=41, pool_on_device_rng=True)
+    out = _decode(batch)
+    torch.cuda.synchronize()
+    _assert_parity(out, _decode_oracle, batch)
+
+
+@pytest.mark.parametrize("context", [65_536, 65_552])
+def test_prefill_at_and_past_the_lds_block_window(device, context) -> None:
+    """The MFMA prefill holds up to 4,096 pages (65,536 keys) of a sequence's block ids in
+    LDS; one page more goes to the VALU kernel. Both sides of the boundary, 96 queries at
+    the end of the context, against the oracle."""
+
+    batch = workloads.paged_batch([context, 40], [96, 40], num_q_heads=8, num_kv_heads=2,
+                                  head_dim=64, block_size=16, dtype=torch.bfloat16,
+                                  device=device, seed=context, pool_on_device_rng=True)
+    out = ops.paged_attention_prefill(
+        batch.query, batch.key_cache, batch.value_cache, batch.block_tables, batch.seq_lens,
+        batch.cu_seqlens_q, layer_index=0, max_query_len=batch.max_query_len,
+        max_seq_len=batch.max_seq_len)
+    torch.cuda.synchronize()
+    q, kc, vc, bt, lens, cu = _cpu(batch)
+    assert_close(out.cpu(), paged.prefill_batch(q, kc, vc, bt, lens, cu, 0, torch.float32),
+                 rtol=0, atol=2e-2)

@@ -16,8 +16,8 @@
 // K and V pages move HBM -> LDS with global_load_lds_dwordx4 (16 bytes per lane
 // written straight into LDS, no registers) into a three-stage ring, two steps
 // ahead of the compute. Rows keep their natural [key][dim] layout with the 16-byte
-// chunks of row k XOR-swizzled by k % (Dh/8), which spreads the 16 rows an MFMA
-// operand read touches over all LDS banks. V^T operands come from the same
+// chunks of each row XOR-swizzled (Swizzle below), so that neither operand read
+// has LDS bank conflicts. V^T operands come from the same
 // layout through ds_read_b64_tr_b16: within each 16-lane group, result element e
 // of lane j is element j % 4 of the 8 bytes that lane 4e + j / 4 addressed, so a
 // lane addressing dims 4c .. 4c+3 of key m hands dim j of keys 0..3 to lane j.
@@ -231,6 +231,26 @@ struct Const {
   static constexpr int value = N;
 };
 
+// XOR swizzles of the 16-byte chunks of a K or V row in LDS, a function of the
+// row within its 16-row page (so the second page of a step, read at an
+// immediate offset, has the same pattern). Chosen so that neither operand read
+// has bank conflicts (64 banks of 4 bytes):
+//   K (ds_read_b128, 16 lanes = rows 0..15 at one logical chunk): Dh 128 rows
+//     are 256 bytes, so row r takes chunk c ^ r; Dh 64 rows are 128 bytes and
+//     rows r, r + 8 share banks, so the chunk index mixes r >> 1 instead.
+//   V^T (ds_read_b64_tr_b16, 16 lanes = rows 4g .. 4g+3 x chunks 2d, 2d+1 x
+//     two 8-byte halves): Dh 128 takes c ^ 2 (row & 7), which sends the eight
+//     (row, chunk) pairs to eight different chunks; Dh 64 takes c ^ row.
+template <int DH>
+struct Swizzle {
+  static __device__ __forceinline__ int k(int row) {
+    return DH == 128 ? (row & 15) : ((row >> 1) & 7);
+  }
+  static __device__ __forceinline__ int v(int row) {
+    return DH == 128 ? 2 * (row & 7) : (row & 7);
+  }
+};
+
 template <typename T, int DH, int G, int RT>
 __global__ __launch_bounds__(64 * kPWaves) __attribute__((amdgpu_waves_per_eu(2, 2))) void prefill_mfma_kernel(
     PrefillArgs a) {
@@ -336,12 +356,16 @@ __global__ __launch_bounds__(64 * kPWaves) __attribute__((amdgpu_waves_per_eu(2,
   auto page_of_load = [&](int step, int k) {
     return step * (KS / 16) + ((k * kPWaves + wave) * 64 / CPR) / 16;
   };
-  uint32_t src_off[LOADS];  // byte offset of this lane's chunk inside its block
+  using Swz = Swizzle<DH>;
+  // Byte offsets of this lane's K and V chunks inside their page: LDS slot
+  // (row, physical chunk) receives logical chunk physical ^ swizzle(row).
+  uint32_t src_off_k[LOADS], src_off_v[LOADS];
 #pragma unroll
   for (int k = 0; k < LOADS; ++k) {
     const int slot = (k * kPWaves + wave) * 64 + lane;
     const int row = slot / CPR;
-    src_off[k] = ((row % 16) * DH + ((slot % CPR) ^ (row % CPR)) * 8) * (int)sizeof(T);
+    src_off_k[k] = ((row % 16) * DH + ((slot % CPR) ^ Swz::k(row)) * 8) * (int)sizeof(T);
+    src_off_v[k] = ((row % 16) * DH + ((slot % CPR) ^ Swz::v(row)) * 8) * (int)sizeof(T);
   }
   // Issues the loads of one step into ring stage STG; blk[k] is wave-uniform.
   auto issue = [&](auto stage_c, const int32_t (&blk)[LOADS]) {
@@ -350,8 +374,8 @@ __global__ __launch_bounds__(64 * kPWaves) __attribute__((amdgpu_waves_per_eu(2,
     for (int k = 0; k < LOADS; ++k) {
       const int slot0 = (k * kPWaves + wave) * 64;
       const int64_t base = (int64_t)__builtin_amdgcn_readfirstlane(blk[k]) * kPageBytes;
-      load_lds16(kc + base + src_off[k], &ring[STG * STAGE + slot0 * 8]);
-      load_lds16(vc + base + src_off[k], &ring[STG * STAGE + TILE + slot0 * 8]);
+      load_lds16(kc + base + src_off_k[k], &ring[STG * STAGE + slot0 * 8]);
+      load_lds16(vc + base + src_off_v[k], &ring[STG * STAGE + TILE + slot0 * 8]);
     }
   };
 
@@ -359,12 +383,12 @@ __global__ __launch_bounds__(64 * kPWaves) __attribute__((amdgpu_waves_per_eu(2,
   const uint32_t ring_base = lds_address(&ring[0]);
   uint32_t ka_addr[NC], va_addr[DT];
 #pragma unroll
-  for (int c = 0; c < NC; ++c) ka_addr[c] = ring_base + (r * CPR + ((c * 4 + g) ^ (r % CPR))) * 16;
+  for (int c = 0; c < NC; ++c) ka_addr[c] = ring_base + (r * CPR + ((c * 4 + g) ^ Swz::k(r))) * 16;
 #pragma unroll
   for (int d = 0; d < DT; ++d) {
     const int row = g * 4 + r / 4;  // + 16 for the second page (immediate offset)
     const int lc = d * 2 + (r % 4) / 2;
-    va_addr[d] = ring_base + TILE * (int)sizeof(T) + (row * CPR + (lc ^ (row % CPR))) * 16 + (r & 1) * 8;
+    va_addr[d] = ring_base + TILE * (int)sizeof(T) + (row * CPR + (lc ^ Swz::v(row))) * 16 + (r & 1) * 8;
   }
   const uint32_t bt_base = lds_address(&bt_s[0]);
 
