@@ -280,6 +280,29 @@ int32_t tks_rope(const void *query, void *query_out, int64_t q_sb, int64_t q_sh,
                  tks_stream_t stream);
 
 /* ------------------------------------------------------------------------
+ * RoPE fused with the KV append, for a packed step (one launch where the model
+ * layer would run tks_rope and then tks_kv_append; the reference does the two
+ * in turn per request, tokserve/engine/attention.py:247-265 and
+ * tokserve/engine/paged/sequence_cache.py:86-131):
+ *   query token t, head h (strides q_ts, q_hs) is rotated at positions[t] into
+ *   query_out (may equal query); key rows are rotated and written to pool slot
+ *   slot_mapping[t] of layer_index (and to key_out when it is not NULL); value
+ *   rows are copied to the same slot. Pools [L, NB, Hkv, BS, Dh] in `dtype`.
+ * Results are bit-identical to tks_rope followed by tks_kv_append of the rotated
+ * keys; negative slots skip the token's append (its Q is still rotated).
+ */
+int32_t tks_rope_kv_append(const void *query, void *query_out, int64_t q_ts, int64_t q_hs,
+                           int64_t qo_ts, int64_t qo_hs, int32_t num_q_heads, const void *key,
+                           void *key_out, int64_t k_ts, int64_t k_hs, int64_t ko_ts,
+                           int64_t ko_hs, const void *value, int64_t v_ts, int64_t v_hs,
+                           int32_t num_kv_heads, int64_t num_tokens, int32_t head_dim,
+                           const int64_t *positions, const void *cos_cache,
+                           const void *sin_cache, int64_t cache_len, void *key_cache,
+                           void *value_cache, int32_t num_layers, int64_t num_blocks,
+                           int32_t block_size, int32_t layer_index,
+                           const int64_t *slot_mapping, int32_t dtype, tks_stream_t stream);
+
+/* ------------------------------------------------------------------------
  * Greedy token selection: first index of the row maximum (NaN counts as the
  * maximum, as torch.argmax does).
  * Replaces select_greedy (tokserve/generation/greedy.py:6-18) on a (B, V) batch.

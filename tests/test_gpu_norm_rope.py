@@ -153,3 +153,55 @@ def test_greedy_argmax_matches_torch(device, dtype) -> None:
     torch.cuda.synchronize()
     assert torch.equal(actual.cpu(), expected)
     assert int(actual[3]) == 7 and int(actual[5]) == 2
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize(("hq", "hkv", "dh", "bs"), [(32, 8, 128, 16), (32, 4, 64, 16),
+                                                     (4, 2, 10, 3)])
+def test_rope_kv_append_equals_rope_then_append(device, dtype, hq, hkv, dh, bs) -> None:
+    """The fused launch on the model's packed QKV rows: rotated Q in place, rotated K and V
+    in the pools, bit-identical to rope() then kv_append() and to the oracle (torch
+    apply_rope, the C append); a negative slot rotates Q and appends nothing
+    (Dh 10: the element path)."""
+
+    from oracle import kvslots
+
+    n, layers, blocks = 37, 2, 40
+    g = torch.Generator().manual_seed(dh + hq)
+    qkv = torch.randn(n, (hq + 2 * hkv) * dh, generator=g).to(dtype)
+    pos = torch.randint(0, 200, (n,), generator=g)
+    slots = torch.randperm(blocks * bs, generator=g)[:n].to(torch.int64)
+    slots[3] = -1
+    table = ops.RotaryTable(dh, theta=10_000.0, max_position=256, dtype=dtype, device=device)
+
+    def views(t):
+        return (t[:, : hq * dh].view(n, hq, dh), t[:, hq * dh : (hq + hkv) * dh].view(n, hkv, dh),
+                t[:, (hq + hkv) * dh :].view(n, hkv, dh))
+
+    shape = (layers, blocks, hkv, bs, dh)
+    fused_rows = qkv.to(device)
+    q, k, v = views(fused_rows)
+    kc, vc = torch.zeros(shape, dtype=dtype, device=device), torch.zeros(shape, dtype=dtype, device=device)
+    k_rot = torch.empty(n, hkv, dh, dtype=dtype, device=device)
+    ops.rope_kv_append(q, k, v, pos.to(device), table, kc, vc, slots.to(device), 1, key_out=k_rot)
+
+    split_rows = qkv.to(device)
+    q2, k2, v2 = views(split_rows)
+    q4, k4 = q2.transpose(0, 1).unsqueeze(0), k2.transpose(0, 1).unsqueeze(0)
+    ops.rope(q4, k4, pos.to(device), table, query_out=q4, key_out=k4)
+    kc2, vc2 = torch.zeros_like(kc), torch.zeros_like(vc)
+    ops.kv_append(k2, v2, kc2, vc2, slots.to(device), 1)
+    torch.cuda.synchronize()
+
+    assert torch.equal(q.cpu(), q2.cpu())
+    assert torch.equal(k_rot.cpu(), k2.cpu())
+    assert torch.equal(kc.cpu(), kc2.cpu()) and torch.equal(vc.cpu(), vc2.cpu())
+    assert torch.equal(k.cpu(), views(qkv)[1])  # the K rows themselves are left as they were
+
+    qc, kcpu, vcpu = views(qkv)
+    eq, ek = torch_path.apply_rope(qc.transpose(0, 1).unsqueeze(0), kcpu.transpose(0, 1).unsqueeze(0),
+                                   pos, theta=10_000.0)
+    assert torch.equal(q.cpu(), eq[0].transpose(0, 1))
+    ekc, evc = torch.zeros(shape, dtype=dtype), torch.zeros(shape, dtype=dtype)
+    kvslots.kv_append(ek[0].transpose(0, 1).contiguous(), vcpu.contiguous(), ekc, evc, slots, 1)
+    assert torch.equal(kc.cpu(), ekc) and torch.equal(vc.cpu(), evc)

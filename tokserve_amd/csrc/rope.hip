@@ -25,11 +25,12 @@ struct RopeTensor {
   int32_t heads;
 };
 
+// Rotates one chunk pair of x into o1 (dims c..c+V) and o2 (dims c+D/2..).
 template <typename T, int V>
-__device__ __forceinline__ void rotate(const T *x, T *y, const float *c, const float *s,
-                                       int half) {
+__device__ __forceinline__ void rotate_values(const T *x, const float *c, const float *s,
+                                              int half, float *o1, float *o2) {
 #pragma clang fp contract(off)
-  float x1[V], x2[V], o1[V], o2[V];
+  float x1[V], x2[V];
   if constexpr (V * sizeof(T) == 16) {
     unpack<T>(ld16(x), x1);
     unpack<T>(ld16(x + half), x2);
@@ -49,6 +50,10 @@ __device__ __forceinline__ void rotate(const T *x, T *y, const float *c, const f
     o1[j] = a1 + b1;
     o2[j] = a2 + b2;
   }
+}
+
+template <typename T, int V>
+__device__ __forceinline__ void store_pair(T *y, const float *o1, const float *o2, int half) {
   if constexpr (V * sizeof(T) == 16) {
     st16(y, pack<T>(o1));
     st16(y + half, pack<T>(o2));
@@ -57,6 +62,29 @@ __device__ __forceinline__ void rotate(const T *x, T *y, const float *c, const f
     for (int j = 0; j < V; ++j) {
       y[j] = from_float<T>(o1[j]);
       y[half + j] = from_float<T>(o2[j]);
+    }
+  }
+}
+
+template <typename T, int V>
+__device__ __forceinline__ void rotate(const T *x, T *y, const float *c, const float *s,
+                                       int half) {
+  float o1[V], o2[V];
+  rotate_values<T, V>(x, c, s, half, o1, o2);
+  store_pair<T, V>(y, o1, o2, half);
+}
+
+template <typename T, int V>
+__device__ __forceinline__ void load_table(const T *crow, const T *srow, int c, float *cf,
+                                           float *sf) {
+  if constexpr (V * sizeof(T) == 16) {
+    unpack<T>(ld16(crow + c), cf);
+    unpack<T>(ld16(srow + c), sf);
+  } else {
+#pragma unroll
+    for (int j = 0; j < V; ++j) {
+      cf[j] = to_float(crow[c + j]);
+      sf[j] = to_float(srow[c + j]);
     }
   }
 }
@@ -95,6 +123,77 @@ __global__ __launch_bounds__(kThreads) void rope_kernel(RopeTensor q, RopeTensor
     const T *src = static_cast<const T *>(x.in) + b * x.sb + hh * x.sh + t * x.st + c;
     T *dst = static_cast<T *>(x.out) + b * x.osb + hh * x.osh + t * x.ost + c;
     rotate<T, V>(src, dst, cf, sf, half);
+  }
+}
+
+// RoPE on a packed step's Q and K fused with the KV append: token t's rotated
+// K rows go straight to pool slot slot_mapping[t] (and to k_out when given), its
+// V rows are copied there, Q is rotated into q_out. One workgroup per token.
+// Equal, bit for bit, to tks_rope followed by tks_kv_append on the rotated K.
+struct AppendView {
+  const void *v;
+  int64_t v_ts, v_hs;
+  void *kc, *vc;
+  int64_t layer_base, block_stride, head_stride, num_slots;
+  int32_t block_size;
+  const int64_t *slots;
+};
+
+template <typename T, int V>
+__global__ __launch_bounds__(kThreads) void rope_append_kernel(
+    RopeTensor q, RopeTensor k, AppendView a, const int64_t *__restrict__ positions,
+    const T *__restrict__ cos_cache, const T *__restrict__ sin_cache, int64_t cache_len,
+    int32_t head_dim) {
+  const int64_t t = blockIdx.x;
+  const int half = head_dim / 2;
+  const int chunks = half / V;
+  int64_t pos = positions[t];
+  pos = pos < 0 ? 0 : (pos >= cache_len ? cache_len - 1 : pos);
+  const T *crow = cos_cache + pos * half;
+  const T *srow = sin_cache + pos * half;
+  const int64_t slot = a.slots[t];
+  const bool keep = slot >= 0 && slot < a.num_slots;
+  int64_t row = 0;
+  if (keep) {
+    const int64_t block = slot / a.block_size;
+    row = a.layer_base + block * a.block_stride + (slot - block * a.block_size) * head_dim;
+  }
+  T *kc = static_cast<T *>(a.kc);
+  T *vc = static_cast<T *>(a.vc);
+  const int rot_items = (q.heads + k.heads) * chunks;
+  const int v_chunks = head_dim / V;
+  const int items = rot_items + (keep ? k.heads * v_chunks : 0);
+  for (int it = threadIdx.x; it < items; it += kThreads) {
+    if (it >= rot_items) {  // V copy
+      const int j = it - rot_items;
+      const int h = j / v_chunks;
+      const int c = (j - h * v_chunks) * V;
+      const T *src = static_cast<const T *>(a.v) + t * a.v_ts + h * a.v_hs + c;
+      T *dst = vc + row + h * a.head_stride + c;
+      if constexpr (V * sizeof(T) == 16) {
+        st16(dst, ld16(src));
+      } else {
+#pragma unroll
+        for (int e = 0; e < V; ++e) dst[e] = src[e];
+      }
+      continue;
+    }
+    const int h = it / chunks;
+    const int c = (it - h * chunks) * V;
+    float cf[V], sf[V], o1[V], o2[V];
+    load_table<T, V>(crow, srow, c, cf, sf);
+    if (h < q.heads) {
+      const T *src = static_cast<const T *>(q.in) + h * q.sh + t * q.st + c;
+      T *dst = static_cast<T *>(q.out) + h * q.osh + t * q.ost + c;
+      rotate<T, V>(src, dst, cf, sf, half);
+    } else {
+      const int hh = h - q.heads;
+      const T *src = static_cast<const T *>(k.in) + hh * k.sh + t * k.st + c;
+      rotate_values<T, V>(src, cf, sf, half, o1, o2);
+      if (k.out != nullptr)
+        store_pair<T, V>(static_cast<T *>(k.out) + hh * k.osh + t * k.ost + c, o1, o2, half);
+      if (keep) store_pair<T, V>(kc + row + hh * a.head_stride + c, o1, o2, half);
+    }
   }
 }
 
@@ -157,4 +256,65 @@ extern "C" int32_t tks_rope(const void *query, void *query_out, int64_t q_sb, in
       return launch<bf16_t>(q, k, batch, num_tokens, head_dim, positions, cos_cache, sin_cache,
                             cache_len, s);
   }
+}
+
+extern "C" int32_t tks_rope_kv_append(
+    const void *query, void *query_out, int64_t q_ts, int64_t q_hs, int64_t qo_ts,
+    int64_t qo_hs, int32_t num_q_heads, const void *key, void *key_out, int64_t k_ts,
+    int64_t k_hs, int64_t ko_ts, int64_t ko_hs, const void *value, int64_t v_ts, int64_t v_hs,
+    int32_t num_kv_heads, int64_t num_tokens, int32_t head_dim, const int64_t *positions,
+    const void *cos_cache, const void *sin_cache, int64_t cache_len, void *key_cache,
+    void *value_cache, int32_t num_layers, int64_t num_blocks, int32_t block_size,
+    int32_t layer_index, const int64_t *slot_mapping, int32_t dtype, tks_stream_t stream) {
+  if (!valid_dtype(dtype)) return TKS_ERR_TYPE;
+  if (head_dim < 2 || head_dim % 2 != 0 || num_q_heads < 0 || num_kv_heads <= 0 ||
+      num_tokens < 0 || cache_len <= 0 || num_layers <= 0 || num_blocks <= 0 || block_size <= 0)
+    return TKS_ERR_VALUE;
+  if (layer_index < 0 || layer_index >= num_layers) return TKS_ERR_INDEX;
+  if (num_tokens == 0) return TKS_OK;
+  if (num_tokens > 0x7fffffff) return TKS_ERR_VALUE;
+  if ((num_q_heads > 0 && (!query || !query_out)) || !key || !value || !positions ||
+      !cos_cache || !sin_cache || !key_cache || !value_cache || !slot_mapping)
+    return TKS_ERR_VALUE;
+  const RopeTensor q{query, query_out, 0, q_hs, q_ts, 0, qo_hs, qo_ts, num_q_heads};
+  const RopeTensor k{key, key_out, 0, k_hs, k_ts, 0, ko_hs, ko_ts, num_kv_heads};
+  AppendView a;
+  a.v = value;
+  a.v_ts = v_ts;
+  a.v_hs = v_hs;
+  a.kc = key_cache;
+  a.vc = value_cache;
+  a.head_stride = static_cast<int64_t>(block_size) * head_dim;
+  a.block_stride = a.head_stride * num_kv_heads;
+  a.layer_base = a.block_stride * num_blocks * layer_index;
+  a.num_slots = num_blocks * block_size;
+  a.block_size = block_size;
+  a.slots = slot_mapping;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const dim3 grid(static_cast<unsigned>(num_tokens));
+#define TKS_ROPE_APPEND(TYPE)                                                                  \
+  {                                                                                            \
+    constexpr int V = Vec<TYPE>::N;                                                            \
+    const RopeTensor kk{key, key_out ? key_out : const_cast<void *>(key), 0, k_hs, k_ts, 0,    \
+                        ko_hs, ko_ts, num_kv_heads};                                           \
+    const bool vec = (head_dim / 2) % V == 0 && aligned16(cos_cache) && aligned16(sin_cache) && \
+                     (num_q_heads == 0 || strides_ok(q, V)) && strides_ok(kk, V) &&             \
+                     v_ts % V == 0 && v_hs % V == 0 && aligned16(value) &&                      \
+                     aligned16(key_cache) && aligned16(value_cache);                            \
+    if (vec)                                                                                   \
+      rope_append_kernel<TYPE, V><<<grid, kThreads, 0, s>>>(                                   \
+          q, k, a, positions, static_cast<const TYPE *>(cos_cache),                            \
+          static_cast<const TYPE *>(sin_cache), cache_len, head_dim);                          \
+    else                                                                                       \
+      rope_append_kernel<TYPE, 1><<<grid, kThreads, 0, s>>>(                                   \
+          q, k, a, positions, static_cast<const TYPE *>(cos_cache),                            \
+          static_cast<const TYPE *>(sin_cache), cache_len, head_dim);                          \
+  }
+  switch (dtype) {
+    case TKS_FLOAT32: TKS_ROPE_APPEND(float); break;
+    case TKS_FLOAT16: TKS_ROPE_APPEND(_Float16); break;
+    default: TKS_ROPE_APPEND(bf16_t); break;
+  }
+#undef TKS_ROPE_APPEND
+  return check_launch();
 }

@@ -127,11 +127,18 @@ class GroupedQueryAttention(nn.Module):
         query = qkv[:, : hq * dh].view(tokens, hq, dh)
         key = qkv[:, hq * dh : (hq + hkv) * dh].view(tokens, hkv, dh)
         value = qkv[:, (hq + hkv) * dh :].view(tokens, hkv, dh)
-        # In-place rotation of the packed (1, H, N, Dh) views.
-        q4 = query.transpose(0, 1).unsqueeze(0)
-        k4 = key.transpose(0, 1).unsqueeze(0)
-        ops.rope(q4, k4, batch.positions, rotary, query_out=q4, key_out=k4)
-        storage.write_slots(layer_index, batch.slot_mapping, key, value)
+        if ops.is_fp8_pool(storage.key_storage):
+            # In-place rotation of the packed (1, H, N, Dh) views, then the quantizing append.
+            q4 = query.transpose(0, 1).unsqueeze(0)
+            k4 = key.transpose(0, 1).unsqueeze(0)
+            ops.rope(q4, k4, batch.positions, rotary, query_out=q4, key_out=k4)
+            storage.write_slots(layer_index, batch.slot_mapping, key, value)
+        else:
+            # Q rotated in place; rotated K and V go straight to the pool slots.
+            if layer_index < 0 or layer_index >= storage.num_layers:
+                raise IndexError("layer_index is out of range")
+            ops.rope_kv_append(query, key, value, batch.positions, rotary, storage.key_storage,
+                               storage.value_storage, batch.slot_mapping, layer_index)
         attended = torch.empty((tokens, hq, dh), dtype=inputs.dtype, device=inputs.device)
         split = batch.num_prefill_tokens
         if split > 0:

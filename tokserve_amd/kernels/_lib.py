@@ -75,6 +75,13 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
          _i32, _i64, _i32, _c_void_p, _c_void_p, _c_void_p, _i64, _i32, _c_void_p],
     ),
     "tks_argmax": (_i32, [_c_void_p, _i64, _i64, _i64, _c_void_p, _i32, _c_void_p]),
+    "tks_rope_kv_append": (
+        _i32,
+        [_c_void_p, _c_void_p, _i64, _i64, _i64, _i64, _i32,
+         _c_void_p, _c_void_p, _i64, _i64, _i64, _i64,
+         _c_void_p, _i64, _i64, _i32, _i64, _i32, _c_void_p, _c_void_p, _c_void_p, _i64,
+         _c_void_p, _c_void_p, _i32, _i64, _i32, _i32, _c_void_p, _i32, _c_void_p],
+    ),
     "tks_vector_add": (_i32, [_c_void_p, _c_void_p, _c_void_p, _i64, _i32, _c_void_p]),
     "tks_silu_mul": (_i32, [_c_void_p, _i64, _i64, _i64, _c_void_p, _i64, _i32, _c_void_p]),
     "tks_kv_append_fp8": (

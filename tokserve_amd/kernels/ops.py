@@ -577,6 +577,70 @@ def rope(
     return query_out, key_out
 
 
+def rope_kv_append(
+    query: torch.Tensor,
+    key: torch.Tensor,
+    value: torch.Tensor,
+    positions: torch.Tensor,
+    table: RotaryTable,
+    key_cache: torch.Tensor,
+    value_cache: torch.Tensor,
+    slot_mapping: torch.Tensor,
+    layer_index: int,
+    *,
+    query_out: torch.Tensor | None = None,
+    key_out: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """Packed step: rotate query (N, Hq, Dh) into query_out (in place by default), rotate
+    key (N, Hkv, Dh) and append it with value (N, Hkv, Dh) to the pools at slot_mapping.
+
+    One launch, bit-identical to rope() followed by kv_append() of the rotated keys.
+    key_out, when given, also receives the rotated keys. Pools in the rows' dtype
+    (fp8 pools take rope() and kv_append() separately).
+    """
+
+    require_hip("rope_kv_append", query, key, value, positions, key_cache, value_cache,
+                slot_mapping)
+    num_layers, num_blocks, num_kv_heads, block_size, head_dim = _pool_shape(
+        key_cache, value_cache
+    )
+    if query.ndim != 3 or key.ndim != 3 or value.shape != key.shape:
+        raise ValueError("query (N, Hq, Dh), key and value (N, Hkv, Dh) expected")
+    tokens = query.shape[0]
+    if key.shape != (tokens, num_kv_heads, head_dim) or query.shape[2] != head_dim:
+        raise ValueError("key and value rows must match the pool's (Hkv, Dh)")
+    if len({query.dtype, key.dtype, value.dtype, key_cache.dtype, table.dtype}) != 1:
+        raise ValueError("query, key, value, pools and the rotary table must share a dtype")
+    if head_dim != table.head_dim:
+        raise ValueError("head_dim must match the rotary table")
+    if positions.shape != (tokens,) or slot_mapping.shape != (tokens,):
+        raise ValueError("positions and slot_mapping must have shape (N,)")
+    pos = positions if positions.dtype == torch.int64 else positions.to(torch.int64)
+    pos = pos.contiguous()
+    slots = _int_tensor(slot_mapping, torch.int64, "slot_mapping")
+    for name, t in (("query", query), ("key", key), ("value", value)):
+        if t.stride(-1) != 1:
+            raise ValueError(f"{name} must be contiguous in head_dim")
+    if query_out is None:
+        query_out = query
+    if query_out.shape != query.shape or query_out.stride(-1) != 1:
+        raise ValueError("query_out must match query and be contiguous in head_dim")
+    if key_out is not None and (key_out.shape != key.shape or key_out.stride(-1) != 1):
+        raise ValueError("key_out must match key and be contiguous in head_dim")
+    status = _lib.load().tks_rope_kv_append(
+        query.data_ptr(), query_out.data_ptr(), query.stride(0), query.stride(1),
+        query_out.stride(0), query_out.stride(1), query.shape[1],
+        key.data_ptr(), _lib.ptr(key_out), key.stride(0), key.stride(1),
+        0 if key_out is None else key_out.stride(0), 0 if key_out is None else key_out.stride(1),
+        value.data_ptr(), value.stride(0), value.stride(1), num_kv_heads, tokens, head_dim,
+        pos.data_ptr(), table.cos.data_ptr(), table.sin.data_ptr(), table.length,
+        key_cache.data_ptr(), value_cache.data_ptr(), num_layers, num_blocks, block_size,
+        layer_index, slots.data_ptr(), _lib.dtype_code(query.dtype), _lib.stream_of(query),
+    )
+    _lib.check(status, "rope_kv_append")
+    return query_out
+
+
 # ----------------------------------------------------------------------------
 # Greedy selection
 
