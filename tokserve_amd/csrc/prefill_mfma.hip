@@ -251,9 +251,15 @@ struct Swizzle {
   }
 };
 
+// Waves per SIMD the register budget is cut for: Dh 128 (64 KB of LDS per
+// workgroup) runs 2 workgroups per CU, Dh 64 (40 KB) fits 4 in LDS and, at 128
+// registers, 4 waves per SIMD (measured 448 -> 372 us on a 63k-token Dh 64 prefill).
+template <int DH>
+constexpr int kPrefillOccupancy = DH == 64 ? 4 : 2;
+
 template <typename T, int DH, int G, int RT>
-__global__ __launch_bounds__(64 * kPWaves) __attribute__((amdgpu_waves_per_eu(2, 2))) void prefill_mfma_kernel(
-    PrefillArgs a) {
+__global__ __launch_bounds__(64 * kPWaves) __attribute__((amdgpu_waves_per_eu(
+    kPrefillOccupancy<DH>, kPrefillOccupancy<DH>))) void prefill_mfma_kernel(PrefillArgs a) {
   constexpr int ROWS = kPWaves * RT * 16;
   constexpr int QT = ROWS / G;           // query tokens per workgroup
   constexpr int NC = DH / 32;            // QK k-chunks
