@@ -150,6 +150,12 @@ def main() -> int:
 
     total_bytes = algorithmic_bytes(batch)
     achieved = total_bytes / (ms * 1e-3) / 1e9
+    # The same launch timed alone (HIP events around each launch, no inter-launch
+    # gap), then with the last-level cache flushed before each launch.
+    ms_alone = _time_ms_cold(step, args.steps, torch.zeros(1, device=device))
+    flush = _llc_flush_buffer(device)
+    ms_cold = _time_ms_cold(step, args.steps, flush)
+    del flush
     traffic = measured_traffic()
     result = {
         "metric": METRIC,
@@ -174,6 +180,14 @@ def main() -> int:
             "schedule": "longest-first sequence order (host plan)",
         },
         "pct_of_peak_hbm": round(100.0 * achieved / PEAK_HBM_GBPS, 2),
+        "per_launch": {
+            "note": "each launch bracketed by its own HIP events (back-to-back steps also "
+                    "hold the gap between consecutive launches)",
+            "ms": round(ms_alone, 5),
+            "gbps": round(total_bytes / (ms_alone * 1e-3) / 1e9, 2),
+            "llc_flushed_ms": round(ms_cold, 5),
+            "llc_flushed_gbps": round(total_bytes / (ms_cold * 1e-3) / 1e9, 2),
+        },
         "decode_tokens_per_s_one_layer": round(batch.num_seqs / (ms * 1e-3), 1),
         "roofline": {
             "bound": "hbm",
@@ -224,6 +238,31 @@ def _time_ms(fn, steps: int, warmup: int) -> float:
     end.record()
     torch.cuda.synchronize()
     return start.elapsed_time(end) / steps
+
+
+def _time_ms_cold(fn, steps: int, flush) -> float:
+    """Mean time of fn() with the last-level cache flushed before each launch: every
+    launch is bracketed by its own HIP events, the flush (a read of a buffer twice the
+    256 MB Infinity Cache, so no dirty lines are left to write back) stays outside them."""
+
+    import torch
+
+    stream = torch.cuda.current_stream()
+    events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+              for _ in range(steps)]
+    for start, end in events:
+        flush.sum()
+        start.record(stream)
+        fn()
+        end.record(stream)
+    torch.cuda.synchronize()
+    return sum(start.elapsed_time(end) for start, end in events) / steps
+
+
+def _llc_flush_buffer(device):
+    import torch
+
+    return torch.zeros(512 << 20, dtype=torch.uint8, device=device)
 
 
 def measure_mixed(device, steps: int, warmup: int, kv_dtype=None) -> dict:
@@ -357,12 +396,16 @@ def measure_small_fp32_step(device, steps: int, warmup: int) -> dict:
     with torch.cuda.graph(graph):
         step()
     graph_us = _time_ms(graph.replay, steps, warmup) * 1e3
+    flush = _llc_flush_buffer(device)
+    graph_us_cold = _time_ms_cold(graph.replay, steps, flush) * 1e3
+    del flush
     kv_bytes = sum(batch.contexts) * 2 * 64 * 2 * 4
     return {
         "workload": "decode_fp32_small: 8 seqs, ctx U[16,512]+1, Hq 8 / Hkv 2, Dh 64, block 16, "
                     "fp32; RMSNorm 512 + RoPE + KV append + decode attention",
         "step_us_eager": round(eager_us, 2),
         "step_us_graph": round(graph_us, 2),
+        "step_us_graph_llc_flushed": round(graph_us_cold, 2),
         "kv_bytes": kv_bytes,
     }
 
@@ -392,6 +435,10 @@ def measure_norm_rope(device, steps: int, warmup: int) -> dict:
 
     ms_norm = _time_ms(norm, steps, warmup)
     ms_rope = _time_ms(rope, steps, warmup)
+    flush = _llc_flush_buffer(device)
+    ms_norm_cold = _time_ms_cold(norm, steps, flush)
+    ms_rope_cold = _time_ms_cold(rope, steps, flush)
+    del flush
     norm_bytes = n * 4096 * (2 + 4) + 4096 * 4
     rope_bytes = n * (40 * 128 * 2 * 2 + 8)
     return {
@@ -401,6 +448,12 @@ def measure_norm_rope(device, steps: int, warmup: int) -> dict:
         "rmsnorm_gbps": round(norm_bytes / (ms_norm * 1e-3) / 1e9, 1),
         "rope_ms": round(ms_rope, 5),
         "rope_gbps": round(rope_bytes / (ms_rope * 1e-3) / 1e9, 1),
+        "llc_flushed": {
+            "rmsnorm_ms": round(ms_norm_cold, 5),
+            "rmsnorm_gbps": round(norm_bytes / (ms_norm_cold * 1e-3) / 1e9, 1),
+            "rope_ms": round(ms_rope_cold, 5),
+            "rope_gbps": round(rope_bytes / (ms_rope_cold * 1e-3) / 1e9, 1),
+        },
     }
 
 
