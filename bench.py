@@ -96,7 +96,8 @@ def main() -> int:
     parser = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     parser.add_argument("--gpus", type=int, default=1)
     parser.add_argument("--steps", type=int, default=50)
-    parser.add_argument("--warmup", type=int, default=10)
+    # 400 launches (~0.12 s of back-to-back work) bring the GPU's clocks out of idle.
+    parser.add_argument("--warmup", type=int, default=400)
     parser.add_argument("--seed", type=int, default=0)
     parser.add_argument("--pages-per-split", type=int, default=0)
     parser.add_argument("--cpu-seconds", type=float, default=10.0)
@@ -222,14 +223,29 @@ def main() -> int:
     return 0
 
 
-def _time_ms(fn, steps: int, warmup: int) -> float:
-    """Mean time of fn() over `steps` launches, HIP events on the current stream."""
+def _settle(fn, warmup: int, seconds: float = 0.15) -> None:
+    """Untimed warm-up: at least `warmup` calls and at least `seconds` of back-to-back
+    work, so the GPU's clocks have left their idle state (from idle, a 250 us kernel runs
+    ~25 % slower in its first 5 ms of launches than after ~50 ms of sustained work)."""
 
     import torch
 
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
+    start = time.perf_counter()
+    while time.perf_counter() - start < seconds:
+        for _ in range(4):
+            fn()
+        torch.cuda.synchronize()
+
+
+def _time_ms(fn, steps: int, warmup: int) -> float:
+    """Mean time of fn() over `steps` launches, HIP events on the current stream."""
+
+    import torch
+
+    _settle(fn, warmup)
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
     start.record()
@@ -355,8 +371,9 @@ def measure_decode_fp8(device, seed: int, steps: int, warmup: int) -> dict:
 def measure_small_fp32_step(device, steps: int, warmup: int) -> dict:
     """The CPU-runnable fp32 decode step (8 sequences, contexts U[16, 512] + 1, 8/2 heads,
     Dh 64, block 16, 512-block pool): RMSNorm (hidden 512, eps 1e-5), RoPE (theta 1e4) of
-    the new Q/K at each sequence's next position, KV append through slot_mapping, split-K
-    decode attention. Launch-bound: reported in microseconds, eager and as a HIP graph."""
+    the new Q/K at each sequence's next position with the KV append through slot_mapping
+    in the same launch (as the model layer runs them), split-K decode attention.
+    Launch-bound: reported in microseconds, eager and as a HIP graph."""
 
     import torch
 
@@ -376,17 +393,14 @@ def measure_small_fp32_step(device, steps: int, warmup: int) -> dict:
                           for b, c in enumerate(batch.contexts)], dtype=torch.int64, device=device)
     table = ops.RotaryTable(64, theta=10_000.0, max_position=1024, dtype=torch.float32, device=device)
     out = torch.empty_like(batch.query)
-    q4 = batch.query.transpose(0, 1).unsqueeze(0)
-    k4 = new_k.transpose(0, 1).unsqueeze(0)
-    q_rot = torch.empty_like(q4)
-    k_rot = torch.empty_like(k4)
+    q_rot = torch.empty_like(batch.query)
 
     def step() -> None:
         ops.rms_norm(hidden, weight, 1e-5, out=normed)
-        ops.rope(q4, k4, positions, table, query_out=q_rot, key_out=k_rot)
-        ops.kv_append(k_rot[0].transpose(0, 1), new_v, batch.key_cache, batch.value_cache, slots, 0)
+        ops.rope_kv_append(batch.query, new_k, new_v, positions, table, batch.key_cache,
+                           batch.value_cache, slots, 0, query_out=q_rot)
         ops.paged_attention_decode(
-            q_rot[0].transpose(0, 1), batch.key_cache, batch.value_cache, batch.block_tables,
+            q_rot, batch.key_cache, batch.value_cache, batch.block_tables,
             batch.seq_lens, layer_index=0, max_seq_len=batch.max_seq_len, out=out)
 
     eager_us = _time_ms(step, steps, warmup) * 1e3
@@ -402,7 +416,7 @@ def measure_small_fp32_step(device, steps: int, warmup: int) -> dict:
     kv_bytes = sum(batch.contexts) * 2 * 64 * 2 * 4
     return {
         "workload": "decode_fp32_small: 8 seqs, ctx U[16,512]+1, Hq 8 / Hkv 2, Dh 64, block 16, "
-                    "fp32; RMSNorm 512 + RoPE + KV append + decode attention",
+                    "fp32; RMSNorm 512 + RoPE with KV append + decode attention",
         "step_us_eager": round(eager_us, 2),
         "step_us_graph": round(graph_us, 2),
         "step_us_graph_llc_flushed": round(graph_us_cold, 2),
