@@ -476,6 +476,9 @@ __global__ __launch_bounds__(64 * kPWaves) __attribute__((amdgpu_waves_per_eu(
 #pragma unroll
         for (int c = 0; c < NC; ++c) st[j][kt] = M::run(ka[kt][c], qb[j][c], st[j][kt]);
       }
+    // The softmax issues at raised priority, so a SIMD's other wave (another
+    // workgroup, usually in its MFMA phase) yields it the VALU (mixed step 236 -> 232 us).
+    __builtin_amdgcn_s_setprio(1);
     const bool tail = s * KS + KS > n_keys;
     const bool need_mask = s * KS + KS - 1 > min_pos || tail;
 
@@ -548,6 +551,7 @@ __global__ __launch_bounds__(64 * kPWaves) __attribute__((amdgpu_waves_per_eu(
         }
       }
     }
+    __builtin_amdgcn_s_setprio(0);
 #pragma unroll
     for (int j = 0; j < RT; ++j)
 #pragma unroll
