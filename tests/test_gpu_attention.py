@@ -315,3 +315,44 @@ def test_prefill_at_and_past_the_lds_block_window(device, context) -> None:
     q, kc, vc, bt, lens, cu = _cpu(batch)
     assert_close(out.cpu(), paged.prefill_batch(q, kc, vc, bt, lens, cu, 0, torch.float32),
                  rtol=0, atol=2e-2)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize(("hq", "hkv", "dh"), [(32, 8, 128), (32, 4, 64)])
+def test_prefill_rising_scores_move_the_softmax_reference(device, dtype, hq, hkv, dh) -> None:
+    """Keys scaled up page by page along each sequence (x1 + i/4 for page i), so a row's
+    running max keeps rising and the prefill kernels move their softmax reference (and
+    rescale O and l) many times per row, not only at the first keys. Scores reach ~50, where
+    the torch backend's per-op bf16 rounding is coarse, so the check is the fp32-arithmetic
+    oracle at 2e-2. The near one-hot rows put outputs at |o| up to ~5, where one bf16 step
+    of the stored result is 2^-5 > 2e-2: the bound adds that one step (rtol 2^-7)."""
+
+    contexts, qlens = [700, 64, 300], [200, 64, 33]
+    batch = workloads.paged_batch(contexts, qlens, num_q_heads=hq, num_kv_heads=hkv, head_dim=dh,
+                                  block_size=16, dtype=dtype, device=device, seed=dh + hq)
+    for b, context in enumerate(contexts):
+        for i in range((context + 15) // 16):
+            batch.key_cache[0, int(batch.block_tables[b, i])] *= 1 + i / 4
+    out = _prefill(batch)
+    torch.cuda.synchronize()
+    assert_close(out.cpu(), _prefill_oracle(batch, torch.float32), rtol=2 ** -7, atol=2e-2)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("sign", [-1.0, 0.0])
+def test_prefill_non_positive_scale(device, dtype, sign) -> None:
+    """A scale of -1/sqrt(Dh) attends as the default scale does with the query negated, and
+    a zero scale averages the visible values uniformly (q scaled by zero); such scales take
+    the VALU kernel, since the MFMA kernel's row maxima assume a positive scale."""
+
+    batch = workloads.paged_batch([90, 33], [40, 33], num_q_heads=32, num_kv_heads=8,
+                                  head_dim=128, block_size=16, dtype=dtype, device=device, seed=9)
+    out = ops.paged_attention_prefill(
+        batch.query, batch.key_cache, batch.value_cache, batch.block_tables, batch.seq_lens,
+        batch.cu_seqlens_q, layer_index=0, max_query_len=batch.max_query_len,
+        max_seq_len=batch.max_seq_len, scale=sign / 128 ** 0.5)
+    torch.cuda.synchronize()
+    q, kc, vc, bt, lens, cu = _cpu(batch)
+    expected = paged.prefill_batch(q * sign, kc, vc, bt, lens, cu, 0, torch.float32)
+    assert_close(out.cpu(), expected, **(TOL[dtype] if dtype == torch.float32 else
+                                         dict(rtol=0, atol=2e-2)))

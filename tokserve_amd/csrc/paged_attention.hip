@@ -585,7 +585,9 @@ int32_t prefill_impl(const void *query, int64_t q_token_stride, int64_t q_head_s
   const int32_t pps = static_cast<int32_t>(ceil_div(max_seq_len > 0 ? max_seq_len : 1, block_size));
   const int32_t key_cap = std::min(block_table_stride, pps) * block_size;
   const int64_t scratch_blocks = static_cast<int64_t>(num_seqs) * block_table_stride;
+  // The MFMA kernel takes row maxima of raw scores, which needs a positive scale.
   const bool mfma_shape =
+      scale_log2 > 0.f && scale_log2 < INFINITY &&
       prefill_mfma_supported(dtype, head_dim, G, key_cap, block_size,
                              fp8_pools ? scratch_blocks : num_blocks, num_kv_heads) &&
       aligned16(query) && aligned16(key_cache) && aligned16(value_cache) &&

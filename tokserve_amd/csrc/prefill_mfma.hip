@@ -351,9 +351,11 @@ __global__ __launch_bounds__(64 * kPWaves) __attribute__((amdgpu_waves_per_eu(
   }
   // Smallest query position among this wave's rows: key steps entirely at or
   // below it (and inside n_keys) need no mask.
-  int min_pos = qpos[0];
+  // Padding rows (qpos -1) are left out: their Q^T operands are zero and their
+  // results are never stored, so they need no mask.
+  int min_pos = 0x7fffffff;
 #pragma unroll
-  for (int j = 1; j < RT; ++j) min_pos = min(min_pos, qpos[j]);
+  for (int j = 0; j < RT; ++j) min_pos = qpos[j] < 0 ? min_pos : min(min_pos, qpos[j]);
   min_pos = __reduce_min_sync(~0ull, min_pos);
   __syncthreads();  // bt_s ready
 
@@ -403,16 +405,25 @@ __global__ __launch_bounds__(64 * kPWaves) __attribute__((amdgpu_waves_per_eu(
   for (int j = 0; j < RT; ++j)
 #pragma unroll
     for (int d = 0; d < DT; ++d) o[j][d] = f4{0.f, 0.f, 0.f, 0.f};
-  float m[RT], l[RT];
+  // Online softmax state of row tile j (row r of the tile in lanes r, r+16,
+  // r+32, r+48), with m the reference max in log2 units (-inf before the first
+  // finite score): negref = -m (0 while m is -inf, so fully masked rows give
+  // p = 0), thr = the raw score above which m must move ((m + 8) / c, -inf
+  // exactly while m is), l = this lane's share of the row sum. The reference
+  // only moves when a score exceeds it by more than 8 (probabilities stay
+  // <= 2^8 meanwhile); until then a step needs no cross-lane max, only each
+  // lane's check of its own 8 scores.
+  float negref[RT], thr[RT], l[RT];
 #pragma unroll
   for (int j = 0; j < RT; ++j) {
-    m[j] = -INFINITY;
+    negref[j] = 0.f;
+    thr[j] = -INFINITY;
     l[j] = 0.f;
   }
 
   // Q is in registers before the first HBM -> LDS load, so no wait inside the
   // loop has to count it; likewise the scalars the loop reads.
-  float scale_log2 = a.scale_log2;
+  float scale_log2 = a.scale_log2;  // > 0 (the host routes other scales elsewhere)
   settle_sgpr(scale_log2);
   settle_sgpr(kc);
   settle_sgpr(vc);
@@ -442,22 +453,8 @@ __global__ __launch_bounds__(64 * kPWaves) __attribute__((amdgpu_waves_per_eu(
     Reads::template keys<0, kRowsBytes>(ka_addr, kraw);
     Reads::wait_keys(kraw);
   }
-
-  // One step: keys s*KS .. s*KS + KS - 1 from ring stage STG, whose K operands
-  // are already in kraw. Pipeline: V(s) LDS reads overlap QK(s) and the
-  // softmax; after a barrier that also frees stage s, K(s+1) is read while the
-  // PV(s) MFMAs run, and the loads of step s+3 go into stage s.
-  auto step = [&](auto stage_c, int s) {
-    constexpr int STG = decltype(stage_c)::value;
-    constexpr int O0 = STG * kStageBytes;
-    constexpr int N0 = ((STG + 1) % kStages) * kStageBytes;
-    const int ahead = min(s + 3, n_steps - 1);
-    const uint32_t ba = bt_base + page_of_load(ahead, 0) * 4;
-    u32x2 vraw[2 * DT];
-    uint32_t bid[LOADS];
-    Reads::template values<O0, O0 + kRowsBytes>(va_addr, ba, vraw, bid);
-
-    v8 ka[2][NC];
+  // K(s) as MFMA A operands: ka[kt][c] = keys kt*16 + (0..15), dims c*32 + ...
+  auto k_operands = [&](v8 (&ka)[2][NC]) {
 #pragma unroll
     for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
@@ -466,72 +463,113 @@ __global__ __launch_bounds__(64 * kPWaves) __attribute__((amdgpu_waves_per_eu(
                              kraw[kt * NC + c][3]);
         ka[kt][c] = as_v8<T>(u);
       }
-    // S^T for both row tiles first: the softmax of tile 0 then overlaps tile 1's MFMAs.
-    f4 st[RT][2];
+  };
+  // S^T of row tile j against the keys in ka.
+  auto scores = [&](const v8 (&ka)[2][NC], int j, f4 (&t)[2]) {
 #pragma unroll
-    for (int j = 0; j < RT; ++j)
+    for (int kt = 0; kt < 2; ++kt) {
+      t[kt] = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int kt = 0; kt < 2; ++kt) {
-        st[j][kt] = f4{0.f, 0.f, 0.f, 0.f};
+      for (int c = 0; c < NC; ++c) t[kt] = M::run(ka[kt][c], qb[j][c], t[kt]);
+    }
+  };
+
+  // Largest of a lane's 8 scores of one tile (NaN-propagating; a NaN score
+  // never moves the reference and yields NaN probabilities, as in softmax).
+  auto lane_max = [](const f4 (&t)[2]) {
+    const float a0 = nan_max(nan_max(t[0][0], t[0][1]), t[0][2]);
+    const float a1 = nan_max(nan_max(t[0][3], t[1][0]), t[1][1]);
+    const float a2 = nan_max(nan_max(t[1][2], t[1][3]), a0);
+    return nan_max(a1, a2);
+  };
+  // Probabilities of one tile against its reference: bf16/fp16 MFMA operand,
+  // returns the lane's sum of them (fp32, before rounding).
+  auto probs = [&](const f4 (&t)[2], float nr, v8 &pb) {
+    float p[8];
 #pragma unroll
-        for (int c = 0; c < NC; ++c) st[j][kt] = M::run(ka[kt][c], qb[j][c], st[j][kt]);
-      }
-    // The softmax issues at raised priority, so a SIMD's other wave (another
-    // workgroup, usually in its MFMA phase) yields it the VALU (mixed step 236 -> 232 us).
-    __builtin_amdgcn_s_setprio(1);
+    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) p[kt * 4 + i] = fast_exp2(__builtin_fmaf(t[kt][i], scale_log2, nr));
+#pragma unroll
+    for (int i = 0; i < 8; ++i) pb[i] = static_cast<typename M::elem>(p[i]);
+    return ((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7]));
+  };
+  // Moves tile j's reference to the row max when that exceeds it by more than
+  // 8 (rare after a row's first keys), rescaling O and l to the new reference.
+  auto rebase = [&](int j, float lm) {
+    const float mx = xgroup_max(lm) * scale_log2;
+    const float m_old = thr[j] == -INFINITY ? -INFINITY : -negref[j];
+    const bool bump = mx > m_old + 8.f;
+    const float m_new = bump ? mx : m_old;
+    const float alpha = bump ? fast_exp2(m_old - m_new) : 1.f;
+    negref[j] = m_new == -INFINITY ? 0.f : -m_new;
+    thr[j] = (m_new + 8.f) / scale_log2;
+    l[j] *= alpha;
+#pragma unroll
+    for (int d = 0; d < DT; ++d) o[j][d] *= alpha;
+  };
+
+  // One step: keys s*KS .. s*KS + KS - 1 from ring stage STG, whose K operands
+  // are already in kraw. Pipeline: V(s) LDS reads overlap QK(s) and the
+  // softmax; tile 1's QK MFMAs run under tile 0's softmax and tile 0's PV MFMAs
+  // under tile 1's probabilities; after a barrier that also frees stage s,
+  // K(s+1) is read and the loads of step s+3 go into stage s. Steps whose keys
+  // reach past the wave's first query position (or past the last key) apply
+  // the causal mask; uniform branches around it keep the unmasked steps free of
+  // mask work.
+  auto step = [&](auto stage_c, int s) {
+    static_assert(RT == 2, "the step interleaves two row tiles");
+    constexpr int STG = decltype(stage_c)::value;
+    constexpr int O0 = STG * kStageBytes;
+    constexpr int N0 = ((STG + 1) % kStages) * kStageBytes;
+    const int ahead = min(s + 3, n_steps - 1);
+    const uint32_t ba = bt_base + page_of_load(ahead, 0) * 4;
     const bool tail = s * KS + KS > n_keys;
     const bool need_mask = s * KS + KS - 1 > min_pos || tail;
+    u32x2 vraw[2 * DT];
+    uint32_t bid[LOADS];
+    Reads::template values<O0, O0 + kRowsBytes>(va_addr, ba, vraw, bid);
 
-    v8 pb[RT];
-#pragma unroll
-    for (int j = 0; j < RT; ++j) {
-      float sv[8];
+    v8 ka[2][NC];
+    k_operands(ka);
+    f4 st[RT][2];
+    scores(ka, 0, st[0]);
+    // Key kp = s*KS + kt*16 + g*4 + i is visible to a row iff kp <= qpos
+    // (which also keeps it below n_keys).
+    auto mask = [&](int j) {
+      const int rel = qpos[j] - (s * KS + g * 4);
 #pragma unroll
       for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) sv[kt * 4 + i] = st[j][kt][i];
-      if (need_mask) {
+        for (int i = 0; i < 4; ++i)
+          if (kt * 16 + i > rel) st[j][kt][i] = -INFINITY;
+    };
+    v8 pb[RT];
+    float ps[RT];
+    if (need_mask) mask(0);
+    scores(ka, 1, st[1]);
+    const float lm0 = lane_max(st[0]);
+    bool over = lm0 > thr[0];
+    ps[0] = probs(st[0], negref[0], pb[0]);
+    // Tile 0's probabilities issue between tile 1's QK MFMAs (one MFMA, then
+    // three VALU instructions), and stay here rather than sinking past the
+    // rebase branch below.
 #pragma unroll
-        for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const int kp = s * KS + kt * 16 + g * 4 + i;
-            if (!(kp <= qpos[j] && kp < n_keys)) sv[kt * 4 + i] = -INFINITY;
-          }
-      }
-      // Row max of the raw scores (row r lives in lanes r, r+16, r+32, r+48);
-      // the scale is positive, so max(s * c) = max(s) * c.
-      float mx = nan_max(nan_max(nan_max(sv[0], sv[1]), nan_max(sv[2], sv[3])),
-                         nan_max(nan_max(sv[4], sv[5]), nan_max(sv[6], sv[7])));
-      mx = xgroup_max(mx) * scale_log2;
-      // The reference max only moves when the new scores exceed it by more
-      // than 8 (probabilities stay <= 2^8 meanwhile); the rescale of O and l
-      // that a move costs is then rare after the first keys of a row.
-      const float m_old = m[j];
-      const bool bump = mx > m_old + 8.f;
-      const float m_new = bump ? mx : m_old;
-      m[j] = m_new;
-      if (__builtin_amdgcn_ballot_w64(bump && m_old != -INFINITY)) {
-        const float alpha = fast_exp2(m_old - m_new);
-        l[j] *= alpha;
-#pragma unroll
-        for (int d = 0; d < DT; ++d) o[j][d] *= alpha;
-      }
-      const float ref = m_new == -INFINITY ? 0.f : m_new;  // fully masked so far: p = 0
-      float ps = 0.f;
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const float p = fast_exp2(__builtin_fmaf(sv[i], scale_log2, -ref));
-        ps += p;
-        pb[j][i] = static_cast<typename M::elem>(p);
-      }
-      l[j] += ps;
+    for (int i = 0; i < 2 * NC; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);
+    }
+    pin_vgpr(pb[0]);
+    pin_vgpr(ps[0]);
+    if (need_mask) mask(1);
+    const float lm1 = lane_max(st[1]);
+    over = over || lm1 > thr[1];
+    if (__builtin_amdgcn_ballot_w64(over)) {
+      rebase(0, lm0);
+      rebase(1, lm1);
+      ps[0] = probs(st[0], negref[0], pb[0]);
     }
 
-    // The probabilities are computed while the V reads are in flight, not after
-    // the wait (the compiler would otherwise sink them to their MFMA use).
-#pragma unroll
-    for (int j = 0; j < RT; ++j) pin_vgpr(pb[j]);
     Reads::wait_values(vraw, bid);
     v8 va[DT];
 #pragma unroll
@@ -551,11 +589,17 @@ __global__ __launch_bounds__(64 * kPWaves) __attribute__((amdgpu_waves_per_eu(
         }
       }
     }
-    __builtin_amdgcn_s_setprio(0);
+    ps[1] = probs(st[1], negref[1], pb[1]);
 #pragma unroll
     for (int j = 0; j < RT; ++j)
 #pragma unroll
       for (int d = 0; d < DT; ++d) o[j][d] = M::run(va[d], pb[j], o[j][d]);
+    // Tile 1's probabilities issue between tile 0's PV MFMAs.
+#pragma unroll
+    for (int d = 0; d < DT; ++d) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);
+    }
 
     if (s + 1 < n_steps) {
       // Step s+1's loads done (only step s+2's may remain), and every wave is
@@ -573,6 +617,8 @@ __global__ __launch_bounds__(64 * kPWaves) __attribute__((amdgpu_waves_per_eu(
       }
       Reads::wait_keys(kraw);
     }
+#pragma unroll
+    for (int j = 0; j < RT; ++j) l[j] += ps[j];
   };
 
   for (int s = 0; s < n_steps; s += kStages) {
