@@ -84,6 +84,13 @@ __device__ __forceinline__ typename Mfma<T>::v8 as_v8(uint4 v) {
   return r;
 }
 
+// Decode grids put the split index in the slowest dimension: every split-0
+// workgroup (one per (sequence, KV head), all of them real) is dispatched
+// before any later split, most of which are empty for short sequences (their
+// workgroups find no keys and exit). Mixing the empty ones in between would
+// leave regular gaps in the round-robin placement over XCDs and CUs.
+constexpr int32_t kMaxGridSplits = 65535;
+
 struct DecodeArgs {
   const void *q;
   int64_t q_ss, q_hs;

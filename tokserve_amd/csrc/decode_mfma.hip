@@ -12,11 +12,16 @@
 //     B operand: column n holds token n of the page, straight from 16-byte
 //     HBM loads (lane (grp, r) reads dims c*32 + grp*8 .. +8 of token r);
 //     lane (grp, r) receives the scores of heads (grp*4 + i) % G for token r.
-// Softmax is online per page (running max m, sum l, rescale alpha); the page's
-// probabilities (G x 16) go through a per-wave LDS slice. P.V runs on the VALU:
-// lane (hg, tg, dc) owns dims dc*8 .. +8 of heads hg*HPL .. +HPL and tokens
-// tg*4 .. +3 of every page, so V also arrives as 16-byte loads; the four token
-// groups are summed once per wave. Every K/V byte is read from HBM exactly once
+// Softmax is online with a lazy reference: each lane checks its own scores
+// against reference + 8 (log2 units), and only when some score passes it does
+// the wave take row maxima, move the reference and rescale l and the P.V
+// accumulators (rare after a row's first page). The page's probabilities
+// (G x 16) go through a per-wave LDS slice. P.V runs on the VALU as packed
+// two-element dot products (v_dot2_f32_bf16 / _f16: P rounded to the model
+// dtype, V exact, fp32 accumulation): lane (hg, tg, dc) owns dims dc*8 .. +8
+// of heads hg*HPL .. +HPL and tokens tg*4 .. +3 of every page, so V also
+// arrives as 16-byte (fp8: 8-byte) loads, regrouped into token pairs by byte
+// permutes; the four token groups are summed once per wave. Every K/V byte is read from HBM exactly once
 // for all G query heads. Pages are double-buffered in registers and a wave's
 // block ids sit in one VGPR (broadcast with readlane), so nothing in the page
 // loop waits on a dependent memory access.
@@ -26,6 +31,9 @@ namespace tks {
 namespace {
 
 constexpr int kWaves = 4;
+// Register pages per wave: the page being consumed and the next one in flight
+// (3 or 4 measured no faster, for bf16 and for fp8 pages, and cost occupancy).
+constexpr int kRing = 2;
 
 template <int DH, int G>
 struct DecodeShape {
@@ -51,12 +59,85 @@ __device__ __forceinline__ void wave_lds_sync() {
 // K/V rows as stored: T itself, or fp8 e4m3 decoded to T (K, exactly: every
 // e4m3 value is a bf16 and an f16) or to f32 (V) right after the load. A lane's
 // 8 elements are one 16-byte load of T or one 8-byte load of fp8.
+// Packed pairs of the model dtype for the P.V dot products.
+template <typename T>
+struct Dot2;
+template <>
+struct Dot2<bf16_t> {
+  typedef __bf16 pair __attribute__((ext_vector_type(2)));
+  static __device__ __forceinline__ float run(pair a, pair b, float c) {
+#if __HIP_DEVICE_COMPILE__
+    return __builtin_amdgcn_fdot2_f32_bf16(a, b, c, false);
+#else
+    return c;
+#endif
+  }
+  // Two e4m3 codes of a word (bytes 0, 1, or 2, 3 with HI) as a pair, exactly.
+  template <bool HI>
+  static __device__ __forceinline__ pair from_fp8(uint32_t w) {
+#if __HIP_DEVICE_COMPILE__
+    return __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, HI);
+#else
+    (void)w;
+    return pair{};
+#endif
+  }
+};
+template <>
+struct Dot2<_Float16> {
+  typedef _Float16 pair __attribute__((ext_vector_type(2)));
+  static __device__ __forceinline__ float run(pair a, pair b, float c) {
+#if __HIP_DEVICE_COMPILE__
+    return __builtin_amdgcn_fdot2(a, b, c, false);
+#else
+    return c;
+#endif
+  }
+  template <bool HI>
+  static __device__ __forceinline__ pair from_fp8(uint32_t w) {
+#if __HIP_DEVICE_COMPILE__
+    return __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w, 1.0f, HI);
+#else
+    (void)w;
+    return pair{};
+#endif
+  }
+};
+
+template <typename P>
+__device__ __forceinline__ P pair_bits(uint32_t w) {
+  P r;
+  __builtin_memcpy(&r, &w, 4);
+  return r;
+}
+
+// Byte permute: byte i of the result is byte sel_i of (hi : lo), bytes 0-3 from
+// lo and 4-7 from hi.
+__device__ __forceinline__ uint32_t byte_perm(uint32_t hi, uint32_t lo, uint32_t sel) {
+#if __HIP_DEVICE_COMPILE__
+  return __builtin_amdgcn_perm(hi, lo, sel);
+#else
+  (void)hi, (void)sel;
+  return lo;
+#endif
+}
+
 template <typename T, typename KV>
 struct PageIO {
   typedef uint4 raw;
+  typedef typename Dot2<T>::pair pair;
   static __device__ __forceinline__ raw load(const KV *p) { return ld16_stream(p); }
   static __device__ __forceinline__ typename Mfma<T>::v8 k_operand(raw r) { return as_v8<T>(r); }
-  static __device__ __forceinline__ void v_floats(raw r, float *f) { unpack<T>(r, f); }
+  // Rows t0, t1 (8 elements each) as token pairs: vp[d] = {row t0[d], row t1[d]}.
+  static __device__ __forceinline__ void v_pairs(raw t0, raw t1, pair (&vp)[8]) {
+    const uint32_t a[4] = {t0.x, t0.y, t0.z, t0.w}, b[4] = {t1.x, t1.y, t1.z, t1.w};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      vp[2 * k] = pair_bits<pair>(byte_perm(b[k], a[k], 0x05040100u));
+      vp[2 * k + 1] = pair_bits<pair>(byte_perm(b[k], a[k], 0x07060302u));
+    }
+  }
+  static __device__ __forceinline__ raw zero() { return make_uint4(0, 0, 0, 0); }
 };
 template <typename T>
 struct PageIO<T, fp8e4m3_t> {
@@ -93,10 +174,22 @@ struct PageIO<T, fp8e4m3_t> {
 #endif
     return o;
   }
-  static __device__ __forceinline__ void v_floats(raw r, float *f) {
-    fp8x4_to_float(r.x, f);
-    fp8x4_to_float(r.y, f + 4);
+  typedef typename Dot2<T>::pair pair;
+  // Rows t0, t1 (8 e4m3 codes each) as token pairs of T, decoded exactly: the
+  // permutes put (t0[d], t1[d]) side by side, one conversion decodes a pair.
+  static __device__ __forceinline__ void v_pairs(raw t0, raw t1, pair (&vp)[8]) {
+    const uint32_t a[2] = {t0.x, t0.y}, b[2] = {t1.x, t1.y};
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      const uint32_t x = byte_perm(b[k], a[k], 0x05010400u);  // t0.0 t1.0 t0.1 t1.1
+      const uint32_t y = byte_perm(b[k], a[k], 0x07030602u);  // t0.2 t1.2 t0.3 t1.3
+      vp[4 * k] = Dot2<T>::template from_fp8<false>(x);
+      vp[4 * k + 1] = Dot2<T>::template from_fp8<true>(x);
+      vp[4 * k + 2] = Dot2<T>::template from_fp8<false>(y);
+      vp[4 * k + 3] = Dot2<T>::template from_fp8<true>(y);
+    }
   }
+  static __device__ __forceinline__ raw zero() { return make_uint2(0, 0); }
 };
 
 template <typename T, typename KV, int DH, int G>
@@ -120,10 +213,10 @@ __global__ __launch_bounds__(64 * kWaves) void decode_mfma_kernel(DecodeArgs a) 
   const int tg = (lane / LPR) % TG;   // P.V: token group
   const int hg = lane / (LPR * TG);   // P.V: head group
 
-  const int split = blockIdx.x;
-  const int kvh = blockIdx.y;
-  const int b = a.seq_order ? min(max(a.seq_order[blockIdx.z], 0), (int)gridDim.z - 1)
-                            : (int)blockIdx.z;
+  const int kvh = blockIdx.x;
+  const int split = blockIdx.z;
+  const int b = a.seq_order ? min(max(a.seq_order[blockIdx.y], 0), (int)gridDim.y - 1)
+                            : (int)blockIdx.y;
   // A length above the host bound is clamped so no access can leave its buffer.
   const int len = min(a.seq_lens[b], a.key_cap);
   const int n_pages = (len + BS - 1) / BS;
@@ -159,12 +252,15 @@ __global__ __launch_bounds__(64 * kWaves) void decode_mfma_kernel(DecodeArgs a) 
   for (int j = 0; j < HPL; ++j)
 #pragma unroll
     for (int d = 0; d < 8; ++d) acc[j][d] = 0.f;
+  // Per row i of this lane (head (grp*4 + i) % G, token r): m = reference max
+  // in log2 units (-inf before the first key), l = this lane's share of the sum.
   float m[4], l[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     m[i] = -INFINITY;
     l[i] = 0.f;
   }
+  const float scale_log2 = a.scale_log2;
 
   // Every page is read once: non-temporal loads.
   auto load_page = [&](int blk_reg, int idx, raw (&kr)[NC], raw (&vr)[4]) {
@@ -177,73 +273,106 @@ __global__ __launch_bounds__(64 * kWaves) void decode_mfma_kernel(DecodeArgs a) 
     for (int j = 0; j < 4; ++j) vr[j] = IO::load(vp + j * DH);
   };
 
+  using pair = typename IO::pair;
   auto consume = [&](const raw (&kr)[NC], const raw (&vr)[4], int p) {
     typename M::f4 s4 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int c = 0; c < NC; ++c) s4 = M::run(qa[c], IO::k_operand(kr[c]), s4);
     const bool valid = p * BS + r < len;
+    float sv[4];
+    bool over = false;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const float sv = valid ? s4[i] * a.scale_log2 : -INFINITY;
-      const float mn = fmaxf(m[i], row16_max(sv));
-      const float alpha = fast_exp2(m[i] - mn);
-      const float pv = fast_exp2(sv - mn);
-      m[i] = mn;
-      l[i] = l[i] * alpha + pv;
-      const int h = grp * 4 + i;
-      if (h < G) {
-        p_s[wave][h][r] = pv;
-        if (r == 0) alpha_s[wave][h] = alpha;
+      sv[i] = valid ? s4[i] * scale_log2 : -INFINITY;
+      over = over || sv[i] > m[i] + 8.f;
+    }
+    // A score more than 8 above its row's reference (every row on the first
+    // page): row maxima, new references, l rescaled here and the P.V
+    // accumulators below (alpha through LDS).
+    const bool rebase = __builtin_amdgcn_ballot_w64(over) != 0;
+    if (rebase) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float mx = row16_max(sv[i]);
+        const bool bump = mx > m[i] + 8.f;
+        const float alpha = bump ? fast_exp2(m[i] - mx) : 1.f;
+        m[i] = bump ? mx : m[i];
+        l[i] *= alpha;
+        const int h = grp * 4 + i;
+        if (h < G && r == 0) alpha_s[wave][h] = alpha;
       }
     }
-    wave_lds_sync();
-    float vf[4][8];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) IO::v_floats(vr[j], vf[j]);
+    for (int i = 0; i < 4; ++i) {
+      // m is -inf only while every score so far is (then p = 0).
+      const float pv = fast_exp2(sv[i] - (m[i] == -INFINITY ? 0.f : m[i]));
+      l[i] += pv;
+      const int h = grp * 4 + i;
+      if (h < G) p_s[wave][h][r] = pv;
+    }
+    wave_lds_sync();
+    raw vz[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) vz[j] = vr[j];
     if ((p + 1) * BS > len) {
       // The sequence's last page: rows past the last key hold whatever the pool
       // has there. Their probabilities are 0, and 0 * NaN would not be.
 #pragma unroll
       for (int j = 0; j < 4; ++j)
-        if (p * BS + tg * 4 + j >= len)
-#pragma unroll
-          for (int d = 0; d < 8; ++d) vf[j][d] = 0.f;
+        if (p * BS + tg * 4 + j >= len) vz[j] = IO::zero();
     }
+    pair vp[2][8];
+    IO::v_pairs(vz[0], vz[1], vp[0]);
+    IO::v_pairs(vz[2], vz[3], vp[1]);
 #pragma unroll
     for (int j = 0; j < HPL; ++j) {
       const int h = hg * HPL + j;
-      const float al = alpha_s[wave][h];
+      if (rebase) {
+        const float al = alpha_s[wave][h];
+#pragma unroll
+        for (int d = 0; d < 8; ++d) acc[j][d] *= al;
+      }
       const float4 pv = *reinterpret_cast<const float4 *>(&p_s[wave][h][tg * 4]);
+      pair p01, p23;
+      p01[0] = static_cast<typename M::elem>(pv.x);
+      p01[1] = static_cast<typename M::elem>(pv.y);
+      p23[0] = static_cast<typename M::elem>(pv.z);
+      p23[1] = static_cast<typename M::elem>(pv.w);
 #pragma unroll
       for (int d = 0; d < 8; ++d)
-        acc[j][d] = acc[j][d] * al + pv.x * vf[0][d] + pv.y * vf[1][d] + pv.z * vf[2][d] +
-                    pv.w * vf[3][d];
+        acc[j][d] = Dot2<T>::run(vp[1][d], p23, Dot2<T>::run(vp[0][d], p01, acc[j][d]));
     }
     wave_lds_sync();
   };
 
-  // Two register pages in flight: the steady-state loop always has the next
-  // page's loads issued behind the page being consumed (straight-line, so the
-  // wait before each consume covers only its own page); the last one or two
-  // pages of a 64-page chunk drain in the epilogue.
+  // A ring of kRing register pages: the steady-state loop always has the next
+  // kRing - 1 pages' loads issued behind the page being consumed (straight-line,
+  // so the wait before each consume covers only its own page); the last pages
+  // of a 64-page chunk drain in the epilogue.
+  constexpr int D = kRing;
   for (int c0 = w_begin; c0 < w_end; c0 += 64) {
     const int n = min(w_end, c0 + 64) - c0;
     const int blk_reg = lane < n ? bt_row[c0 + lane] : 0;
-    raw kA[NC], vA[4], kB[NC], vB[4];
-    load_page(blk_reg, 0, kA, vA);
-    int i = 0;
-    for (; i + 2 < n; i += 2) {
-      load_page(blk_reg, i + 1, kB, vB);
-      consume(kA, vA, c0 + i);
-      load_page(blk_reg, i + 2, kA, vA);
-      consume(kB, vB, c0 + i + 1);
+    raw kb[D][NC], vb[D][4];
+#pragma unroll
+    for (int j = 0; j < D - 1; ++j)
+      if (j < n) load_page(blk_reg, j, kb[j], vb[j]);
+    int i = 0;  // page i sits in ring slot i % D
+    for (; i + 2 * D - 1 <= n; i += D) {
+#pragma unroll
+      for (int j = 0; j < D; ++j) {
+        load_page(blk_reg, i + j + D - 1, kb[(j + D - 1) % D], vb[(j + D - 1) % D]);
+        consume(kb[j], vb[j], c0 + i + j);
+      }
     }
-    if (i + 1 < n) {
-      load_page(blk_reg, i + 1, kB, vB);
-      consume(kA, vA, c0 + i);
-      consume(kB, vB, c0 + i + 1);
-    } else {
-      consume(kA, vA, c0 + i);
+    // Fewer than 2D - 1 pages left; those before i + D - 1 are already loaded.
+#pragma unroll
+    for (int j = 0; j < 2 * D - 2; ++j) {
+      if (i + j < n) {
+        if (i + j + D - 1 < n)
+          load_page(blk_reg, i + j + D - 1, kb[(j + D - 1) % D], vb[(j + D - 1) % D]);
+        consume(kb[j % D], vb[j % D], c0 + i + j);
+      }
     }
   }
 
@@ -306,7 +435,9 @@ __global__ __launch_bounds__(64 * kWaves) void decode_mfma_kernel(DecodeArgs a) 
 template <typename T, typename KV>
 int32_t launch_typed(const DecodeArgs &a, int32_t num_seqs, int32_t num_kv_heads, int32_t G,
                      int32_t head_dim, hipStream_t s) {
-  const dim3 grid(a.max_splits, num_kv_heads, num_seqs);
+  // KV heads vary fastest (consecutive workgroups, dealt round-robin over the
+  // XCDs, carry equal work), splits slowest.
+  const dim3 grid(num_kv_heads, num_seqs, a.max_splits);
 #define TKS_DECODE(DH, GG)                                              \
   if (head_dim == DH && G == GG) {                                      \
     decode_mfma_kernel<T, KV, DH, GG><<<grid, 64 * kWaves, 0, s>>>(a);  \

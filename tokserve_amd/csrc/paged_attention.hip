@@ -83,8 +83,8 @@ __global__ __launch_bounds__(kGenThreads) void attn_generic_kernel(GenericArgs a
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  const int slot = blockIdx.x / a.max_splits;
-  const int split = blockIdx.x - slot * a.max_splits;
+  const int slot = blockIdx.x;
+  const int split = blockIdx.z;
   const int row = a.seq_order ? min(max(a.seq_order[slot], 0), a.num_seqs - 1) : slot;
   const int kvh = blockIdx.y;
   const int G = a.group;
@@ -421,8 +421,7 @@ PoolView make_pool(int32_t layer_index, int64_t num_blocks, int32_t num_kv_heads
 template <typename T, typename KV>
 int32_t launch_generic_kv(const GenericArgs &a, int32_t rows, int32_t num_kv_heads,
                           hipStream_t s) {
-  const dim3 grid(static_cast<unsigned>(static_cast<int64_t>(rows) * a.max_splits),
-                  num_kv_heads);
+  const dim3 grid(static_cast<unsigned>(rows), num_kv_heads, a.max_splits);
   if (a.pool.head_dim <= 64)
     attn_generic_kernel<T, KV, 64><<<grid, kGenThreads, 0, s>>>(a);
   else
@@ -509,6 +508,7 @@ int32_t decode_impl(const void *query, int64_t q_seq_stride, int64_t q_head_stri
   const int32_t pps =
       choose_pages_per_split(num_seqs, num_kv_heads, block_size, max_seq_len, pages_per_split);
   const int32_t max_splits = split_count(max_seq_len, block_size, pps);
+  if (max_splits > kMaxGridSplits) return TKS_ERR_VALUE;
   Workspace w = carve(workspace, num_seqs, num_q_heads, max_splits, head_dim);
   if (max_splits > 1 && (workspace == nullptr || workspace_bytes < w.bytes))
     return TKS_ERR_WORKSPACE;
