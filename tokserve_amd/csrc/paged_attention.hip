@@ -364,22 +364,24 @@ __global__ __launch_bounds__(64) void merge_splits_kernel(
 // Key splits for decode. A (sequence, KV head) pair runs as one workgroup
 // whose four waves walk its pages in order, so an unsplit launch lasts at least
 // as long as its longest sequence takes; with few pairs that chain, not the
-// bytes, sets the time. Below kSplitBelowItems pairs, batches whose longest
-// sequence spans at least two splits are cut into kSplitPages-page splits
+// bytes, sets the time. Below kSplitBelowItems pairs, batches whose length
+// bound reaches kSplitFromPages pages are cut into kSplitPages-page splits
 // (merged by a second launch). Measured on Llama-3-8B shapes (8 KV heads, Dh 128,
 // contexts log-uniform in [128, 8192]): 16 sequences 59 -> 44 us, 32: 107 -> 61,
 // 64: 145 -> 101, 128: 183 -> 173; 192 and 256 sequences are faster unsplit
-// (224 vs 256 us, 291 vs 302+); 128 sequences x 4 KV heads with contexts up to
-// 1152 (72 pages) stay unsplit (21 us; 24 us split in 64-page splits).
+// (224 vs 256 us, 291 vs 302+). Short contexts stay unsplit: 128 sequences x 4
+// KV heads, Dh 64, contexts up to 1152 take 20.5 us unsplit, 20.9 + 5.1 (merge)
+// split at a 2048-token bound.
 constexpr int64_t kSplitBelowItems = 1536;
 constexpr int64_t kSplitPages = 64;
+constexpr int64_t kSplitFromPages = 256;
 
 int32_t choose_pages_per_split(int32_t num_seqs, int32_t num_kv_heads, int32_t block_size,
                                int32_t max_seq_len, int32_t requested) {
   if (requested > 0) return requested;
   const int64_t max_pages = ceil_div(max_seq_len > 0 ? max_seq_len : 1, block_size);
   const int64_t items = static_cast<int64_t>(num_seqs) * num_kv_heads;
-  if (items >= kSplitBelowItems || max_pages < 2 * kSplitPages)
+  if (items >= kSplitBelowItems || max_pages < kSplitFromPages)
     return static_cast<int32_t>(max_pages);
   return static_cast<int32_t>(kSplitPages);
 }
