@@ -356,3 +356,25 @@ def test_prefill_non_positive_scale(device, dtype, sign) -> None:
     expected = paged.prefill_batch(q * sign, kc, vc, bt, lens, cu, 0, torch.float32)
     assert_close(out.cpu(), expected, **(TOL[dtype] if dtype == torch.float32 else
                                          dict(rtol=0, atol=2e-2)))
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize(("hq", "hkv", "dh"), [(32, 8, 128), (32, 4, 64), (8, 8, 128)])
+@pytest.mark.parametrize("pages_per_split", [0, 3])
+def test_decode_rising_scores_move_the_softmax_reference(device, dtype, hq, hkv, dh,
+                                                         pages_per_split) -> None:
+    """Keys scaled up page by page (x1 + i/4 for page i) so each row's running max keeps
+    rising: the decode kernel moves its lazy softmax reference and rescales l and the P.V
+    accumulators on many pages, in every wave's range and (split) every split. Outputs are
+    near one-hot, |o| up to ~5, so the bound adds one bf16 step of the stored result."""
+
+    contexts = [700, 64, 300, 1, 1500]
+    batch = workloads.paged_batch(contexts, [1] * len(contexts), num_q_heads=hq,
+                                  num_kv_heads=hkv, head_dim=dh, block_size=16, dtype=dtype,
+                                  device=device, seed=dh + hq + pages_per_split)
+    for b, context in enumerate(contexts):
+        for i in range((context + 15) // 16):
+            batch.key_cache[0, int(batch.block_tables[b, i])] *= 1 + i / 4
+    out = _decode(batch, pages_per_split=pages_per_split)
+    torch.cuda.synchronize()
+    assert_close(out.cpu(), _decode_oracle(batch, torch.float32), rtol=2 ** -7, atol=2e-2)
