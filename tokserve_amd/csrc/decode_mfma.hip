@@ -56,9 +56,6 @@ __device__ __forceinline__ void wave_lds_sync() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-// K/V rows as stored: T itself, or fp8 e4m3 decoded to T (K, exactly: every
-// e4m3 value is a bf16 and an f16) or to f32 (V) right after the load. A lane's
-// 8 elements are one 16-byte load of T or one 8-byte load of fp8.
 // Packed pairs of the model dtype for the P.V dot products.
 template <typename T>
 struct Dot2;
@@ -122,6 +119,10 @@ __device__ __forceinline__ uint32_t byte_perm(uint32_t hi, uint32_t lo, uint32_t
 #endif
 }
 
+// K/V rows as stored: T itself, or fp8 e4m3 decoded exactly to T (every e4m3
+// value is a bf16 and an f16), K as MFMA operands and V as token pairs for the
+// dot products. A lane's 8 elements of a row are one 16-byte load of T or one
+// 8-byte load of fp8.
 template <typename T, typename KV>
 struct PageIO {
   typedef uint4 raw;
