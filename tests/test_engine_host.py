@@ -202,3 +202,120 @@ def test_plan_and_request_lifecycle_checks() -> None:
     eos.append_generated_token(3)
     assert eos.completion_reason == "eos"
     assert eos.build_result().token_ids.tolist() == [[1, 3]]
+
+
+# The scheduling scenarios of tests/integration/test_continuous_batch_pressure.py:60-244 and
+# tests/integration/test_continuous_batch_engine.py:57-233 (block size 2), with the GPU
+# forward replaced by token 0: admission, FIFO order, cache pressure and membership do not
+# depend on the token values (every request ends by max_new_tokens).
+
+def _submit(scheduler, rid, prompt, n):
+    request = ScheduledRequest(rid, torch.tensor([prompt]), GenerationConfig(max_new_tokens=n))
+    scheduler.submit(request)
+    return request
+
+
+def _ids(record):
+    return (record.admitted_ids, record.prefill_ids, record.decode_ids, record.completed_ids)
+
+
+def test_arrivals_preserve_fifo_across_iteration_boundaries() -> None:
+    engine, scheduler, _, _ = _host_engine(2, 16, 2)
+    a = _submit(scheduler, "A", [1, 2], 4)
+    b = _submit(scheduler, "B", [3], 2)
+    zero = engine.step()
+    assert zero.admitted_ids == ("A", "B") and zero.prefill_ids == ("A", "B")
+    c = _submit(scheduler, "C", [4, 5, 6], 2)
+    one = engine.step()
+    assert (one.admitted_ids, one.decode_ids, one.completed_ids) == ((), ("A", "B"), ("B",))
+    assert c.state is RequestState.WAITING
+    d = _submit(scheduler, "D", [7], 1)
+    two = engine.step()
+    assert (two.admitted_ids, two.prefill_ids, two.decode_ids) == (("C",), ("C",), ("A",))
+    assert d.state is RequestState.WAITING
+    three = engine.step()
+    assert (three.decode_ids, three.completed_ids) == (("A", "C"), ("A", "C"))
+    assert d.state is RequestState.WAITING
+    four = engine.step()
+    assert (four.admitted_ids, four.prefill_ids, four.completed_ids) == (("D",), ("D",), ("D",))
+    assert scheduler.waiting_count == 0 and scheduler.running_count == 0
+    assert all(r.state is RequestState.FINISHED for r in (a, b, c, d))
+
+
+def test_cache_pressure_keeps_request_waiting_until_capacity_returns() -> None:
+    engine, scheduler, manager, _ = _host_engine(2, 3, 2)
+    _submit(scheduler, "A", [1, 2], 3)  # ceil((2 + 3) / 2) = 3 blocks: the whole pool
+    b = _submit(scheduler, "B", [3], 1)
+    zero = engine.step()
+    assert (zero.admitted_ids, zero.prefill_ids) == (("A",), ("A",))
+    assert b.state is RequestState.WAITING and scheduler.waiting_count == 1
+    one = engine.step()
+    assert (one.admitted_ids, one.decode_ids) == ((), ("A",)) and b.state is RequestState.WAITING
+    two = engine.step()
+    assert (two.decode_ids, two.completed_ids) == (("A",), ("A",))
+    assert b.state is RequestState.WAITING and manager.allocator.allocated_count == 0
+    three = engine.step()
+    assert (three.admitted_ids, three.prefill_ids, three.completed_ids) == (("B",),) * 3
+    assert b.state is RequestState.FINISHED
+    assert scheduler.waiting_count == 0 and scheduler.running_count == 0
+    assert manager.active_sequence_ids == ()
+    assert manager.allocator.allocated_count == 0 and manager.allocator.free_count == 3
+
+
+def test_waiting_order_is_unchanged_during_resource_pressure() -> None:
+    engine, scheduler, _, _ = _host_engine(3, 3, 2)
+    _submit(scheduler, "A", [1, 2], 3)
+    _submit(scheduler, "B", [3], 1)
+    _submit(scheduler, "C", [4], 1)
+    engine.step()
+    assert tuple(r.request_id for r in scheduler.waiting_requests) == ("B", "C")
+    engine.step()
+    assert tuple(r.request_id for r in scheduler.waiting_requests) == ("B", "C")
+    engine.step()
+    last = engine.step()
+    assert (last.admitted_ids, last.prefill_ids, last.completed_ids) == (("B", "C"),) * 3
+
+
+def test_batch_membership_changes_between_iterations() -> None:
+    engine, scheduler, _, _ = _host_engine(2, 16, 2)
+    _submit(scheduler, "A", [1, 2], 3)
+    _submit(scheduler, "B", [3, 4, 5], 1)
+    c = _submit(scheduler, "C", [6], 2)
+    first = engine.step()
+    assert _ids(first) == (("A", "B"), ("A", "B"), (), ("B",)) and first.active_ids == ("A",)
+    assert scheduler.get_request("B").state is RequestState.FINISHED
+    assert c.state is RequestState.WAITING
+    second = engine.step()
+    assert _ids(second) == (("C",), ("C",), ("A",), ()) and second.active_ids == ("A", "C")
+    assert c.num_generated_tokens == 1
+    third = engine.step()
+    assert _ids(third) == ((), (), ("A", "C"), ("A", "C")) and third.active_ids == ()
+    assert scheduler.waiting_count == 0 and scheduler.running_count == 0
+
+
+def test_newly_prefilled_request_waits_until_next_decode_iteration() -> None:
+    engine, scheduler, _, _ = _host_engine(1, 16, 2)
+    request = _submit(scheduler, "A", [1, 2], 3)
+    first = engine.step()
+    assert (first.prefill_ids, first.decode_ids) == (("A",), ()) and request.num_generated_tokens == 1
+    second = engine.step()
+    assert (second.prefill_ids, second.decode_ids) == ((), ("A",))
+    assert request.num_generated_tokens == 2
+
+
+def test_completed_requests_never_execute_again() -> None:
+    engine, scheduler, _, _ = _host_engine(1, 16, 2)
+    _submit(scheduler, "A", [1], 1)
+    first = engine.step()
+    second = engine.step()
+    assert first.completed_ids == ("A",)
+    assert (second.prefill_ids, second.decode_ids, second.completed_ids) == ((), (), ())
+    assert engine.executor.calls == [(1, 0)]
+
+
+def test_engine_rejects_different_cache_manager() -> None:
+    engine, scheduler, _, _ = _host_engine(1, 16, 2)
+    other = PagedKVCacheManager(num_layers=2, num_blocks=16, num_key_value_heads=2, block_size=2,
+                                head_dim=4, device=torch.device("cpu"), dtype=torch.float32)
+    with pytest.raises(ValueError, match="share the cache manager"):
+        ContinuousBatchEngine(engine.model, scheduler, other)

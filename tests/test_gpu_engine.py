@@ -220,3 +220,34 @@ def test_engine_fp8_kv_pools_fp32_tokens_identical(device, scales) -> None:
     for rid, _, _ in specs:
         assert engine.scheduler.get_request(rid).result.generated_token_ids[0].tolist() == \
             reference.finished[rid].generated, rid
+
+
+@pytest.mark.parametrize(("specs", "max_running", "num_blocks"), [
+    ((("A", [1, 2], 3), ("B", [3, 4, 5], 1), ("C", [6], 2)), 2, 16),
+    ((("A", [1, 2], 3), ("B", [3], 1)), 2, 3),
+    ((("A", [1, 2], 3), ("B", [3], 1), ("C", [4], 1)), 3, 3),
+    ((("A", [1, 2], 4), ("B", [3], 2), ("C", [4, 5, 6], 2), ("D", [7], 1)), 2, 16),
+])
+def test_engine_reference_scenarios_tokens_identical(device, specs, max_running,
+                                                     num_blocks) -> None:
+    """The request mixes of tests/integration/test_continuous_batch_engine.py:117-166 and
+    test_continuous_batch_pressure.py:60-244 (block size 2; the pools of 3 blocks make later
+    requests wait for capacity) run through the GPU engine with the fixture model: every
+    iteration record, released block list and fp32 greedy token equals the oracle engine's,
+    whose tokens are those of independent per-request generation."""
+
+    model = _fixture_model(device)
+    engine, scheduler, manager, released, reference, expected = _run_both(
+        model, device, list(specs), max_running=max_running, num_blocks=num_blocks,
+        block_size=2)
+    assert [tuple(r.__dict__.values()) for r in engine.history] == \
+        [tuple(r.__dict__.values()) for r in expected]
+    for rid, prompt, n in specs:
+        result = scheduler.get_request(rid).result
+        assert result.generated_token_ids[0].tolist() == reference.finished[rid].generated, rid
+        assert released[rid] == reference.finished[rid].released_blocks
+        alone = generate(model, torch.tensor([prompt], device=device),
+                         GenerationConfig(max_new_tokens=n))
+        assert result.token_ids.tolist() == alone.token_ids.tolist(), rid
+    assert manager.active_sequence_ids == ()
+    assert manager.allocator.free_count == num_blocks
