@@ -319,3 +319,48 @@ def test_engine_rejects_different_cache_manager() -> None:
                                 head_dim=4, device=torch.device("cpu"), dtype=torch.float32)
     with pytest.raises(ValueError, match="share the cache manager"):
         ContinuousBatchEngine(engine.model, scheduler, other)
+
+
+def test_continuous_batching_end_to_end_records() -> None:
+    """tests/integration/test_continuous_batch_end_to_end.py:58-188 (8 blocks of 2): C and D
+    arrive mid-run."""
+
+    engine, scheduler, manager, released = _host_engine(2, 8, 2)
+    requests = {"A": _submit(scheduler, "A", [1, 2], 4), "B": _submit(scheduler, "B", [3, 4, 5], 2)}
+    zero = engine.step()
+    assert (zero.iteration, *_ids(zero), zero.active_ids) == (
+        0, ("A", "B"), ("A", "B"), (), (), ("A", "B"))
+    one = engine.step()
+    assert (one.iteration, *_ids(one), one.active_ids) == (1, (), (), ("A", "B"), ("B",), ("A",))
+    requests["C"] = _submit(scheduler, "C", [6], 3)
+    two = engine.step()
+    assert (two.iteration, *_ids(two), two.active_ids) == (
+        2, ("C",), ("C",), ("A",), (), ("A", "C"))
+    requests["D"] = _submit(scheduler, "D", [7, 8, 9, 10], 1)
+    three = engine.step()
+    assert (three.iteration, *_ids(three), three.active_ids) == (
+        3, (), (), ("A", "C"), ("A",), ("C",))
+    assert requests["D"].state is RequestState.WAITING
+    four = engine.step()
+    assert (four.iteration, *_ids(four), four.active_ids) == (
+        4, ("D",), ("D",), ("C",), ("C", "D"), ())
+    assert engine.history == (zero, one, two, three, four)
+    assert all(r.state is RequestState.FINISHED for r in requests.values())
+    assert set(released) == {"A", "B", "C", "D"}
+    assert set(released["D"]) & set(released["A"] + released["B"])  # freed blocks are reused
+    assert manager.active_sequence_ids == () and manager.allocator.allocated_count == 0
+    assert manager.allocator.free_count == manager.allocator.num_blocks
+    assert scheduler.waiting_count == 0 and scheduler.running_count == 0
+
+
+def test_run_until_idle_records_every_iteration() -> None:
+    engine, scheduler, manager, _ = _host_engine(2, 16, 2)
+    _submit(scheduler, "A", [1], 2)
+    _submit(scheduler, "B", [2, 3], 3)
+    results = engine.run_until_idle()
+    assert len(results) == 2 and len(engine.history) == 3
+    assert engine.history[0].prefill_ids == ("A", "B")
+    assert (engine.history[1].decode_ids, engine.history[1].completed_ids) == (("A", "B"), ("A",))
+    assert (engine.history[2].decode_ids, engine.history[2].completed_ids) == (("B",), ("B",))
+    assert scheduler.waiting_count == 0 and scheduler.running_count == 0
+    assert manager.allocator.allocated_count == 0
