@@ -364,14 +364,20 @@ __global__ __launch_bounds__(64) void merge_splits_kernel(
 // Key splits for decode. A (sequence, KV head) pair runs as one workgroup
 // whose four waves walk its pages in order, so an unsplit launch lasts at least
 // as long as its longest sequence takes; with few pairs that chain, not the
-// bytes, sets the time. Below kSplitBelowItems pairs, batches whose length
-// bound reaches kSplitFromPages pages are cut into kSplitPages-page splits
-// (merged by a second launch). Measured on Llama-3-8B shapes (8 KV heads, Dh 128,
-// contexts log-uniform in [128, 8192]): 16 sequences 59 -> 44 us, 32: 107 -> 61,
-// 64: 145 -> 101, 128: 183 -> 173; 192 and 256 sequences are faster unsplit
-// (224 vs 256 us, 291 vs 302+). Short contexts stay unsplit: 128 sequences x 4
-// KV heads, Dh 64, contexts up to 1152 take 20.5 us unsplit, 20.9 + 5.1 (merge)
-// split at a 2048-token bound.
+// bytes, sets the time. Splits are merged by a second launch.
+//  * Fewer than kFillItems pairs (less than one workgroup per CU): cut every
+//    sequence so the batch has about kFillItems workgroups, splits of 16 to 64
+//    pages (fp32 decode step, 8 sequences x 2 KV heads, contexts <= 513: 12.8 +
+//    4.0 us merge split against 18.4 us unsplit; 16 Llama-3-8B sequences x 8 KV
+//    heads, contexts log-uniform in [128, 8192]: 59 -> 44 us at 64 pages).
+//  * Fewer than kSplitBelowItems pairs and a length bound of kSplitFromPages
+//    pages or more: 64-page splits (32 / 64 / 128 such Llama-3-8B sequences:
+//    107 / 145 / 183 -> 61 / 101 / 172 us).
+//  * Otherwise unsplit: 192 and 256 Llama-3-8B sequences (224 vs 256 us, 291 vs
+//    302+ split), and short contexts (128 sequences x 4 KV heads, Dh 64, contexts
+//    up to 1152 under a 2048-token bound: 20.5 us, 20.9 + 5.1 split).
+constexpr int64_t kFillItems = 256;
+constexpr int64_t kMinSplitPages = 16;
 constexpr int64_t kSplitBelowItems = 1536;
 constexpr int64_t kSplitPages = 64;
 constexpr int64_t kSplitFromPages = 256;
@@ -381,9 +387,13 @@ int32_t choose_pages_per_split(int32_t num_seqs, int32_t num_kv_heads, int32_t b
   if (requested > 0) return requested;
   const int64_t max_pages = ceil_div(max_seq_len > 0 ? max_seq_len : 1, block_size);
   const int64_t items = static_cast<int64_t>(num_seqs) * num_kv_heads;
-  if (items >= kSplitBelowItems || max_pages < kSplitFromPages)
-    return static_cast<int32_t>(max_pages);
-  return static_cast<int32_t>(kSplitPages);
+  if (items > 0 && items < kFillItems) {
+    const int64_t per_split = ceil_div(max_pages, ceil_div(kFillItems, items));
+    return static_cast<int32_t>(std::min(kSplitPages, std::max(kMinSplitPages, per_split)));
+  }
+  if (items < kSplitBelowItems && max_pages >= kSplitFromPages)
+    return static_cast<int32_t>(kSplitPages);
+  return static_cast<int32_t>(max_pages);
 }
 
 int32_t split_count(int32_t max_seq_len, int32_t block_size, int32_t pps) {
