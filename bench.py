@@ -206,6 +206,7 @@ def main() -> int:
             "norm_rope": measure_norm_rope(device, 20, 5),
             "small_fp32_step": measure_small_fp32_step(device, 50, 10),
             "decode_fp8_kv": measure_decode_fp8(device, args.seed, 50, 10),
+            "decode_small_batches": measure_decode_small_batches(device, args.seed, 50, 10),
         }
     if not args.no_e2e:
         e2e = measure_e2e(device, args.seed,
@@ -365,6 +366,38 @@ def measure_decode_fp8(device, seed: int, steps: int, warmup: int) -> dict:
         "algorithmic_bytes": nbytes,
         "gbps": round(nbytes / (ms * 1e-3) / 1e9, 1),
         "decode_tokens_per_s_one_layer": round(batch.num_seqs / (ms * 1e-3), 1),
+    }
+
+
+def measure_decode_small_batches(device, seed: int, steps: int, warmup: int) -> dict:
+    """The headline decode shape at 16, 32 and 64 sequences (auto key splits)."""
+
+    import torch
+
+    from tokserve_amd import workloads
+    from tokserve_amd.kernels import ops
+
+    rows = {}
+    for num_seqs in (16, 32, 64):
+        batch = workloads.decode_llama3_8b(device, seed=seed, num_seqs=num_seqs)
+        out = torch.empty_like(batch.query)
+        order = ops.longest_first(batch.contexts, device)
+
+        def step() -> None:
+            ops.paged_attention_decode(
+                batch.query, batch.key_cache, batch.value_cache, batch.block_tables,
+                batch.seq_lens, layer_index=0, max_seq_len=batch.max_seq_len, out=out,
+                seq_order=order)
+
+        ms = _time_ms(step, steps, warmup)
+        nbytes = algorithmic_bytes(batch)
+        rows[str(num_seqs)] = {"ms_per_step": round(ms, 5),
+                               "gbps": round(nbytes / (ms * 1e-3) / 1e9, 1)}
+        del batch, out
+    return {
+        "workload": "decode_llama3_8b at 16 / 32 / 64 seqs (ctx log-uniform [128, 8192], "
+                    "Hq 32 / Hkv 8, Dh 128, block 16, bf16; auto key splits)",
+        "by_num_seqs": rows,
     }
 
 
