@@ -13,7 +13,6 @@ import torch
 from torch.testing import assert_close
 
 from oracle import engine as oracle_engine
-from oracle import model as oracle_model
 from tokserve_amd.batching.engine import ContinuousBatchEngine
 from tokserve_amd.engine.config import LlamaConfig
 from tokserve_amd.engine.model import LlamaModel
