@@ -234,17 +234,24 @@ __global__ __launch_bounds__(64 * kWaves) void decode_mfma_kernel(DecodeArgs a) 
   const int w_begin = p_begin + wave * per_wave;
   const int w_end = min(p_end, w_begin + per_wave);
 
+  // The QK dot product runs over the dims in any order Q and K share. Pools in
+  // the model dtype: MFMA c takes dims c*32 + grp*8 .. +8 (one 16-byte K load
+  // each). fp8 pools: lane group grp holds the contiguous slab of dims
+  // grp*NC*8 .. +NC*8 and MFMA c its c-th 8 dims, so a lane's K bytes of a page
+  // come in NC/2 16-byte loads instead of NC 8-byte ones.
+  constexpr bool kSlab = sizeof(KV) == 1;
+  constexpr int kQStep = kSlab ? 8 : 32;
   typename M::v8 qa[NC];
   {
     const T *qp = static_cast<const T *>(a.q) + b * a.q_ss + (int64_t)(kvh * G + r % G) * a.q_hs +
-                  grp * 8;
+                  grp * (kSlab ? NC * 8 : 8);
 #pragma unroll
-    for (int c = 0; c < NC; ++c) qa[c] = as_v8<T>(ld16(qp + c * 32));
+    for (int c = 0; c < NC; ++c) qa[c] = as_v8<T>(ld16(qp + c * kQStep));
   }
 
   const KV *kc = static_cast<const KV *>(a.kc) + a.pool.layer_base + (int64_t)kvh * a.pool.head_stride;
   const KV *vc = static_cast<const KV *>(a.vc) + a.pool.layer_base + (int64_t)kvh * a.pool.head_stride;
-  const int k_off = r * DH + grp * 8;
+  const int k_off = r * DH + grp * (kSlab ? NC * 8 : 8);
   const int v_off = tg * 4 * DH + dc * 8;
   const int32_t *bt_row = a.bt + (int64_t)b * a.bt_stride;
 
@@ -268,8 +275,18 @@ __global__ __launch_bounds__(64 * kWaves) void decode_mfma_kernel(DecodeArgs a) 
     const int64_t blk = clamp_block(__builtin_amdgcn_readlane(blk_reg, idx), a.pool.num_blocks);
     const KV *kp = kc + blk * a.pool.block_stride + k_off;
     const KV *vp = vc + blk * a.pool.block_stride + v_off;
+    if constexpr (kSlab) {
+      static_assert(NC % 2 == 0, "fp8 K slab in 16-byte loads");
 #pragma unroll
-    for (int c = 0; c < NC; ++c) kr[c] = IO::load(kp + c * 32);
+      for (int c = 0; c < NC; c += 2) {
+        const uint4 u = ld16_stream(kp + c * 8);
+        kr[c] = raw{u.x, u.y};
+        kr[c + 1] = raw{u.z, u.w};
+      }
+    } else {
+#pragma unroll
+      for (int c = 0; c < NC; ++c) kr[c] = IO::load(kp + c * 32);
+    }
 #pragma unroll
     for (int j = 0; j < 4; ++j) vr[j] = IO::load(vp + j * DH);
   };
