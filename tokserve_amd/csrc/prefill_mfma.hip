@@ -39,7 +39,15 @@ namespace {
 constexpr int kPWaves = 4;
 constexpr int kXcds = 8;  // MI355X: 8 accelerator dies, workgroups dealt round-robin
 constexpr int kKeysPerStep = 32;
-constexpr int kStages = 3;  // LDS ring: steps s+1 and s+2 load while step s computes
+// LDS ring stages. Dh 128 runs its steps in pairs over 4 stages: the wait for
+// the next pair's loads and the workgroup barrier come once per pair, and the
+// second step's K tile is read right behind the first step's PV MFMAs; the
+// next pair loads meanwhile. Dh 64 keeps 3 stages (steps s+1 and s+2 load while
+// step s computes, one barrier per step) so that 4 workgroups fit a CU's LDS.
+template <int DH>
+constexpr bool kPairSteps = DH == 128;
+template <int DH>
+constexpr int kStagesOf = kPairSteps<DH> ? 4 : 3;
 
 typedef __attribute__((address_space(3))) void lds_void;
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
@@ -251,7 +259,7 @@ struct Swizzle {
   }
 };
 
-// Waves per SIMD the register budget is cut for: Dh 128 (64 KB of LDS per
+// Waves per SIMD the register budget is cut for: Dh 128 (80 KB of LDS per
 // workgroup) runs 2 workgroups per CU, Dh 64 (40 KB) fits 4 in LDS and, at 128
 // registers, 4 waves per SIMD (measured 448 -> 372 us on a 63k-token Dh 64 prefill).
 template <int DH>
@@ -265,6 +273,8 @@ __global__ __launch_bounds__(64 * kPWaves) __attribute__((amdgpu_waves_per_eu(
   constexpr int NC = DH / 32;            // QK k-chunks
   constexpr int DT = DH / 16;            // PV output dim tiles
   constexpr int KS = kKeysPerStep;
+  constexpr bool kPairs = kPairSteps<DH>;
+  constexpr int kStages = kStagesOf<DH>;
   constexpr int CPR = DH / 8;            // 16-byte chunks per key row
   constexpr int TILE = KS * DH;          // elements of one K (or V) step tile
   constexpr int STAGE = 2 * TILE;        // K tile then V tile
@@ -429,24 +439,29 @@ __global__ __launch_bounds__(64 * kPWaves) __attribute__((amdgpu_waves_per_eu(
   settle_sgpr(vc);
   __builtin_amdgcn_s_waitcnt(0);
   {
-    int32_t blk[3][LOADS];
+    int32_t blk[kStages][LOADS];
 #pragma unroll
-    for (int i = 0; i < 3; ++i)
+    for (int i = 0; i < kStages; ++i)
 #pragma unroll
       for (int k = 0; k < LOADS; ++k) blk[i][k] = bt_s[min(page_of_load(i, k), kPrefillBtWindow - 1)];
     if (n_steps > 0) issue(Const<0>{}, blk[0]);
     if (n_steps > 1) issue(Const<1>{}, blk[1]);
     if (n_steps > 2) issue(Const<2>{}, blk[2]);
+    if constexpr (kStages > 3) {
+      if (n_steps > 3) issue(Const<3>{}, blk[3]);
+    }
   }
   using Reads = StepReads<DH>;
   constexpr int kStageBytes = STAGE * (int)sizeof(T);
   constexpr int kRowsBytes = 16 * DH * (int)sizeof(T);
   u32x4 kraw[2 * NC];  // K operands of the step about to run
   if (n_steps > 0) {
-    // Step 0's loads are the first issued: wait until only steps 1 and 2 remain.
-    if (n_steps > 2)
+    // Loads complete in issue order: wait for step 0's (with pairs, steps 0
+    // and 1), so that only the later steps' may remain.
+    constexpr int kFirst = kPairs ? 2 : 1;
+    if (n_steps > kFirst + 1)
       wait_loads_and_barrier<4 * LOADS>();
-    else if (n_steps > 1)
+    else if (n_steps > kFirst)
       wait_loads_and_barrier<2 * LOADS>();
     else
       wait_loads_and_barrier<0>();
@@ -512,17 +527,22 @@ __global__ __launch_bounds__(64 * kPWaves) __attribute__((amdgpu_waves_per_eu(
   // One step: keys s*KS .. s*KS + KS - 1 from ring stage STG, whose K operands
   // are already in kraw. Pipeline: V(s) LDS reads overlap QK(s) and the
   // softmax; tile 1's QK MFMAs run under tile 0's softmax and tile 0's PV MFMAs
-  // under tile 1's probabilities; after a barrier that also frees stage s,
-  // K(s+1) is read and the loads of step s+3 go into stage s. Steps whose keys
+  // under tile 1's probabilities; then K(s+1) is read. With one barrier per
+  // step (3 stages), the barrier before that read also frees stage s, which
+  // takes the loads of step s+3; with step pairs (4 stages) only the pair's
+  // second step waits and joins the barrier, and its stages take the loads of
+  // steps s+3 and s+4. Steps whose keys
   // reach past the wave's first query position (or past the last key) apply
   // the causal mask; uniform branches around it keep the unmasked steps free of
   // mask work.
+  int32_t blk_pair[LOADS];  // block ids of step s+3, read in the pair's first step s-1
   auto step = [&](auto stage_c, int s) {
     static_assert(RT == 2, "the step interleaves two row tiles");
     constexpr int STG = decltype(stage_c)::value;
     constexpr int O0 = STG * kStageBytes;
     constexpr int N0 = ((STG + 1) % kStages) * kStageBytes;
-    const int ahead = min(s + 3, n_steps - 1);
+    // Block ids of the step whose loads this step hands to issue().
+    const int ahead = min(s + (kPairs ? 4 : 3), n_steps - 1);
     const uint32_t ba = bt_base + page_of_load(ahead, 0) * 4;
     const bool tail = s * KS + KS > n_keys;
     const bool need_mask = s * KS + KS - 1 > min_pos || tail;
@@ -602,20 +622,41 @@ __global__ __launch_bounds__(64 * kPWaves) __attribute__((amdgpu_waves_per_eu(
     }
 
     if (s + 1 < n_steps) {
-      // Step s+1's loads done (only step s+2's may remain), and every wave is
-      // past its reads of stage s: K(s+1) can be read and stage s refilled.
-      if (s + 2 < n_steps)
-        wait_loads_and_barrier<2 * LOADS>();
-      else
-        wait_loads_and_barrier<0>();
-      Reads::template keys<N0, N0 + kRowsBytes>(ka_addr, kraw);
-      if (s + 3 < n_steps) {
-        int32_t blk[LOADS];
+      if constexpr (kPairs && STG % 2 == 0) {
+        // First step of a pair: stage s+1 arrived before the pair's barrier.
+        Reads::template keys<N0, N0 + kRowsBytes>(ka_addr, kraw);
 #pragma unroll
-        for (int k = 0; k < LOADS; ++k) blk[k] = (int32_t)bid[k];
-        issue(Const<STG>{}, blk);
+        for (int k = 0; k < LOADS; ++k) blk_pair[k] = (int32_t)bid[k];
+        Reads::wait_keys(kraw);
+      } else if constexpr (kPairs) {
+        // Second step: the next pair's loads are done and every wave is past
+        // its reads of this pair's stages, which take steps s+3 and s+4.
+        wait_loads_and_barrier<0>();
+        Reads::template keys<N0, N0 + kRowsBytes>(ka_addr, kraw);
+        if (s + 3 < n_steps) issue(Const<(STG + 3) % kStages>{}, blk_pair);
+        if (s + 4 < n_steps) {
+          int32_t blk[LOADS];
+#pragma unroll
+          for (int k = 0; k < LOADS; ++k) blk[k] = (int32_t)bid[k];
+          issue(Const<STG>{}, blk);
+        }
+        Reads::wait_keys(kraw);
+      } else {
+        // Step s+1's loads done (only step s+2's may remain), and every wave
+        // is past its reads of stage s: K(s+1) can be read and stage s refilled.
+        if (s + 2 < n_steps)
+          wait_loads_and_barrier<2 * LOADS>();
+        else
+          wait_loads_and_barrier<0>();
+        Reads::template keys<N0, N0 + kRowsBytes>(ka_addr, kraw);
+        if (s + 3 < n_steps) {
+          int32_t blk[LOADS];
+#pragma unroll
+          for (int k = 0; k < LOADS; ++k) blk[k] = (int32_t)bid[k];
+          issue(Const<STG>{}, blk);
+        }
+        Reads::wait_keys(kraw);
       }
-      Reads::wait_keys(kraw);
     }
 #pragma unroll
     for (int j = 0; j < RT; ++j) l[j] += ps[j];
@@ -625,6 +666,9 @@ __global__ __launch_bounds__(64 * kPWaves) __attribute__((amdgpu_waves_per_eu(
     step(Const<0>{}, s);
     if (s + 1 < n_steps) step(Const<1>{}, s + 1);
     if (s + 2 < n_steps) step(Const<2>{}, s + 2);
+    if constexpr (kStages > 3) {
+      if (s + 3 < n_steps) step(Const<3>{}, s + 3);
+    }
   }
 
   // Row sums over the four lane groups, then O = O^T / l for the valid rows.
