@@ -40,17 +40,41 @@ __device__ __forceinline__ float nan_max(float a, float b) { return __builtin_el
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 // Merged output element of one (row, head, dim) from n_splits partials at w.
+// The partials are read kMergeBatch splits at a time, every load of a batch
+// issued before the first is used, so a merge costs about two memory latencies
+// per batch (max, then sums) rather than two per split; the arithmetic runs in
+// split order either way.
+constexpr int kMergeBatch = 8;
 __device__ __forceinline__ float merge_splits(const float *__restrict__ ws_m,
                                               const float *__restrict__ ws_l,
                                               const float *__restrict__ ws_acc, int64_t w,
                                               int n_splits, int head_dim, int d, float *inv_l) {
   float M = -INFINITY;
-  for (int s = 0; s < n_splits; ++s) M = fmaxf(M, ws_m[w + s]);
+  for (int s0 = 0; s0 < n_splits; s0 += kMergeBatch) {
+    float mv[kMergeBatch];
+#pragma unroll
+    for (int u = 0; u < kMergeBatch; ++u) mv[u] = s0 + u < n_splits ? ws_m[w + s0 + u] : -INFINITY;
+#pragma unroll
+    for (int u = 0; u < kMergeBatch; ++u) M = fmaxf(M, mv[u]);
+  }
   float L = 0.f, o = 0.f;
-  for (int s = 0; s < n_splits; ++s) {
-    const float e = exp2f(ws_m[w + s] - M);
-    L += e * ws_l[w + s];
-    o += e * ws_acc[(w + s) * head_dim + d];
+  for (int s0 = 0; s0 < n_splits; s0 += kMergeBatch) {
+    float mv[kMergeBatch], lv[kMergeBatch], av[kMergeBatch];
+#pragma unroll
+    for (int u = 0; u < kMergeBatch; ++u) {
+      const bool in = s0 + u < n_splits;
+      mv[u] = in ? ws_m[w + s0 + u] : 0.f;
+      lv[u] = in ? ws_l[w + s0 + u] : 0.f;
+      av[u] = in ? ws_acc[(w + s0 + u) * head_dim + d] : 0.f;
+    }
+#pragma unroll
+    for (int u = 0; u < kMergeBatch; ++u) {
+      if (s0 + u < n_splits) {
+        const float e = exp2f(mv[u] - M);
+        L += e * lv[u];
+        o += e * av[u];
+      }
+    }
   }
   *inv_l = 1.f / L;
   return o;

@@ -366,10 +366,11 @@ __global__ __launch_bounds__(64) void merge_splits_kernel(
 // as long as its longest sequence takes; with few pairs that chain, not the
 // bytes, sets the time. Splits are merged by a second launch.
 //  * Fewer than kFillItems pairs (less than one workgroup per CU): cut every
-//    sequence so the batch has about kFillItems workgroups, splits of 16 to 64
+//    sequence so the batch has about kFillItems workgroups, splits of 16 to 48
 //    pages (fp32 decode step, 8 sequences x 2 KV heads, contexts <= 513: 12.8 +
-//    4.0 us merge split against 18.4 us unsplit; 16 Llama-3-8B sequences x 8 KV
-//    heads, contexts log-uniform in [128, 8192]: 59 -> 44 us at 64 pages).
+//    4.0 us merge split against 18.4 us unsplit; 8 / 16 Llama-3-8B sequences x 8
+//    KV heads, contexts log-uniform in [128, 8192]: 39.3 / 41.8 us at 64 pages,
+//    34.8 / 37.0 us at 48, 39.3 / 45.9 us at 16; 16 sequences unsplit: 59 us).
 //  * Fewer than kSplitBelowItems pairs and a length bound of kSplitFromPages
 //    pages or more: 64-page splits (32 / 64 / 128 such Llama-3-8B sequences:
 //    107 / 145 / 183 -> 61 / 101 / 172 us).
@@ -378,6 +379,7 @@ __global__ __launch_bounds__(64) void merge_splits_kernel(
 //    up to 1152 under a 2048-token bound: 20.5 us, 20.9 + 5.1 split).
 constexpr int64_t kFillItems = 256;
 constexpr int64_t kMinSplitPages = 16;
+constexpr int64_t kMaxFillSplitPages = 48;
 constexpr int64_t kSplitBelowItems = 1536;
 constexpr int64_t kSplitPages = 64;
 constexpr int64_t kSplitFromPages = 256;
@@ -389,7 +391,7 @@ int32_t choose_pages_per_split(int32_t num_seqs, int32_t num_kv_heads, int32_t b
   const int64_t items = static_cast<int64_t>(num_seqs) * num_kv_heads;
   if (items > 0 && items < kFillItems) {
     const int64_t per_split = ceil_div(max_pages, ceil_div(kFillItems, items));
-    return static_cast<int32_t>(std::min(kSplitPages, std::max(kMinSplitPages, per_split)));
+    return static_cast<int32_t>(std::min(kMaxFillSplitPages, std::max(kMinSplitPages, per_split)));
   }
   if (items < kSplitBelowItems && max_pages >= kSplitFromPages)
     return static_cast<int32_t>(kSplitPages);
