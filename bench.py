@@ -216,6 +216,8 @@ def main() -> int:
         if not args.no_secondary:
             result["secondary"]["e2e_tinyllama_fp8_kv"] = measure_e2e(
                 device, args.seed, None, kv_dtype=torch.float8_e4m3fn)
+            result["secondary"]["e2e_tinyllama_fp32"] = measure_e2e(
+                device, args.seed, None, dtype=torch.float32)
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(batch, args.cpu_seconds)
     print(json.dumps(result), flush=True)
@@ -528,12 +530,15 @@ def _e2e_engine(model, specs, device, block_size: int = 16, kv_dtype=None):
     return ContinuousBatchEngine(model, scheduler, manager)
 
 
-def measure_e2e(device, seed: int, cpu_seconds: float | None, kv_dtype=None) -> dict:
+def measure_e2e(device, seed: int, cpu_seconds: float | None, kv_dtype=None,
+                dtype=None) -> dict:
     """TinyLlama-1.1B (random init, bf16) serving 128 requests, prompts U[64, 1024],
     128 greedy tokens each, block size 16, max 128 running: the whole run through the
     continuous-batching engine, timed on the host wall clock (each step ends with its
     tokens on the host). tokens/s = generated tokens / wall time. kv_dtype
-    torch.float8_e4m3fn runs the same workload over fp8 K/V pools (scale 1)."""
+    torch.float8_e4m3fn runs the same workload over fp8 K/V pools (scale 1); dtype
+    torch.float32 runs it with the model in fp32 (the configuration whose greedy tokens
+    must equal the reference's)."""
 
     import torch
 
@@ -545,7 +550,8 @@ def measure_e2e(device, seed: int, cpu_seconds: float | None, kv_dtype=None) -> 
     torch.manual_seed(seed)
     with torch.device(device):
         model = LlamaModel(config)
-    model = model.to(torch.bfloat16).eval()
+    dtype = torch.bfloat16 if dtype is None else dtype
+    model = model.to(dtype).eval()
     specs = workloads.tinyllama_requests(seed=seed)
     # Warm-up at the timed run's shapes (a full-size prefill iteration and two decode
     # iterations of another request set): library GEMM kernels for those shapes load
@@ -571,9 +577,10 @@ def measure_e2e(device, seed: int, cpu_seconds: float | None, kv_dtype=None) -> 
         captured = graphs._graphs[max(graphs._graphs)]
         replay_ms = _time_ms(captured.graph.replay, 20, 3)
     pools = "" if kv_dtype is None else "; fp8 e4m3 K/V pools"
+    dtype_name = {torch.bfloat16: "bf16", torch.float32: "fp32"}.get(dtype, str(dtype))
     result = {
         "workload": "e2e_tinyllama: TinyLlama-1.1B shape (22 layers, hidden 2048, 32/4 heads, "
-                    "Dh 64, MLP 5632, vocab 32000), random init, bf16; 128 requests, prompts "
+                    "Dh 64, MLP 5632, vocab 32000), random init, " + dtype_name + "; 128 requests, prompts "
                     "U[64,1024], 128 greedy tokens, block 16, max_running 128" + pools,
         "requests": len(specs),
         "prompt_tokens": sum(len(s.prompt) for s in specs),

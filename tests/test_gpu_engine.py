@@ -164,6 +164,31 @@ def test_tinyllama_width_fp32_greedy_tokens_identical(device) -> None:
     assert [r.completed_ids for r in engine.history] == [r.completed_ids for r in expected]
 
 
+def test_e2e_config_fp32_greedy_tokens_identical(device) -> None:
+    """The end-to-end serving configuration's model in fp32: TinyLlama-1.1B shape (22
+    layers, hidden 2048, 32/4 heads of 64, MLP 5632, vocabulary 32000), random init under
+    a seed, the first three requests of the e2e workload (prompts of 113, 962 and 544
+    tokens) with 4 greedy tokens each, block size 16. The batched engine on the GPU and
+    the oracle engine on the host give identical tokens and iteration records."""
+
+    from tokserve_amd import workloads
+    from tokserve_amd.engine.config import tinyllama_1_1b
+
+    torch.manual_seed(0)
+    with torch.device(device):
+        model = LlamaModel(tinyllama_1_1b(max_position_embeddings=2048))
+    model = model.eval()
+    specs = [(s.request_id, list(s.prompt), 4) for s in workloads.tinyllama_requests(seed=0)[:3]]
+    blocks = sum((len(prompt) + n + 15) // 16 for _, prompt, n in specs)
+    engine, _, _, _, reference, expected = _run_both(model, device, specs, max_running=128,
+                                                     num_blocks=blocks, block_size=16)
+    for rid, _, _ in specs:
+        assert engine.scheduler.get_request(rid).result.generated_token_ids[0].tolist() == \
+            reference.finished[rid].generated, rid
+    assert [r.decode_ids for r in engine.history] == [r.decode_ids for r in expected]
+    assert [r.completed_ids for r in engine.history] == [r.completed_ids for r in expected]
+
+
 def test_decode_graph_replays_match_eager_and_oracle(device) -> None:
     """Decode-only iterations replay a captured HIP graph; between replays the engine does
     its own eager work (metadata upload, prefill of late requests, token read-back). Every
