@@ -219,6 +219,21 @@ def test_prefill_mfma_tiles(device, dtype, hq, hkv, dh, history, length) -> None
     _assert_parity(out, _prefill_oracle, batch)
 
 
+@pytest.mark.parametrize(("hq", "hkv", "dh"), [(32, 8, 128), (32, 4, 64)])
+@pytest.mark.parametrize("n_keys", [64, 65, 96, 97, 128, 129, 160, 192, 193, 224, 256, 289])
+def test_prefill_mfma_key_step_counts(device, hq, hkv, dh, n_keys) -> None:
+    """Every count of 32-key steps from 2 to 10, whole and with a partial last step: the
+    paired steps of the four-stage LDS ring (Dh 128) and the three-stage ring (Dh 64) at
+    each position of the ring where the keys can end."""
+
+    batch = workloads.paged_batch([n_keys], [8], num_q_heads=hq, num_kv_heads=hkv, head_dim=dh,
+                                  block_size=16, dtype=torch.bfloat16, device=device,
+                                  seed=n_keys)
+    out = _prefill(batch)
+    torch.cuda.synchronize()
+    _assert_parity(out, _prefill_oracle, batch)
+
+
 @pytest.mark.parametrize("block_size", [32, 64, 256])
 @pytest.mark.parametrize(("contexts", "qlens"), [([300, 45, 1000], [100, 45, 3]), ([17], [17])])
 def test_prefill_mfma_large_blocks(device, block_size, contexts, qlens) -> None:
