@@ -142,6 +142,37 @@ int32_t tks_paged_attention_decode(const void *query, int64_t q_seq_stride, int6
                                    tks_stream_t stream);
 
 /* ------------------------------------------------------------------------
+ * Decode attention that allocates nothing: tks_paged_attention_decode with the
+ * split-K partials in a static device buffer the library owns instead of a
+ * caller workspace. No counterpart in the reference (whose kernels allocate
+ * through torch); it is for callers that cannot allocate device memory: code
+ * under HIP graph capture, serving loops and harnesses that forbid hipMalloc.
+ *   - Same arguments and results as tks_paged_attention_decode, minus the
+ *     workspace. The call makes no hipMalloc / hipFree or allocating library
+ *     call.
+ *   - The buffer holds at most
+ *     tks_paged_attention_decode_noalloc_max_workspace_bytes() bytes (32 MiB);
+ *     a batch whose tks_paged_attention_decode_workspace_bytes exceeds it gets
+ *     TKS_ERR_WORKSPACE and launches nothing.
+ *   - Each GPU holds one copy of the buffer for the life of the process; its
+ *     device address is looked up on the first call on each device, with the
+ *     calling thread's current device, which must be the device of the stream
+ *     and buffers. Every call on a GPU shares that GPU's copy: calls that can
+ *     overlap on one GPU (different streams, or threads without ordering) race
+ *     and must be serialised by the caller. No initial contents are needed.
+ */
+int64_t tks_paged_attention_decode_noalloc_max_workspace_bytes(void);
+
+int32_t tks_paged_attention_decode_noalloc(
+    const void *query, int64_t q_seq_stride, int64_t q_head_stride, const void *key_cache,
+    const void *value_cache, int32_t num_layers, int64_t num_blocks, int32_t num_kv_heads,
+    int32_t block_size, int32_t head_dim, int32_t layer_index, const int32_t *block_tables,
+    int32_t block_table_stride, const int32_t *seq_lens, const int32_t *seq_order,
+    int32_t num_seqs, int32_t num_q_heads, int32_t max_seq_len, float scale,
+    int32_t pages_per_split, void *out, int64_t out_seq_stride, int64_t out_head_stride,
+    int32_t dtype, tks_stream_t stream);
+
+/* ------------------------------------------------------------------------
  * Paged attention over a ragged batch of query chunks (chunked prefill).
  * Replaces triton_paged_attention for Tq >= 1 with query_position_offset
  * (tokserve/kernels/paged_attention.py:11-88) and the contiguous

@@ -21,6 +21,16 @@
 #include "attention_common.hpp"
 
 #include <algorithm>
+#include <atomic>
+#include <mutex>
+
+// Split-K partials of tks_paged_attention_decode_noalloc, for callers that may
+// not allocate (code under HIP graph capture, serving loops that forbid
+// allocation). Every GPU the library runs on holds its own copy until the
+// process ends. Host code never uses this name as an address: the device
+// address of each GPU's copy comes from hipGetSymbolAddress (scratch_address).
+constexpr int64_t kStaticScratchBytes = int64_t{32} << 20;
+static __device__ __align__(256) unsigned char scratch[kStaticScratchBytes];
 
 namespace tks {
 namespace {
@@ -655,7 +665,66 @@ int32_t prefill_impl(const void *query, int64_t q_token_stride, int64_t q_head_s
   return launch_generic(a, dtype, static_cast<int32_t>(num_tokens), num_kv_heads, fp8_pools, s);
 }
 
+// Device address of `scratch` on the calling thread's current device, looked
+// up once per device (with that device current) and kept.
+constexpr int kMaxScratchDevices = 64;
+std::atomic<void *> g_scratch_ptr[kMaxScratchDevices];
+std::mutex g_scratch_mutex;
+
+int32_t scratch_address(void **ptr) {
+  int device = -1;
+  hipError_t err = hipGetDevice(&device);
+  if (err != hipSuccess) {
+    set_hip_error(err);
+    return TKS_ERR_LAUNCH;
+  }
+  if (device < 0 || device >= kMaxScratchDevices) return TKS_ERR_VALUE;
+  void *known = g_scratch_ptr[device].load(std::memory_order_acquire);
+  if (known == nullptr) {
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    known = g_scratch_ptr[device].load(std::memory_order_relaxed);
+    if (known == nullptr) {
+      err = hipGetSymbolAddress(&known, HIP_SYMBOL(scratch));
+      if (err != hipSuccess || known == nullptr) {
+        set_hip_error(err != hipSuccess ? err : hipErrorInvalidSymbol);
+        return TKS_ERR_LAUNCH;
+      }
+      g_scratch_ptr[device].store(known, std::memory_order_release);
+    }
+  }
+  *ptr = known;
+  return TKS_OK;
+}
+
 }  // namespace
+
+extern "C" int64_t tks_paged_attention_decode_noalloc_max_workspace_bytes(void) {
+  return kStaticScratchBytes;
+}
+
+extern "C" int32_t tks_paged_attention_decode_noalloc(
+    const void *query, int64_t q_seq_stride, int64_t q_head_stride, const void *key_cache,
+    const void *value_cache, int32_t num_layers, int64_t num_blocks, int32_t num_kv_heads,
+    int32_t block_size, int32_t head_dim, int32_t layer_index, const int32_t *block_tables,
+    int32_t block_table_stride, const int32_t *seq_lens, const int32_t *seq_order,
+    int32_t num_seqs, int32_t num_q_heads, int32_t max_seq_len, float scale,
+    int32_t pages_per_split, void *out, int64_t out_seq_stride, int64_t out_head_stride,
+    int32_t dtype, tks_stream_t stream) {
+  const int64_t needed = tks_paged_attention_decode_workspace_bytes(
+      num_seqs, num_q_heads, num_kv_heads, head_dim, block_size, max_seq_len, pages_per_split);
+  if (needed < 0) return TKS_ERR_VALUE;
+  if (needed > kStaticScratchBytes) return TKS_ERR_WORKSPACE;
+  void *ws = nullptr;
+  if (needed > 0) {
+    const int32_t st = scratch_address(&ws);
+    if (st != TKS_OK) return st;
+  }
+  return decode_impl(query, q_seq_stride, q_head_stride, key_cache, value_cache, num_layers,
+                     num_blocks, num_kv_heads, block_size, head_dim, layer_index, block_tables,
+                     block_table_stride, seq_lens, seq_order, num_seqs, num_q_heads, max_seq_len,
+                     scale, pages_per_split, out, out_seq_stride, out_head_stride, ws,
+                     needed > 0 ? kStaticScratchBytes : 0, false, 1.f, 1.f, dtype, stream);
+}
 
 extern "C" int32_t tks_paged_attention_decode(
     const void *query, int64_t q_seq_stride, int64_t q_head_stride, const void *key_cache,
