@@ -1,12 +1,20 @@
 """Paged attention (decode split-K and ragged prefill) on the GPU against the CPU oracle.
 
 Tolerances (stated by the hot path's parity contract): fp32 within 1e-5
-relative (rtol 1e-5, atol 1e-6); bf16/fp16 within 2e-2 absolute of the
-reference's GPU-kernel arithmetic (fp32 scores, softmax and accumulator, one
-rounding on the store), and within the 4e-2 the reference's own tests allow
-between that kernel and its torch backend (per-op bf16 rounding). The oracle is
-the reference's torch backend (gather + repeat_kv + causal_attention,
-oracle/paged.py) run in either arithmetic.
+relative (rtol 1e-5, atol 1e-6); bf16/fp16 within 2e-2 absolute of both of the
+reference's arithmetics: its GPU kernel's (fp32 scores, softmax and accumulator,
+one rounding on the store) and its torch backend's (a rounding to the dtype after
+every op). The oracle is the reference's torch backend (gather + repeat_kv +
+causal_attention, oracle/paged.py) run in either arithmetic.
+
+Against the torch backend, 2e-2 absolute is asserted as it stands on the
+benchmark-shaped batches (Llama-3-8B decode subset, mixed-step subset, long
+contexts), whose outputs average many keys and stay small. The short synthetic
+cases (a handful of keys, |o| up to ~4) add one step of the stored dtype at the
+element's magnitude (bf16 2^-7 relative, fp16 2^-10): one bf16 step at |o| in
+[2, 4) is 0.0156, and the torch backend's own roundings put it up to 0.0234 away
+from the fp32 arithmetic on these cases (measured on the CPU), so two correct
+bf16 results can differ by more than 2e-2 there.
 """
 
 import pytest
@@ -39,17 +47,22 @@ def _decode_oracle(batch, compute_dtype=None):
     return paged.decode_batch(q, kc, vc, bt, lens, 0, compute_dtype)
 
 
-def _assert_parity(actual, oracle, batch) -> None:
-    """fp32: the oracle within 1e-5 relative. bf16/fp16: the reference kernel's fp32
-    arithmetic within 2e-2 absolute, and the torch backend's per-op rounding within the
-    4e-2 the reference allows between the two (tests/gpu/test_tiled_attention_prefill.py:50-59)."""
+STEP = {torch.bfloat16: 2.0 ** -7, torch.float16: 2.0 ** -10}
+
+
+def _assert_parity(actual, oracle, batch, *, strict: bool = False) -> None:
+    """fp32: the oracle within 1e-5 relative. bf16/fp16: within 2e-2 absolute of the
+    reference kernel's fp32 arithmetic, and of the torch backend's per-op rounding; for
+    the latter, unless `strict`, plus one step of the stored dtype (see the module
+    docstring)."""
 
     actual = actual.cpu()
     if actual.dtype == torch.float32:
         assert_close(actual, oracle(batch, None), **TOL[torch.float32])
         return
     assert_close(actual, oracle(batch, torch.float32), rtol=0, atol=2e-2)
-    assert_close(actual, oracle(batch, None), rtol=0, atol=4e-2)
+    per_op = oracle(batch, None)
+    assert_close(actual, per_op, rtol=0 if strict else STEP[actual.dtype], atol=2e-2)
 
 
 def test_decode_fp32_small_config(device) -> None:
@@ -131,7 +144,7 @@ def test_decode_llama3_8b_subset_matches_oracle(device) -> None:
     batch = workloads.decode_llama3_8b(device, seed=1, num_seqs=24)
     out = _decode(batch)
     torch.cuda.synchronize()
-    _assert_parity(out, _decode_oracle, batch)
+    _assert_parity(out, _decode_oracle, batch, strict=True)
 
 
 def test_decode_llama3_8b_full_size_properties(device) -> None:
@@ -254,8 +267,8 @@ def test_mixed_step_subset_matches_oracle(device) -> None:
     out_p = _prefill(prefill)
     out_d = _decode(decode)
     torch.cuda.synchronize()
-    _assert_parity(out_p, _prefill_oracle, prefill)
-    _assert_parity(out_d, _decode_oracle, decode)
+    _assert_parity(out_p, _prefill_oracle, prefill, strict=True)
+    _assert_parity(out_d, _decode_oracle, decode, strict=True)
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
@@ -310,7 +323,7 @@ def test_decode_200k_token_context(device) -> None:
                                   device=device, seed=41, pool_on_device_rng=True)
     out = _decode(batch)
     torch.cuda.synchronize()
-    _assert_parity(out, _decode_oracle, batch)
+    _assert_parity(out, _decode_oracle, batch, strict=True)
 
 
 @pytest.mark.parametrize("context", [65_536, 65_552])
