@@ -5,7 +5,7 @@ and tokserve/kernels/rmsnorm.py:26-27 raise ValueError for non-device tensors)."
 import pytest
 import torch
 
-from tokserve_amd.kernels import ops
+from tokserve_amd.kernels import ops, torch_ops
 
 
 def test_cpu_tensors_are_rejected() -> None:
@@ -45,12 +45,70 @@ def test_workspace_growth_keeps_replaced_buffers_alive() -> None:
 
     cpu = torch.device("cpu")
     key = "test-growth"
-    first = ops._workspace(cpu, 100, key)
+    first = torch_ops.workspace(cpu, 100, key)
     assert first is not None and first.numel() >= 100
-    assert ops._workspace(cpu, 50, key) is first
-    grown = ops._workspace(cpu, first.numel() + 1, key)
+    assert torch_ops.workspace(cpu, 50, key) is first
+    grown = torch_ops.workspace(cpu, first.numel() + 1, key)
     assert grown is not first and grown.numel() >= 2 * first.numel()
-    assert any(t is first for t in ops._retired)
-    other = ops._workspace(cpu, 10, key + "-other")
+    assert any(t is first for t in torch_ops._retired)
+    other = torch_ops.workspace(cpu, 10, key + "-other")
     assert other is not grown
-    assert ops._workspace(cpu, 0, key) is None
+    assert torch_ops.workspace(cpu, 0, key) is None
+
+
+def test_every_operator_is_registered_with_its_writes_marked() -> None:
+    """Each C-ABI kernel family is a torch.library operator; the tensors it writes (KV
+    pools, outputs, in-place rotations) are marked mutable in its schema, and nothing
+    else is."""
+
+    writes = {
+        "kv_append": {"key_cache", "value_cache"},
+        "paged_gather": {"key_out", "value_out"},
+        "paged_attention_decode": {"out", "workspace"},
+        "paged_attention_decode_noalloc": {"out"},
+        "paged_attention_prefill": {"out"},
+        "rms_norm": {"out", "residual_out"},
+        "rope": {"query_out", "key_out"},
+        "rope_": {"query", "key"},
+        "rope_kv_append": {"key_cache", "value_cache", "query_out", "key_out"},
+        "rope_kv_append_": {"query", "key_cache", "value_cache", "key_out"},
+        "greedy_argmax": {"out"},
+        "silu_mul": {"out"},
+        "vector_add": {"out"},
+    }
+    assert set(torch_ops.SCHEMAS) == set(writes)
+    for name, expected in writes.items():
+        schema = getattr(torch.ops.tokserve_amd, name).default._schema
+        mutated = {a.name for a in schema.arguments if a.alias_info is not None
+                   and a.alias_info.is_write}
+        assert mutated == expected, name
+        assert not schema.returns, name
+
+
+def test_entry_points_behind_the_operators_cover_the_c_abi() -> None:
+    from tokserve_amd.kernels import _lib
+
+    covered = {entry for entries in torch_ops.ENTRY_POINTS.values() for entry in entries}
+    infrastructure = {"tks_abi_version", "tks_status_string", "tks_last_hip_error"}
+    assert covered | infrastructure == set(_lib.SIGNATURES)
+
+
+def test_operators_have_no_cpu_kernel() -> None:
+    with pytest.raises(NotImplementedError):
+        torch.ops.tokserve_amd.vector_add(torch.ones(3), torch.ones(3), torch.empty(3))
+
+
+def test_operators_trace_with_fake_tensors() -> None:
+    """FakeTensor propagation runs the fake kernels (no device, no library call)."""
+
+    from torch._subclasses.fake_tensor import FakeTensorMode
+
+    with FakeTensorMode():
+        q = torch.empty(4, 8, 64, dtype=torch.bfloat16, device="cuda")
+        pool = torch.empty(1, 16, 2, 16, 64, dtype=torch.bfloat16, device="cuda")
+        tables = torch.zeros(4, 4, dtype=torch.int32, device="cuda")
+        lens = torch.ones(4, dtype=torch.int32, device="cuda")
+        out = torch.empty_like(q)
+        torch.ops.tokserve_amd.paged_attention_decode(q, pool, pool, tables, lens, None, 0, 64,
+                                                      0.125, 0, 1.0, 1.0, out, None)
+        assert out.shape == q.shape

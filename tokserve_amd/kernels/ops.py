@@ -1,10 +1,13 @@
-"""Batched device operators of the hot path, one C-ABI call each.
+"""Batched device operators of the hot path.
 
 These take the packed ragged-batch metadata (`cu_seqlens`, `block_tables`,
 `seq_lens`, `slot_mapping`, `positions`) that tokserve/batching lacks (it runs
 one request at a time, tokserve/batching/execution.py:33,81). Every function
-validates shapes and devices on the host, then enqueues the kernel on the
-current torch stream. Tensors must live on a HIP device: there is no CPU path.
+validates shapes and devices with the reference's exception types, allocates
+the outputs the caller did not pass, and calls one PyTorch operator
+(`torch.ops.tokserve_amd.*`, registered in torch_ops.py), whose device kernel
+enqueues one C-ABI entry point on the current torch stream. Tensors must live
+on a HIP device: there is no CPU path.
 """
 
 from __future__ import annotations
@@ -13,7 +16,9 @@ from math import sqrt
 
 import torch
 
-from tokserve_amd.kernels import _lib
+from tokserve_amd.kernels import torch_ops
+
+_ops = torch.ops.tokserve_amd
 
 
 def require_hip(operation: str, *tensors: torch.Tensor) -> torch.device:
@@ -108,24 +113,7 @@ def kv_append(
     slots = _int_tensor(slot_mapping, torch.int64, "slot_mapping")
     key = _last_dim_contiguous(key, "key")
     value = _last_dim_contiguous(value, "value")
-    if fp8:
-        status = _lib.load().tks_kv_append_fp8(
-            key.data_ptr(), key.stride(0), key.stride(1),
-            value.data_ptr(), value.stride(0), value.stride(1),
-            key.shape[0], key_cache.data_ptr(), value_cache.data_ptr(),
-            num_layers, num_blocks, num_kv_heads, block_size, head_dim, layer_index,
-            slots.data_ptr(), k_scale, v_scale, _lib.dtype_code(key.dtype), _lib.stream_of(key),
-        )
-        _lib.check(status, "kv_append")
-        return
-    status = _lib.load().tks_kv_append(
-        key.data_ptr(), key.stride(0), key.stride(1),
-        value.data_ptr(), value.stride(0), value.stride(1),
-        key.shape[0], key_cache.data_ptr(), value_cache.data_ptr(),
-        num_layers, num_blocks, num_kv_heads, block_size, head_dim, layer_index,
-        slots.data_ptr(), _lib.dtype_code(key.dtype), _lib.stream_of(key),
-    )
-    _lib.check(status, "kv_append")
+    _ops.kv_append(key, value, key_cache, value_cache, slots, layer_index, k_scale, v_scale)
 
 
 def paged_gather(
@@ -171,24 +159,8 @@ def paged_gather(
     k_scale, v_scale = _pool_scales(key_cache, k_scale, v_scale)
     if value_out.dtype != key_out.dtype or (not fp8 and key_out.dtype != key_cache.dtype):
         raise ValueError("outputs must match the storage dtype")
-    if fp8:
-        status = _lib.load().tks_paged_gather_fp8(
-            key_cache.data_ptr(), value_cache.data_ptr(), num_layers, num_blocks, num_kv_heads,
-            block_size, head_dim, layer_index, tables.data_ptr(), tables.shape[1],
-            lens.data_ptr(), cu.data_ptr(), tables.shape[0], max_seq_len,
-            key_out.data_ptr(), value_out.data_ptr(), key_out.stride(0), key_out.stride(1),
-            k_scale, v_scale, _lib.dtype_code(key_out.dtype), _lib.stream_of(key_cache),
-        )
-        _lib.check(status, "paged_gather")
-        return
-    status = _lib.load().tks_paged_gather(
-        key_cache.data_ptr(), value_cache.data_ptr(), num_layers, num_blocks, num_kv_heads,
-        block_size, head_dim, layer_index, tables.data_ptr(), tables.shape[1],
-        lens.data_ptr(), cu.data_ptr(), tables.shape[0], max_seq_len,
-        key_out.data_ptr(), value_out.data_ptr(), key_out.stride(0), key_out.stride(1),
-        _lib.dtype_code(key_cache.dtype), _lib.stream_of(key_cache),
-    )
-    _lib.check(status, "paged_gather")
+    _ops.paged_gather(key_cache, value_cache, tables, lens, cu, layer_index, max_seq_len,
+                      key_out, value_out, k_scale, v_scale)
 
 
 # ----------------------------------------------------------------------------
@@ -206,40 +178,8 @@ def decode_workspace_bytes(
 ) -> int:
     """Bytes of split-K scratch the decode kernel needs for this batch."""
 
-    size = _lib.load().tks_paged_attention_decode_workspace_bytes(
-        num_seqs, num_q_heads, num_kv_heads, head_dim, block_size, max_seq_len,
-        pages_per_split,
-    )
-    if size < 0:
-        raise ValueError("invalid decode workspace query")
-    return int(size)
-
-
-_workspaces: dict[tuple[torch.device, str], torch.Tensor] = {}
-# Buffers replaced by larger ones stay allocated: a captured HIP graph keeps the
-# device address it was recorded with, and a freed buffer could be handed to
-# another tensor while such a graph still writes into it.
-_retired: list[torch.Tensor] = []
-
-
-def _workspace(device: torch.device, nbytes: int, key: str) -> torch.Tensor | None:
-    """A per-(device, use) scratch buffer of at least nbytes (None for 0 bytes).
-
-    Growth doubles the buffer; the old one is kept alive (see _retired). Calls
-    that share a buffer must be ordered on one stream, as the kernels require.
-    """
-
-    if nbytes == 0:
-        return None
-    slot = (torch.device(device), key)
-    buffer = _workspaces.get(slot)
-    if buffer is None or buffer.numel() < nbytes:
-        size = max(nbytes, 1 << 20, 0 if buffer is None else 2 * buffer.numel())
-        if buffer is not None:
-            _retired.append(buffer)
-        buffer = torch.empty(size, dtype=torch.uint8, device=device)
-        _workspaces[slot] = buffer
-    return buffer
+    return torch_ops.decode_workspace_bytes(num_seqs, num_q_heads, num_kv_heads, head_dim,
+                                            block_size, max_seq_len, pages_per_split)
 
 
 def longest_first(seq_lens: list[int], device: torch.device | str) -> torch.Tensor:
@@ -311,30 +251,50 @@ def paged_attention_decode(
         order = _int_tensor(seq_order, torch.int32, "seq_order")
         if order.shape != (num_seqs,):
             raise ValueError("seq_order must have shape (B,)")
-    library = _lib.load()
-    nbytes = decode_workspace_bytes(
-        num_seqs, num_q_heads, num_kv_heads, head_dim, block_size, max_seq_len, pages_per_split
-    )
-    if workspace is None:
-        workspace = _workspace(query.device, nbytes, "decode")
-    common = (
-        query.data_ptr(), query.stride(0), query.stride(1),
-        key_cache.data_ptr(), value_cache.data_ptr(), num_layers, num_blocks, num_kv_heads,
-        block_size, head_dim, layer_index, tables.data_ptr(), tables.shape[1],
-        lens.data_ptr(), _lib.ptr(order), num_seqs, num_q_heads, max_seq_len, scale,
-        pages_per_split,
-        out.data_ptr(), out.stride(0), out.stride(1),
-        _lib.ptr(workspace), 0 if workspace is None else workspace.numel(),
-    )
-    if fp8:
-        status = library.tks_paged_attention_decode_fp8(
-            *common, k_scale, v_scale, _lib.dtype_code(query.dtype), _lib.stream_of(query)
-        )
-    else:
-        status = library.tks_paged_attention_decode(
-            *common, _lib.dtype_code(query.dtype), _lib.stream_of(query)
-        )
-    _lib.check(status, "paged_attention_decode")
+    _ops.paged_attention_decode(query, key_cache, value_cache, tables, lens, order, layer_index,
+                                max_seq_len, float(scale), pages_per_split, k_scale, v_scale, out,
+                                workspace)
+    return out
+
+
+def paged_attention_decode_noalloc(
+    query: torch.Tensor,
+    key_cache: torch.Tensor,
+    value_cache: torch.Tensor,
+    block_tables: torch.Tensor,
+    seq_lens: torch.Tensor,
+    *,
+    layer_index: int,
+    max_seq_len: int,
+    out: torch.Tensor,
+    scale: float | None = None,
+    pages_per_split: int = 0,
+    seq_order: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """paged_attention_decode with the split partials in the library's static per-GPU
+    buffer: no device memory is allocated (the output comes from the caller). Batches
+    whose partials exceed the buffer raise ValueError; calls that can overlap on one GPU
+    race on the buffer. Pools in the query dtype."""
+
+    require_hip("paged_attention_decode", query, key_cache, value_cache, block_tables, seq_lens,
+                out)
+    _, _, num_kv_heads, _, head_dim = _pool_shape(key_cache, value_cache)
+    if query.ndim != 3 or query.shape[2] != head_dim or query.stride(-1) != 1:
+        raise ValueError("query must have shape (B, Hq, Dh) with the pool's Dh, Dh contiguous")
+    if query.dtype != key_cache.dtype:
+        raise ValueError("query and paged storage must use the same dtype")
+    if query.shape[1] % num_kv_heads != 0:
+        raise ValueError("query head count must be divisible by KV head count")
+    if out.shape != query.shape or out.dtype != query.dtype or out.stride(-1) != 1:
+        raise ValueError("out must match the query")
+    tables = _int_tensor(block_tables, torch.int32, "block_tables")
+    lens = _int_tensor(seq_lens, torch.int32, "seq_lens")
+    if tables.ndim != 2 or tables.shape[0] != query.shape[0] or lens.shape != (query.shape[0],):
+        raise ValueError("block_tables (B, max_blocks) and seq_lens (B,) must match query")
+    order = None if seq_order is None else _int_tensor(seq_order, torch.int32, "seq_order")
+    _ops.paged_attention_decode_noalloc(
+        query, key_cache, value_cache, tables, lens, order, layer_index, max_seq_len,
+        float(1.0 / sqrt(head_dim) if scale is None else scale), pages_per_split, out)
     return out
 
 
@@ -389,31 +349,8 @@ def paged_attention_prefill(
         out = torch.empty(query.shape, dtype=query.dtype, device=query.device)
     if scale is None:
         scale = 1.0 / sqrt(head_dim)
-    common = (
-        query.data_ptr(), query.stride(0), query.stride(1),
-        key_cache.data_ptr(), value_cache.data_ptr(), num_layers, num_blocks, num_kv_heads,
-        block_size, head_dim, layer_index, tables.data_ptr(), tables.shape[1],
-        lens.data_ptr(), cu.data_ptr(), num_seqs, query.shape[0], num_q_heads,
-        max_query_len, max_seq_len, scale, out.data_ptr(), out.stride(0), out.stride(1),
-    )
-    if fp8:
-        library = _lib.load()
-        nbytes = library.tks_paged_attention_prefill_fp8_workspace_bytes(
-            num_seqs, num_q_heads, num_kv_heads, head_dim, block_size, tables.shape[1],
-            max_seq_len, _lib.dtype_code(query.dtype),
-        )
-        if nbytes < 0:
-            raise ValueError("invalid fp8 prefill workspace query")
-        workspace = _workspace(query.device, nbytes, "prefill_fp8_pages")
-        status = library.tks_paged_attention_prefill_fp8(
-            *common, _lib.ptr(workspace), 0 if workspace is None else workspace.numel(),
-            k_scale, v_scale, _lib.dtype_code(query.dtype), _lib.stream_of(query)
-        )
-    else:
-        status = _lib.load().tks_paged_attention_prefill(
-            *common, _lib.dtype_code(query.dtype), _lib.stream_of(query)
-        )
-    _lib.check(status, "paged_attention_prefill")
+    _ops.paged_attention_prefill(query, key_cache, value_cache, tables, lens, cu, layer_index,
+                                 max_query_len, max_seq_len, float(scale), k_scale, v_scale, out)
     return out
 
 
@@ -460,16 +397,7 @@ def rms_norm(
         if residual_out is None:
             residual_out = torch.empty_like(inputs)
         res_out_rows = residual_out.view(-1, hidden)
-    status = _lib.load().tks_rms_norm(
-        rows_in.data_ptr(), rows_in.stride(0),
-        _lib.ptr(res_rows), 0 if res_rows is None else res_rows.stride(0),
-        _lib.ptr(res_out_rows), 0 if res_out_rows is None else res_out_rows.stride(0),
-        weight.data_ptr(), rows_out.data_ptr(), rows_out.stride(0),
-        rows_in.shape[0], hidden, float(epsilon),
-        _lib.dtype_code(inputs.dtype), _lib.dtype_code(weight.dtype), _lib.dtype_code(out_dtype),
-        _lib.stream_of(inputs),
-    )
-    _lib.check(status, "rms_norm")
+    _ops.rms_norm(rows_in, weight, float(epsilon), res_rows, rows_out, res_out_rows)
     return out
 
 
@@ -562,18 +490,10 @@ def rope(
         key_out = torch.empty(key.shape, dtype=key.dtype, device=key.device)
     if query_out.stride(-1) != 1 or key_out.stride(-1) != 1:
         raise ValueError("rope outputs must be contiguous in head_dim")
-    batch, num_q_heads, tokens, head_dim = query.shape
-    status = _lib.load().tks_rope(
-        query.data_ptr(), query_out.data_ptr(),
-        query.stride(0), query.stride(1), query.stride(2),
-        query_out.stride(0), query_out.stride(1), query_out.stride(2), num_q_heads,
-        key.data_ptr(), key_out.data_ptr(),
-        key.stride(0), key.stride(1), key.stride(2),
-        key_out.stride(0), key_out.stride(1), key_out.stride(2), key.shape[1],
-        batch, tokens, head_dim, pos.data_ptr(), table.cos.data_ptr(), table.sin.data_ptr(),
-        table.length, _lib.dtype_code(query.dtype), _lib.stream_of(query),
-    )
-    _lib.check(status, "rope")
+    if query_out is query and key_out is key:
+        _ops.rope_(query, key, pos, table.cos, table.sin)
+    else:
+        _ops.rope(query, key, pos, table.cos, table.sin, query_out, key_out)
     return query_out, key_out
 
 
@@ -627,17 +547,12 @@ def rope_kv_append(
         raise ValueError("query_out must match query and be contiguous in head_dim")
     if key_out is not None and (key_out.shape != key.shape or key_out.stride(-1) != 1):
         raise ValueError("key_out must match key and be contiguous in head_dim")
-    status = _lib.load().tks_rope_kv_append(
-        query.data_ptr(), query_out.data_ptr(), query.stride(0), query.stride(1),
-        query_out.stride(0), query_out.stride(1), query.shape[1],
-        key.data_ptr(), _lib.ptr(key_out), key.stride(0), key.stride(1),
-        0 if key_out is None else key_out.stride(0), 0 if key_out is None else key_out.stride(1),
-        value.data_ptr(), value.stride(0), value.stride(1), num_kv_heads, tokens, head_dim,
-        pos.data_ptr(), table.cos.data_ptr(), table.sin.data_ptr(), table.length,
-        key_cache.data_ptr(), value_cache.data_ptr(), num_layers, num_blocks, block_size,
-        layer_index, slots.data_ptr(), _lib.dtype_code(query.dtype), _lib.stream_of(query),
-    )
-    _lib.check(status, "rope_kv_append")
+    if query_out is query:
+        _ops.rope_kv_append_(query, key, value, pos, table.cos, table.sin, key_cache,
+                             value_cache, slots, layer_index, key_out)
+    else:
+        _ops.rope_kv_append(query, key, value, pos, table.cos, table.sin, key_cache, value_cache,
+                            slots, layer_index, query_out, key_out)
     return query_out
 
 
@@ -659,11 +574,7 @@ def greedy_argmax(logits: torch.Tensor, out: torch.Tensor | None = None) -> torc
         logits = logits.contiguous()
     if out is None:
         out = torch.empty((logits.shape[0], 1), dtype=torch.int64, device=logits.device)
-    status = _lib.load().tks_argmax(
-        logits.data_ptr(), logits.stride(0), logits.shape[0], logits.shape[1],
-        out.data_ptr(), _lib.dtype_code(logits.dtype), _lib.stream_of(logits),
-    )
-    _lib.check(status, "greedy_argmax")
+    _ops.greedy_argmax(logits, out)
     return out
 
 
@@ -681,11 +592,7 @@ def vector_add(x: torch.Tensor, y: torch.Tensor, out: torch.Tensor | None = None
         raise ValueError("x and y must be contiguous")
     if out is None:
         out = torch.empty_like(x)
-    status = _lib.load().tks_vector_add(
-        x.data_ptr(), y.data_ptr(), out.data_ptr(), x.numel(), _lib.dtype_code(x.dtype),
-        _lib.stream_of(x),
-    )
-    _lib.check(status, "vector_add")
+    _ops.vector_add(x, y, out)
     return out
 
 
@@ -703,9 +610,5 @@ def silu_mul(gate_up: torch.Tensor, out: torch.Tensor | None = None) -> torch.Te
     if out is None:
         out = torch.empty((*gate_up.shape[:-1], inter), dtype=gate_up.dtype, device=gate_up.device)
     out_rows = out.view(-1, inter)
-    status = _lib.load().tks_silu_mul(
-        rows.data_ptr(), rows.stride(0), rows.shape[0], inter, out_rows.data_ptr(),
-        out_rows.stride(0), _lib.dtype_code(gate_up.dtype), _lib.stream_of(gate_up),
-    )
-    _lib.check(status, "silu_mul")
+    _ops.silu_mul(rows, out_rows)
     return out
