@@ -61,6 +61,9 @@ class Engine:
         self.reserved: dict[str, int] = {}
         self.records: list[Record] = []
         self.finished: dict[str, Request] = {}
+        # Metrics hook calls in the reference's order (batching/engine.py:70-72,101-104,
+        # 124-128; batching/execution.py:39-61,95-96): (hook name, arguments...).
+        self.events: list[tuple] = []
 
     def submit(self, request: Request) -> None:
         self.waiting.append(request)
@@ -104,6 +107,7 @@ class Engine:
                 blocks -= need
             admitted.append(request.request_id)
             slots -= 1
+        self.events.extend(("request_admitted", rid) for rid in admitted)
         prefill = [r for r in self.running.values() if r.done is None and not r.prefilled]
         decode = [r for r in self.running.values()
                   if r.done is None and r.prefilled and r.generated]
@@ -112,15 +116,19 @@ class Engine:
                 request.prefilled = True
                 request.done = "max_new_tokens"
                 continue
+            self.events.append(("prefill_started", request.request_id))
             request.kv = oracle_model.SequenceKV()
             self._grow(request, len(request.prompt))
             token = self._next_token(request, request.prompt)
+            self.events.append(("prefill_finished", request.request_id))
             request.prefilled = True
             self._append(request, token)
+            self.events.append(("token_produced", request.request_id))
         for request in decode:
             self._grow(request, len(request.prompt) + len(request.generated))
             token = self._next_token(request, [request.generated[-1]])
             self._append(request, token)
+            self.events.append(("token_produced", request.request_id))
         completed = []
         for request in list(self.running.values()):
             if request.done is None:
@@ -134,10 +142,12 @@ class Engine:
             del self.running[request.request_id]
             self.finished[request.request_id] = request
             completed.append(request.request_id)
+            self.events.append(("complete_request", request.request_id, request.done))
         record = Record(len(self.records), tuple(admitted), tuple(r.request_id for r in prefill),
                         tuple(r.request_id for r in decode), tuple(completed),
                         tuple(self.running))
         self.records.append(record)
+        self.events.append(("record_iteration", len(prefill), len(decode)))
         return record
 
     def run(self, max_iterations: int = 10_000) -> list[Record]:

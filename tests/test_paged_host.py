@@ -80,7 +80,7 @@ def test_block_table_resolves_positions_and_slots() -> None:
     assert table.resolve(4) == PhysicalTokenLocation(2, 0)
     assert table.resolve(11) == PhysicalTokenLocation(5, 3)
     # slot = block * BS + offset, the closed form of block_table.py:53-67.
-    assert table.slots(2, 5) == [30, 31, 8, 9, 10]
+    assert table.slots(2, 5).tolist() == [30, 31, 8, 9, 10]
     with pytest.raises(IndexError, match="exceeds block table capacity"):
         table.resolve(12)
     with pytest.raises(IndexError, match="exceeds block table capacity"):
@@ -158,19 +158,19 @@ def test_sequence_allocates_exactly_the_blocks_it_needs() -> None:
     assert (cache.current_length, cache.num_blocks) == (0, 0)
     cache.begin_append(1)
     assert cache.block_ids == (0,)
-    cache._written = {0, 1}  # both layers written (the write itself needs a HIP device)
+    cache._append.written = 0b11  # both layers written (the write itself needs a HIP device)
     cache.finish_append()
     cache.begin_append(1)  # same block
     assert cache.block_ids == (0,)
-    cache._written = {0, 1}
+    cache._append.written = 0b11
     cache.finish_append()
     cache.begin_append(1)  # crosses a block boundary
     assert cache.block_ids == (0, 1)
-    cache._written = {0, 1}
+    cache._append.written = 0b11
     cache.finish_append()
     cache.begin_append(5)  # positions 3..7: blocks 1, 2, 3
     assert cache.block_ids == (0, 1, 2, 3) and cache.pending_length == 5
-    assert cache.block_table.slots(3, 5) == [3, 4, 5, 6, 7]
+    assert cache.block_table.slots(3, 5).tolist() == [3, 4, 5, 6, 7]
     assert allocator.free_count == 2
 
 

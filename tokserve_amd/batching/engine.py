@@ -1,11 +1,13 @@
 """Iteration-level continuous batching (tokserve/batching/engine.py).
 
-Each step: the scheduler admits waiting requests (FIFO under the slot and
-block limits), the running requests are planned into prefill and decode
-work, the BatchExecutor runs all of it as one packed forward, and requests
-that reached EOS or max_new_tokens are completed (their blocks released).
-The IterationRecord of every step (admitted, prefill, decode, completed and
-still-active ids) is the reference's.
+One step is four phases: admit (the scheduler's FIFO admission under the slot
+and block limits), plan (running requests split into prefill and decode
+work), run (the BatchExecutor's single packed forward) and retire (requests
+that reached EOS or max_new_tokens complete and give their blocks back). The
+step's IterationRecord (admitted, prefill, decode, completed and still-active
+ids) and the metrics hooks are the reference's: request_admitted per admitted
+request, the executor's prefill/token hooks, complete_request per completed
+request and record_iteration per step (engine.py:65-131).
 """
 
 from __future__ import annotations
@@ -13,10 +15,11 @@ from __future__ import annotations
 from dataclasses import dataclass
 
 from tokserve_amd.batching.execution import BatchExecutor
-from tokserve_amd.batching.plan import build_iteration_plan
+from tokserve_amd.batching.plan import IterationPlan, build_iteration_plan
 from tokserve_amd.engine.model import LlamaModel
 from tokserve_amd.engine.paged.manager import PagedKVCacheManager
 from tokserve_amd.generation.types import GenerationResult
+from tokserve_amd.scheduler.request import ScheduledRequest
 from tokserve_amd.scheduler.scheduler import RequestScheduler
 
 __all__ = ["IterationRecord", "ContinuousBatchEngine"]
@@ -31,19 +34,28 @@ class IterationRecord:
     completed_ids: tuple[str, ...]
     active_ids: tuple[str, ...]
 
+    @property
+    def made_progress(self) -> bool:
+        return bool(self.admitted_ids or self.prefill_ids or self.decode_ids
+                    or self.completed_ids)
+
+
+def _ids(requests: tuple[ScheduledRequest, ...] | list[ScheduledRequest]) -> tuple[str, ...]:
+    return tuple(request.request_id for request in requests)
+
 
 class ContinuousBatchEngine:
     """Advances dynamically changing requests one iteration at a time."""
 
     def __init__(self, model: LlamaModel, scheduler: RequestScheduler,
-                 cache_manager: PagedKVCacheManager) -> None:
+                 cache_manager: PagedKVCacheManager, *, metrics=None) -> None:
         if scheduler.cache_manager is not cache_manager:
             raise ValueError("scheduler and engine must share the cache manager")
         self.model = model
         self.scheduler = scheduler
         self.cache_manager = cache_manager
+        self.metrics = metrics
         self.executor = BatchExecutor(model, cache_manager)
-        self._iteration = 0
         self._history: list[IterationRecord] = []
         self._results: list[GenerationResult] = []
 
@@ -56,39 +68,50 @@ class ContinuousBatchEngine:
         return tuple(self._results)
 
     def step(self) -> IterationRecord:
-        admitted = self.scheduler.schedule().admitted_requests
+        admitted = self._admit()
         plan = build_iteration_plan(self.scheduler.running_requests)
-        self.executor.execute(plan.prefill_requests, plan.decode_requests)
-        completed: list[str] = []
-        for request in self.scheduler.running_requests:
-            if request.completion_reason is None:
-                continue
+        self.executor.execute(plan.prefill_requests, plan.decode_requests, metrics=self.metrics)
+        retired = self._retire()
+        return self._record(admitted, plan, retired)
+
+    def _admit(self) -> tuple[ScheduledRequest, ...]:
+        admitted = self.scheduler.schedule().admitted_requests
+        if self.metrics is not None:
+            for request in admitted:
+                self.metrics.request_admitted(request.request_id)
+        return admitted
+
+    def _retire(self) -> list[ScheduledRequest]:
+        finished = [r for r in self.scheduler.running_requests if r.completion_reason is not None]
+        for request in finished:
             result = request.build_result()
             self.scheduler.complete(request.request_id, result)
+            if self.metrics is not None:
+                self.metrics.complete_request(request.request_id, result.stop_reason)
             self._results.append(result)
-            completed.append(request.request_id)
+        return finished
+
+    def _record(self, admitted, plan: IterationPlan, retired) -> IterationRecord:
         record = IterationRecord(
-            iteration=self._iteration,
-            admitted_ids=tuple(r.request_id for r in admitted),
-            prefill_ids=tuple(r.request_id for r in plan.prefill_requests),
-            decode_ids=tuple(r.request_id for r in plan.decode_requests),
-            completed_ids=tuple(completed),
-            active_ids=tuple(r.request_id for r in self.scheduler.running_requests),
-        )
+            iteration=len(self._history), admitted_ids=_ids(admitted),
+            prefill_ids=_ids(plan.prefill_requests), decode_ids=_ids(plan.decode_requests),
+            completed_ids=_ids(retired), active_ids=_ids(self.scheduler.running_requests))
         self._history.append(record)
-        self._iteration += 1
+        if self.metrics is not None:
+            self.metrics.record_iteration(prefill_requests=len(plan.prefill_requests),
+                                          decode_requests=len(plan.decode_requests))
         return record
 
     def run_until_idle(self, *, max_iterations: int = 1_000) -> tuple[GenerationResult, ...]:
+        """Step until nothing waits or runs; stalls and runaway loops raise."""
+
         if max_iterations < 1:
             raise ValueError("max_iterations must be positive")
-        iterations = 0
-        while self.scheduler.waiting_count or self.scheduler.running_count:
-            if iterations >= max_iterations:
-                raise RuntimeError("continuous batching exceeded max_iterations")
-            record = self.step()
-            iterations += 1
-            if not (record.admitted_ids or record.prefill_ids or record.decode_ids
-                    or record.completed_ids):
+        for _ in range(max_iterations):
+            if not (self.scheduler.waiting_count or self.scheduler.running_count):
+                return self.results
+            if not self.step().made_progress:
                 raise RuntimeError("continuous batching cannot make progress")
+        if self.scheduler.waiting_count or self.scheduler.running_count:
+            raise RuntimeError("continuous batching exceeded max_iterations")
         return self.results

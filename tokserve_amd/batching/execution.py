@@ -7,29 +7,54 @@ every prefill chunk and every decode token in one token stream, one launch
 per kernel per layer, logits for the B last tokens only, greedy tokens for
 all B sequences from one argmax launch and one device -> host copy.
 
-What stays identical to the reference: block allocation happens in the same
-order (each prefill's begin_append in plan order, then each decode's), so
-every block id matches; each sequence's positions, causal masking and cached
-keys are its own, so its tokens match; requests with max_new_tokens == 0
-complete at prefill without a forward; the state transitions and their
-checks are the same.
+An iteration runs in three phases:
+  1. check   every request and every sequence the iteration will touch is
+             checked (states, duplicates, lengths against the model and the
+             caches) before anything changes;
+  2. reserve inside one StepReservation of the cache manager, prefills open
+             their sequences and every sequence begins its append, in plan
+             order (prefills, then decodes), so blocks come out of the pool in
+             the reference's order and every block id matches its; then the
+             packed forward runs and the reservation commits. Any failure in
+             this phase (an exhausted pool, a failed launch) rolls the
+             reservation back: the pool and every sequence are as before the
+             call, and no request has changed;
+  3. apply   tokens are appended and the metrics hooks fire, per request in
+             the reference's order: for each prefill, prefill_started,
+             prefill_finished and token_produced; then token_produced for
+             each decode. (The hooks of a prefill all fire after the packed
+             forward that served the whole iteration.)
+Requests with max_new_tokens == 0 complete at prefill without a forward or
+hooks, as in the reference.
 """
 
 from __future__ import annotations
 
+import weakref
 from collections.abc import Sequence
+from dataclasses import dataclass
 
 import torch
 
 from tokserve_amd.batching.graphs import DecodeGraphs
 from tokserve_amd.batching.metadata import PackedBatchBuilder, SequenceWork
 from tokserve_amd.engine.model import LlamaModel
-from tokserve_amd.engine.paged.manager import PagedKVCacheManager
+from tokserve_amd.engine.paged.manager import PagedKVCacheManager, StepReservation
 from tokserve_amd.generation.sampling import select_next_token
 from tokserve_amd.kernels import ops
 from tokserve_amd.scheduler.request import RequestState, ScheduledRequest
 
 __all__ = ["BatchExecutor", "execute_prefill", "execute_decode"]
+
+
+@dataclass(frozen=True)
+class _Checked:
+    """Phase 1's outcome: who runs the forward and who completes without one."""
+
+    no_tokens: tuple[ScheduledRequest, ...]   # prefills with max_new_tokens == 0
+    prefill: tuple[ScheduledRequest, ...]
+    decode: tuple[ScheduledRequest, ...]
+    decode_lengths: tuple[int, ...]            # cached positions of each decode sequence
 
 
 class BatchExecutor:
@@ -44,65 +69,65 @@ class BatchExecutor:
         graphs = DecodeGraphs(model, manager.storage)
         self.graphs = graphs if use_graphs and graphs.supported() else None
 
-    def execute(
-        self, prefill: Sequence[ScheduledRequest], decode: Sequence[ScheduledRequest]
-    ) -> tuple[str, ...]:
-        """Advance every request by one step; returns ids that reached completion."""
+    def execute(self, prefill: Sequence[ScheduledRequest], decode: Sequence[ScheduledRequest],
+                *, metrics=None) -> tuple[str, ...]:
+        """Advance every request by one step; returns the ids that reached completion."""
 
+        checked = self._check(prefill, decode)
+        tokens: list[int] = []
+        if checked.prefill or checked.decode:
+            with self.manager.reservation() as reservation:
+                pre_work, dec_work = self._reserve(reservation, checked)
+                tokens = self._forward(pre_work, dec_work, [*checked.prefill, *checked.decode])
+                reservation.commit()
+        return self._apply(prefill, checked, tokens, metrics)
+
+    # ----------------------------------------------------------- phase 1
+
+    def _check(self, prefill: Sequence[ScheduledRequest],
+               decode: Sequence[ScheduledRequest]) -> _Checked:
         _check_group(prefill, "prefill")
-        _check_group(decode, "decode")
         for request in prefill:
             if request.prefill_complete:
                 raise ValueError("request prefill is already complete")
             if request.completion_reason is not None:
                 raise ValueError("completed request cannot be prefetched")
+        _check_group(decode, "decode")
         for request in decode:
             if not request.decode_ready:
                 raise ValueError("decode requests must be decode-ready")
-
-        completed: list[str] = []
         limit = self.model.config.max_position_embeddings
-        pre_work: list[tuple[ScheduledRequest, SequenceWork]] = []
-        for request in prefill:
-            if request.generation_config.max_new_tokens == 0:
-                request.mark_prefill_complete()
-                completed.append(request.request_id)
-                continue
-            prompt = request.prompt_tokens
-            if len(prompt) > limit:
+        runs = tuple(r for r in prefill if r.generation_config.max_new_tokens)
+        for request in runs:
+            if request.sequence_length > limit:
                 raise ValueError("sequence length exceeds max_position_embeddings")
-            cache = self.manager.create_sequence(request.request_id, max_sequence_length=limit)
-            blocks = cache.reserve(len(prompt))
-            pre_work.append((request, SequenceWork(request.prompt_array, 0, blocks)))
-        dec_work: list[tuple[ScheduledRequest, SequenceWork]] = []
-        caches = []
+        lengths = []
         for request in decode:
             cache = self.manager.get_sequence(request.request_id)
-            length = cache.current_length
-            if length < 1:
+            if cache.current_length < 1:
                 raise ValueError("paged decode requires a populated cache")
-            if length >= cache.max_sequence_length:
+            if cache.current_length >= cache.max_sequence_length:
                 raise ValueError("paged cache capacity exceeded")
-            blocks = cache.reserve(1)
-            dec_work.append((request, SequenceWork((request.last_token,), length, blocks)))
-            caches.append(cache)
-        work = pre_work + dec_work
-        if not work:
-            return tuple(completed)
+            lengths.append(cache.current_length)
+        return _Checked(
+            no_tokens=tuple(r for r in prefill if not r.generation_config.max_new_tokens),
+            prefill=runs, decode=tuple(decode), decode_lengths=tuple(lengths))
 
-        tokens = self._forward([w for _, w in pre_work], [w for _, w in dec_work],
-                               [r for r, _ in work])
-        for request, _ in pre_work:
-            self.manager.get_sequence(request.request_id).commit()
-        for cache in caches:
-            cache.commit()
-        for index, (request, _) in enumerate(work):
-            if index < len(pre_work):
-                request.mark_prefill_complete()
-            request.append_generated_token(tokens[index])
-            if request.completion_reason is not None:
-                completed.append(request.request_id)
-        return tuple(completed)
+    # ----------------------------------------------------------- phase 2
+
+    def _reserve(self, reservation: StepReservation, checked: _Checked):
+        limit = self.model.config.max_position_embeddings
+        pre_work = []
+        for request in checked.prefill:
+            cache = reservation.open(request.request_id, max_sequence_length=limit)
+            prompt = request.prompt_array
+            pre_work.append(SequenceWork(prompt, 0, reservation.extend(cache, prompt.size)))
+        dec_work = [
+            SequenceWork((request.last_token,), length,
+                         reservation.extend(self.manager.get_sequence(request.request_id), 1))
+            for request, length in zip(checked.decode, checked.decode_lengths)
+        ]
+        return pre_work, dec_work
 
     def _forward(self, prefill: list[SequenceWork], decode: list[SequenceWork],
                  requests: list[ScheduledRequest]) -> list[int]:
@@ -129,6 +154,35 @@ class BatchExecutor:
                                                 generator=request.sampling_generator).view(())
         return chosen.tolist()
 
+    # ----------------------------------------------------------- phase 3
+
+    @staticmethod
+    def _apply(prefill: Sequence[ScheduledRequest], checked: _Checked, tokens: list[int],
+               metrics) -> tuple[str, ...]:
+        served = iter(tokens)
+        completed: list[str] = []
+        for request in prefill:
+            if not request.generation_config.max_new_tokens:
+                request.mark_prefill_complete()
+                completed.append(request.request_id)
+                continue
+            if metrics is not None:
+                metrics.prefill_started(request.request_id)
+                metrics.prefill_finished(request.request_id)
+            request.mark_prefill_complete()
+            _take(request, next(served), metrics, completed)
+        for request in checked.decode:
+            _take(request, next(served), metrics, completed)
+        return tuple(completed)
+
+
+def _take(request: ScheduledRequest, token: int, metrics, completed: list[str]) -> None:
+    request.append_generated_token(token)
+    if metrics is not None:
+        metrics.token_produced(request.request_id)
+    if request.completion_reason is not None:
+        completed.append(request.request_id)
+
 
 def _check_group(requests: Sequence[ScheduledRequest], kind: str) -> None:
     seen: set[str] = set()
@@ -140,15 +194,29 @@ def _check_group(requests: Sequence[ScheduledRequest], kind: str) -> None:
             raise ValueError(f"{kind} requests must be running")
 
 
+# One executor per (cache manager, model), kept while the manager lives, so that
+# callers looping over execute_decode reuse its staging buffers and decode graphs.
+_executors: weakref.WeakKeyDictionary[PagedKVCacheManager, BatchExecutor] = (
+    weakref.WeakKeyDictionary())
+
+
+def _executor_for(model: LlamaModel, manager: PagedKVCacheManager) -> BatchExecutor:
+    executor = _executors.get(manager)
+    if executor is None or executor.model is not model:
+        executor = BatchExecutor(model, manager)
+        _executors[manager] = executor
+    return executor
+
+
 def execute_prefill(model: LlamaModel, manager: PagedKVCacheManager,
-                    requests: Sequence[ScheduledRequest]) -> tuple[str, ...]:
+                    requests: Sequence[ScheduledRequest], *, metrics=None) -> tuple[str, ...]:
     """Prefill `requests` and select their first tokens (one packed forward)."""
 
-    return BatchExecutor(model, manager).execute(requests, ())
+    return _executor_for(model, manager).execute(requests, (), metrics=metrics)
 
 
 def execute_decode(model: LlamaModel, manager: PagedKVCacheManager,
-                   requests: Sequence[ScheduledRequest]) -> tuple[str, ...]:
+                   requests: Sequence[ScheduledRequest], *, metrics=None) -> tuple[str, ...]:
     """Advance decode-ready `requests` by one token (one packed forward)."""
 
-    return BatchExecutor(model, manager).execute((), requests)
+    return _executor_for(model, manager).execute((), requests, metrics=metrics)

@@ -22,6 +22,7 @@ from torch import nn
 from torch.nn import functional
 
 from tokserve_amd.engine.config import LlamaConfig
+from tokserve_amd.engine.kernel_backend import KernelBackend, check_backend
 from tokserve_amd.engine.layers import fused_weight
 from tokserve_amd.kernels import ops
 from tokserve_amd.kernels.paged_attention import hip_paged_attention
@@ -39,8 +40,9 @@ __all__ = ["GroupedQueryAttention"]
 class GroupedQueryAttention(nn.Module):
     """Llama grouped-query self-attention over paged K/V."""
 
-    def __init__(self, config: LlamaConfig) -> None:
+    def __init__(self, config: LlamaConfig, *, backend: KernelBackend = "torch") -> None:
         super().__init__()
+        self.backend = check_backend(backend)
         self.hidden_size = config.hidden_size
         self.num_attention_heads = config.num_attention_heads
         self.num_key_value_heads = config.num_key_value_heads

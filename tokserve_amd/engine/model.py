@@ -7,6 +7,9 @@ dicts are interchangeable and torch.manual_seed(s); LlamaModel(config) draws
 the same random weights in both. Pre-norm blocks: h += attn(norm(h));
 h += mlp(norm(h)); logits = lm_head(norm(h)) (model.py:45-82,117-206).
 
+`backend` ("torch" or "triton", the reference's switch, model.py:85-97) is
+checked and kept; both run the same HIP kernels.
+
 `forward` is the reference's one-sequence interface (token_ids (1, T), an
 optional SequencePagedKVCache). `forward_packed` is the batched executor's: a
 whole continuous-batching iteration (prefill chunks and decode tokens of many
@@ -23,6 +26,7 @@ from torch import nn
 
 from tokserve_amd.engine.attention import GroupedQueryAttention
 from tokserve_amd.engine.config import LlamaConfig
+from tokserve_amd.engine.kernel_backend import KernelBackend, check_backend
 from tokserve_amd.engine.layers import RMSNorm, SwiGLU
 from tokserve_amd.kernels import ops
 
@@ -37,11 +41,12 @@ __all__ = ["LlamaDecoderBlock", "LlamaModel"]
 class LlamaDecoderBlock(nn.Module):
     """One pre-norm Llama decoder block."""
 
-    def __init__(self, config: LlamaConfig) -> None:
+    def __init__(self, config: LlamaConfig, *, backend: KernelBackend = "torch") -> None:
         super().__init__()
+        self.backend = check_backend(backend)
         self.hidden_size = config.hidden_size
         self.input_norm = RMSNorm(config.hidden_size, epsilon=config.rms_norm_eps)
-        self.self_attention = GroupedQueryAttention(config)
+        self.self_attention = GroupedQueryAttention(config, backend=backend)
         self.post_attention_norm = RMSNorm(config.hidden_size, epsilon=config.rms_norm_eps)
         self.mlp = SwiGLU(config.hidden_size, config.intermediate_size)
 
@@ -66,11 +71,13 @@ class LlamaDecoderBlock(nn.Module):
 class LlamaModel(nn.Module):
     """Forward-only Llama inference model."""
 
-    def __init__(self, config: LlamaConfig) -> None:
+    def __init__(self, config: LlamaConfig, *, backend: KernelBackend = "torch") -> None:
         super().__init__()
+        self.backend = check_backend(backend)
         self.config = config
         self.embed_tokens = nn.Embedding(config.vocab_size, config.hidden_size)
-        self.layers = nn.ModuleList(LlamaDecoderBlock(config) for _ in range(config.num_hidden_layers))
+        self.layers = nn.ModuleList(LlamaDecoderBlock(config, backend=backend)
+                                    for _ in range(config.num_hidden_layers))
         self.final_norm = RMSNorm(config.hidden_size, epsilon=config.rms_norm_eps)
         self.lm_head = nn.Linear(config.hidden_size, config.vocab_size, bias=False)
         self._rotary: ops.RotaryTable | None = None

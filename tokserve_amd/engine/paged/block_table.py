@@ -1,13 +1,19 @@
 """Logical -> physical block mapping of one sequence (tokserve/engine/paged/block_table.py).
 
-Token position p lives in physical block block_ids[p // block_size] at offset
-p % block_size, i.e. in pool slot block_ids[p // block_size] * block_size +
-p % block_size (block_table.py:53-67): the slot the KV-append kernel takes.
+Token position p lives in physical block ids[p // block_size] at offset
+p % block_size, i.e. in pool slot ids[p // block_size] * block_size +
+p % block_size (block_table.py:53-67), the slot the KV-append kernel takes.
+The ids sit in a growable int64 array whose live prefix (`view()`) the batched
+executor copies straight into its block-table rows, and whose slots for a run
+of positions come out of one vectorised expression.
 """
 
 from __future__ import annotations
 
+from collections.abc import Iterable
 from dataclasses import dataclass
+
+import numpy as np
 
 __all__ = ["PhysicalTokenLocation", "SequenceBlockTable"]
 
@@ -27,47 +33,70 @@ class SequenceBlockTable:
         if block_size < 1:
             raise ValueError("block_size must be positive")
         self.block_size = block_size
-        self._ids: list[int] = []
+        self._store = np.empty(8, dtype=np.int64)
+        self._used = 0
+
+    def view(self) -> np.ndarray:
+        """The live ids (a view: valid until the table next grows or clears)."""
+
+        return self._store[: self._used]
 
     @property
     def block_ids(self) -> tuple[int, ...]:
-        return tuple(self._ids)
+        return tuple(self.view().tolist())
 
     @property
     def num_blocks(self) -> int:
-        return len(self._ids)
+        return self._used
 
     @property
     def capacity(self) -> int:
-        return len(self._ids) * self.block_size
+        return self._used * self.block_size
 
     def append_block(self, physical_block_id: int) -> None:
-        if physical_block_id < 0:
+        self.extend((physical_block_id,))
+
+    def extend(self, physical_block_ids: Iterable[int] | np.ndarray) -> None:
+        """Map the next logical blocks to these physical ids (checked before any is added)."""
+
+        new = np.asarray(physical_block_ids, dtype=np.int64).reshape(-1)
+        if (new < 0).any():
             raise ValueError("physical_block_id must be nonnegative")
-        if physical_block_id in self._ids:
+        if np.unique(new).size != new.size or np.isin(new, self.view()).any():
             raise ValueError("physical block is already in this block table")
-        self._ids.append(physical_block_id)
+        needed = self._used + new.size
+        if needed > self._store.size:
+            grown = np.empty(max(needed, 2 * self._store.size), dtype=np.int64)
+            grown[: self._used] = self.view()
+            self._store = grown
+        self._store[self._used : needed] = new
+        self._used = needed
+
+    def truncate(self, num_blocks: int) -> tuple[int, ...]:
+        """Drop the mappings past the first num_blocks and return their ids."""
+
+        dropped = tuple(self._store[num_blocks : self._used].tolist())
+        self._used = min(self._used, max(num_blocks, 0))
+        return dropped
 
     def resolve(self, position: int) -> PhysicalTokenLocation:
         if position < 0:
             raise ValueError("position must be nonnegative")
-        logical_block, offset = divmod(position, self.block_size)
-        if logical_block >= len(self._ids):
+        block, offset = divmod(position, self.block_size)
+        if block >= self._used:
             raise IndexError("position exceeds block table capacity")
-        return PhysicalTokenLocation(block_id=self._ids[logical_block], offset=offset)
+        return PhysicalTokenLocation(block_id=int(self._store[block]), offset=offset)
 
-    def slots(self, start: int, count: int) -> list[int]:
-        """Pool slots of positions start .. start+count-1 (all must be mapped)."""
+    def slots(self, start: int, count: int) -> np.ndarray:
+        """Pool slots (int64) of positions start .. start+count-1, all of them mapped."""
 
         if start < 0 or count < 0:
             raise ValueError("position must be nonnegative")
         if start + count > self.capacity:
             raise IndexError("position exceeds block table capacity")
-        size = self.block_size
-        ids = self._ids
-        return [ids[p // size] * size + p % size for p in range(start, start + count)]
+        positions = np.arange(start, start + count, dtype=np.int64)
+        return self._store[positions // self.block_size] * self.block_size + (
+            positions % self.block_size)
 
     def clear(self) -> tuple[int, ...]:
-        released = tuple(self._ids)
-        self._ids.clear()
-        return released
+        return self.truncate(0)

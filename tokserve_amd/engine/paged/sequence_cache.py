@@ -1,15 +1,23 @@
 """One sequence's blocks and logical K/V state (tokserve/engine/paged/sequence_cache.py).
 
-An append is bracketed: begin_append reserves blocks for T new positions
-(lowest free ids first), every layer then writes its (Hkv, T, Dh) K/V with
-write_layer, and finish_append makes the positions valid once all layers have
-written (sequence_cache.py:56-84,195-208). The T pool slots of an append are
-computed once, at begin_append, and each write_layer is one KV-append kernel
-launch over them; read_layer is one gather kernel launch.
+A sequence holds a block table and its valid length; an append in progress is
+one `_Append` record (where it starts, how many positions, which blocks it
+took from the pool, which layers have written, its pool slots), so the three
+ways an append ends are one line each: finish (every layer wrote, through
+write_layer), commit (a packed forward wrote every layer with one KV-append
+launch per layer over the whole batch's slots), abort (the blocks it took go
+back to the pool, for a batch that failed before its forward). The protocol
+and its checks are the reference's (sequence_cache.py:56-84,195-224):
+begin_append reserves blocks for T new positions, write_layer writes one layer's
+(Hkv, T, Dh) K/V, finish_append validates the positions once all layers wrote.
+Each write_layer is one KV-append kernel launch; read_layer is one gather launch.
 """
 
 from __future__ import annotations
 
+from dataclasses import dataclass
+
+import numpy as np
 import torch
 
 from tokserve_amd.engine.paged.allocator import PhysicalBlockAllocator
@@ -17,6 +25,15 @@ from tokserve_amd.engine.paged.block_table import SequenceBlockTable
 from tokserve_amd.engine.paged.storage import PagedKVStorage
 
 __all__ = ["SequencePagedKVCache"]
+
+
+@dataclass
+class _Append:
+    start: int               # first new position
+    count: int               # positions being appended
+    kept_blocks: int         # table length before the append took new blocks
+    written: int = 0         # bit l set: layer l has written the new positions
+    slots: torch.Tensor | None = None
 
 
 class SequencePagedKVCache:
@@ -37,159 +54,156 @@ class SequencePagedKVCache:
         self.storage = storage
         self.max_sequence_length = max_sequence_length
         self.block_table = SequenceBlockTable(storage.block_size)
-        self._length = 0
-        self._pending = 0
-        self._pending_slots: torch.Tensor | None = None
-        self._written: set[int] = set()
-        self._all_layers = frozenset(range(storage.num_layers))
-        self._released = False
+        self._valid = 0
+        self._append: _Append | None = None
+        self._every_layer = (1 << storage.num_layers) - 1
+        self._live = True
+
+    # ------------------------------------------------------------ state
 
     @property
     def current_length(self) -> int:
         """Fully written, valid token positions."""
 
-        self._require_active()
-        return self._length
+        return self._active()._valid
 
     @property
     def pending_length(self) -> int:
         """Positions reserved by the append in progress (0 if none)."""
 
-        self._require_active()
-        return self._pending
+        append = self._active()._append
+        return 0 if append is None else append.count
 
     @property
     def num_blocks(self) -> int:
-        self._require_active()
-        return self.block_table.num_blocks
+        return self._active().block_table.num_blocks
 
     @property
     def block_ids(self) -> tuple[int, ...]:
-        self._require_active()
-        return self.block_table.block_ids
+        return self._active().block_table.block_ids
+
+    # ----------------------------------------------------------- append
 
     def begin_append(self, sequence_length: int) -> None:
         """Reserve physical slots for `sequence_length` new positions."""
 
-        self._require_active()
-        if self._pending != 0:
+        self._active()
+        if self._append is not None:
             raise RuntimeError("an append is already in progress")
         if sequence_length < 1:
             raise ValueError("sequence_length must be positive")
-        new_length = self._length + sequence_length
-        if new_length > self.max_sequence_length:
+        end = self._valid + sequence_length
+        if end > self.max_sequence_length:
             raise ValueError("sequence exceeds max_sequence_length")
-        size = self.storage.block_size
-        missing = (new_length + size - 1) // size - self.block_table.num_blocks
-        if missing > 0:
-            for block_id in self.allocator.allocate_many(missing):
-                self.block_table.append_block(block_id)
-        self._pending = sequence_length
-        self._pending_slots = None
-        self._written.clear()
+        table = self.block_table
+        kept = table.num_blocks
+        short = -(-end // table.block_size) - kept
+        if short > 0:
+            table.extend(self.allocator.take_lowest(short))
+        self._append = _Append(start=self._valid, count=sequence_length, kept_blocks=kept)
+
+    def reserve(self, sequence_length: int) -> np.ndarray:
+        """begin_append for the batched executor; returns the live block ids
+        (a read-only view) that now cover the new positions."""
+
+        self.begin_append(sequence_length)
+        return self.block_table.view()
 
     def pending_slots(self) -> torch.Tensor:
         """Pool slots (int64, on the storage device) of the pending positions."""
 
-        self._require_active()
-        if self._pending == 0:
-            raise RuntimeError("begin_append must be called before write_layer")
-        if self._pending_slots is None:
-            slots = self.block_table.slots(self._length, self._pending)
-            self._pending_slots = torch.tensor(slots, dtype=torch.int64).to(self.storage.device)
-        return self._pending_slots
+        append = self._pending("begin_append must be called before write_layer")
+        if append.slots is None:
+            slots = self.block_table.slots(append.start, append.count)
+            append.slots = torch.from_numpy(slots).to(self.storage.device)
+        return append.slots
 
     def write_layer(self, layer_index: int, keys: torch.Tensor, values: torch.Tensor) -> None:
         """Write the pending positions' K/V, each shaped (Hkv, T, Dh), for one layer."""
 
-        self._require_active()
-        if self._pending == 0:
-            raise RuntimeError("begin_append must be called before write_layer")
-        if layer_index < 0 or layer_index >= self.storage.num_layers:
+        append = self._pending("begin_append must be called before write_layer")
+        if not 0 <= layer_index < self.storage.num_layers:
             raise IndexError("layer_index is out of range")
-        if layer_index in self._written:
+        if append.written >> layer_index & 1:
             raise ValueError("layer has already written this append")
-        expected = (self.storage.num_key_value_heads, self._pending, self.storage.head_dim)
+        storage = self.storage
+        expected = (storage.num_key_value_heads, append.count, storage.head_dim)
         if keys.shape != expected or values.shape != expected:
             raise ValueError("keys and values must have shape (Hkv, T, Dh)")
-        if keys.device != self.storage.device or values.device != self.storage.device:
+        if keys.device != storage.device or values.device != storage.device:
             raise ValueError("keys and values must match the storage device")
-        if keys.dtype != self.storage.dtype or values.dtype != self.storage.dtype:
+        if keys.dtype != storage.dtype or values.dtype != storage.dtype:
             raise ValueError("keys and values must match the storage dtype")
         # (T, Hkv, Dh) views: the kernel takes token and head strides.
-        self.storage.write_slots(
-            layer_index, self.pending_slots(), keys.transpose(0, 1), values.transpose(0, 1)
-        )
-        self._written.add(layer_index)
+        storage.write_slots(layer_index, self.pending_slots(), keys.transpose(0, 1),
+                            values.transpose(0, 1))
+        append.written |= 1 << layer_index
 
-    def mark_layers_written(self) -> None:
-        """Record that every layer's K/V of the pending positions was written by packed
-        KV-append launches (one per layer over a whole batch's slots)."""
+    def finish_append(self) -> None:
+        """Make the pending positions valid once every layer has written them."""
 
-        self._require_active()
-        if self._pending == 0:
-            raise RuntimeError("begin_append must be called before write_layer")
-        self._written = self._all_layers
-
-    def reserve(self, sequence_length: int) -> list[int]:
-        """begin_append for the batched executor: returns the live block-id list
-        (read-only for the caller) after reserving the new positions."""
-
-        self.begin_append(sequence_length)
-        return self.block_table._ids
+        append = self._pending("no append is in progress")
+        if append.written != self._every_layer:
+            raise RuntimeError("every layer must write before finishing an append")
+        self._close(keep=True)
 
     def commit(self) -> None:
-        """finish_append after packed KV-append launches wrote every layer."""
+        """finish_append after a packed forward's KV-append launches wrote every layer."""
 
-        if self._released:
-            raise RuntimeError("sequence cache has been released")
-        if self._pending == 0:
-            raise RuntimeError("no append is in progress")
-        self._length += self._pending
-        self._pending = 0
-        self._pending_slots = None
-        self._written = set()
+        self._pending("no append is in progress")
+        self._close(keep=True)
+
+    def abort_append(self) -> None:
+        """Drop the append in progress and return the blocks it took to the pool."""
+
+        append = self._pending("no append is in progress")
+        taken = self.block_table.truncate(append.kept_blocks)
+        if taken:
+            self.allocator.release_many(taken)
+        self._close(keep=False)
+
+    def _close(self, *, keep: bool) -> None:
+        if keep and self._append is not None:
+            self._valid += self._append.count
+        self._append = None
+
+    # ------------------------------------------------------------- read
 
     def read_layer(
         self, layer_index: int, *, include_pending: bool = False
     ) -> tuple[torch.Tensor, torch.Tensor]:
         """One layer's K/V in logical order, each shaped (1, Hkv, S, Dh)."""
 
-        self._require_active()
-        if layer_index < 0 or layer_index >= self.storage.num_layers:
+        self._active()
+        if not 0 <= layer_index < self.storage.num_layers:
             raise IndexError("layer_index is out of range")
-        length = self._length
-        if include_pending and self._pending != 0:
-            if layer_index not in self._written:
+        length = self._valid
+        append = self._append
+        if include_pending and append is not None:
+            if not append.written >> layer_index & 1:
                 raise RuntimeError("pending K/V for this layer have not been written")
-            length += self._pending
+            length += append.count
         keys, values = self.storage.gather(layer_index, self.block_table.block_ids, length)
         return keys.transpose(0, 1).unsqueeze(0), values.transpose(0, 1).unsqueeze(0)
 
-    def finish_append(self) -> None:
-        """Make the pending positions valid once every layer has written them."""
-
-        self._require_active()
-        if self._pending == 0:
-            raise RuntimeError("no append is in progress")
-        if len(self._written) != self.storage.num_layers:
-            raise RuntimeError("every layer must write before finishing an append")
-        self._length += self._pending
-        self._pending = 0
-        self._pending_slots = None
-        self._written.clear()
+    # ---------------------------------------------------------- release
 
     def release(self) -> None:
         """Return every owned block and invalidate this cache."""
 
-        self._require_active()
+        self._active()
         self.allocator.release_many(self.block_table.clear())
-        self._length = 0
-        self._pending = 0
-        self._pending_slots = None
-        self._written.clear()
-        self._released = True
+        self._valid = 0
+        self._append = None
+        self._live = False
 
-    def _require_active(self) -> None:
-        if self._released:
+    def _active(self) -> SequencePagedKVCache:
+        if not self._live:
             raise RuntimeError("sequence cache has been released")
+        return self
+
+    def _pending(self, message: str) -> _Append:
+        self._active()
+        if self._append is None:
+            raise RuntimeError(message)
+        return self._append

@@ -125,6 +125,7 @@ class PagedKVStorage:
         """Copies of one physical slot's K/V, each shaped (Hkv, Dh)."""
 
         self._check_location(layer_index, block_id, offset)
+        # The slot is position `offset` of a one-block table holding block_id.
         keys, values = self.gather(layer_index, (block_id,), offset + 1)
         return keys[offset].clone(), values[offset].clone()
 
@@ -168,9 +169,8 @@ class PagedKVStorage:
         return keys, values
 
     def _check_location(self, layer_index: int, block_id: int, offset: int) -> None:
-        if layer_index < 0 or layer_index >= self.num_layers:
-            raise IndexError("layer_index is out of range")
-        if block_id < 0 or block_id >= self.num_blocks:
-            raise IndexError("block_id is out of range")
-        if offset < 0 or offset >= self.block_size:
-            raise IndexError("offset is out of range")
+        for name, index, bound in (("layer_index", layer_index, self.num_layers),
+                                   ("block_id", block_id, self.num_blocks),
+                                   ("offset", offset, self.block_size)):
+            if not 0 <= index < bound:
+                raise IndexError(f"{name} is out of range")

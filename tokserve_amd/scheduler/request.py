@@ -1,11 +1,17 @@
 """Requests and their lifecycle (tokserve/scheduler/request.py).
 
-The lifecycle and its checks follow the reference: WAITING -> RUNNING ->
-FINISHED (or CANCELLED); a running request first completes its prefill, then
-appends one generated token per decode step until EOS or max_new_tokens.
-Generated tokens are kept as a host list (the batched executor reads every
-iteration's tokens back in one copy) and exposed as (1, n) tensors on the
-prompt's device.
+A request is a prompt, a generation config and a lifecycle: WAITING ->
+RUNNING -> FINISHED, or CANCELLED from either of the first two. The allowed
+source states of each transition are one table (`_SOURCES`); every state
+change goes through `_move`, which raises the reference's messages. While
+RUNNING, the request first completes its prefill, then takes one token per
+step until EOS or max_new_tokens: the stop rule is one function of the token
+just taken and the count.
+
+Tokens (prompt and generated) live in one growable int64 NumPy buffer on the
+host: the batched executor reads a whole iteration's tokens back in one copy
+and appends plain ints, and the (1, n) tensor views the reference API exposes
+are built from the buffer on the prompt's device when asked for.
 """
 
 from __future__ import annotations
@@ -19,7 +25,7 @@ from tokserve_amd.generation.types import GenerationConfig, GenerationResult, St
 
 __all__ = ["RequestState", "ScheduledRequest"]
 
-_INTEGER_DTYPES = (torch.int8, torch.int16, torch.int32, torch.int64, torch.uint8)
+_INTEGER_DTYPES = frozenset((torch.int8, torch.int16, torch.int32, torch.int64, torch.uint8))
 
 
 class RequestState(str, Enum):
@@ -32,63 +38,87 @@ class RequestState(str, Enum):
         return self.value
 
 
+_SOURCES = {
+    RequestState.RUNNING: (RequestState.WAITING,),
+    RequestState.FINISHED: (RequestState.RUNNING,),
+    RequestState.CANCELLED: (RequestState.WAITING, RequestState.RUNNING),
+}
+
+
+def _stop_reason(token: int, produced: int, config: GenerationConfig) -> StopReason | None:
+    """Why generation ends after taking `token` as the produced-th output, if it does."""
+
+    if config.eos_token_id is not None and token == config.eos_token_id:
+        return "eos"
+    if produced >= config.max_new_tokens:
+        return "max_new_tokens"
+    return None
+
+
 class ScheduledRequest:
     """One validated generation request managed by the scheduler."""
 
     def __init__(self, request_id: str, input_ids: torch.Tensor,
                  generation_config: GenerationConfig) -> None:
-        if not request_id:
-            raise ValueError("request_id must be nonempty")
-        if input_ids.ndim != 2 or input_ids.shape[0] != 1:
-            raise ValueError("input_ids must have shape (1, T)")
+        for bad, message in (
+            (not request_id, "request_id must be nonempty"),
+            (input_ids.ndim != 2 or input_ids.shape[0] != 1, "input_ids must have shape (1, T)"),
+        ):
+            if bad:
+                raise ValueError(message)
         if input_ids.shape[1] < 1:
             raise ValueError("input_ids must contain at least one token")
         if input_ids.dtype not in _INTEGER_DTYPES:
             raise TypeError("input_ids must contain integers")
         self.request_id = request_id
         self.generation_config = generation_config
-        self._input_ids = input_ids.clone()
-        self._prompt: tuple[int, ...] = tuple(int(t) for t in input_ids[0].tolist())
-        self._prompt_array = np.asarray(self._prompt, dtype=np.int64)
-        self._generated: list[int] = []
+        self._prompt_ids = input_ids.clone()
+        prompt = input_ids[0].cpu().numpy().astype(np.int64)
+        self._prompt_len = int(prompt.size)
+        self._buffer = np.empty(self._prompt_len + max(generation_config.max_new_tokens, 1),
+                                dtype=np.int64)
+        self._buffer[: self._prompt_len] = prompt
+        self._filled = self._prompt_len
         self._state = RequestState.WAITING
+        self._prefilled = False
+        self._stop: StopReason | None = None
         self._result: GenerationResult | None = None
-        self._prefill_complete = False
-        self._completion_reason: StopReason | None = None
         self._generator: torch.Generator | None = None
         if generation_config.do_sample and generation_config.seed is not None:
             self._generator = torch.Generator(device=input_ids.device)
             self._generator.manual_seed(generation_config.seed)
 
-    # ------------------------------------------------------------- properties
+    # ----------------------------------------------------------- reading
 
     @property
     def input_ids(self) -> torch.Tensor:
-        return self._input_ids.clone()
-
-    @property
-    def prompt_tokens(self) -> tuple[int, ...]:
-        return self._prompt
+        return self._prompt_ids.clone()
 
     @property
     def prompt_array(self) -> np.ndarray:
-        """The prompt as an int64 NumPy array (read-only use)."""
+        """The prompt as int64 (a read-only view into the token buffer)."""
 
-        return self._prompt_array
+        view = self._buffer[: self._prompt_len]
+        view.flags.writeable = False
+        return view
+
+    @property
+    def prompt_tokens(self) -> tuple[int, ...]:
+        return tuple(self._buffer[: self._prompt_len].tolist())
+
+    @property
+    def generated_tokens(self) -> tuple[int, ...]:
+        return tuple(self._buffer[self._prompt_len : self._filled].tolist())
+
+    @property
+    def generated_token_ids(self) -> torch.Tensor:
+        return self._ids(self._prompt_len, self._filled)
 
     @property
     def last_token(self) -> int:
         """The most recently generated token (the next decode input)."""
 
-        return self._generated[-1]
-
-    @property
-    def generated_tokens(self) -> tuple[int, ...]:
-        return tuple(self._generated)
-
-    @property
-    def generated_token_ids(self) -> torch.Tensor:
-        return self._as_ids(self._generated)
+        return int(self._buffer[self._filled - 1])
 
     @property
     def state(self) -> RequestState:
@@ -100,97 +130,109 @@ class ScheduledRequest:
 
     @property
     def prefill_complete(self) -> bool:
-        return self._prefill_complete
+        return self._prefilled
 
     @property
     def decode_ready(self) -> bool:
-        return (self._state is RequestState.RUNNING and self._prefill_complete
-                and bool(self._generated) and self._completion_reason is None)
+        return (self._state is RequestState.RUNNING and self._prefilled
+                and self._filled > self._prompt_len and self._stop is None)
 
     @property
     def next_input_token(self) -> torch.Tensor:
         if not self.decode_ready:
             raise RuntimeError("request is not decode-ready")
-        return self._as_ids(self._generated[-1:])
+        return self._ids(self._filled - 1, self._filled)
 
     @property
     def sequence_length(self) -> int:
-        return len(self._prompt) + len(self._generated)
+        return self._filled
 
     @property
     def num_generated_tokens(self) -> int:
-        return len(self._generated)
+        return self._filled - self._prompt_len
 
     @property
     def completion_reason(self) -> StopReason | None:
-        return self._completion_reason
+        return self._stop
 
     @property
     def sampling_generator(self) -> torch.Generator | None:
         return self._generator
 
-    # ------------------------------------------------------------ transitions
+    # ------------------------------------------------------- transitions
 
     def mark_running(self) -> None:
-        self._require_state(RequestState.WAITING)
-        self._state = RequestState.RUNNING
+        self._move(RequestState.RUNNING)
 
     def mark_prefill_complete(self) -> None:
-        self._require_state(RequestState.RUNNING)
-        if self._prefill_complete:
+        self._expect(RequestState.RUNNING)
+        if self._prefilled:
             raise RuntimeError("prefill is already complete")
-        self._prefill_complete = True
+        self._prefilled = True
         if self.generation_config.max_new_tokens == 0:
-            self._completion_reason = "max_new_tokens"
+            self._stop = "max_new_tokens"
 
     def append_generated_token(self, token: int | torch.Tensor) -> None:
-        """Record one generated token (an int, or a (1, 1) tensor of the prompt's dtype)."""
+        """Record one generated token: an int, or a (1, 1) tensor of the prompt's dtype
+        and device."""
 
-        self._require_state(RequestState.RUNNING)
+        self._expect(RequestState.RUNNING)
         if isinstance(token, torch.Tensor):
-            if token.shape != (1, 1):
-                raise ValueError("token_ids must have shape (1, 1)")
-            if token.dtype != self._input_ids.dtype:
-                raise TypeError("generated tokens must match the prompt dtype")
-            if token.device != self._input_ids.device:
-                raise ValueError("generated tokens must match the prompt device")
-            token = int(token.item())
-        if not self._prefill_complete:
+            token = self._token_from_tensor(token)
+        if not self._prefilled:
             raise RuntimeError("prefill must complete before generating tokens")
-        if self._completion_reason is not None:
+        if self._stop is not None:
             raise RuntimeError("request has already completed generation")
-        self._generated.append(int(token))
-        eos = self.generation_config.eos_token_id
-        if eos is not None and token == eos:
-            self._completion_reason = "eos"
-        elif len(self._generated) >= self.generation_config.max_new_tokens:
-            self._completion_reason = "max_new_tokens"
+        if self._filled == self._buffer.size:
+            self._buffer = np.concatenate((self._buffer, np.empty_like(self._buffer)))
+        self._buffer[self._filled] = token
+        self._filled += 1
+        self._stop = _stop_reason(int(token), self.num_generated_tokens, self.generation_config)
 
     def build_result(self) -> GenerationResult:
-        self._require_state(RequestState.RUNNING)
-        if self._completion_reason is None:
+        self._expect(RequestState.RUNNING)
+        if self._stop is None:
             raise RuntimeError("request has not reached a completion condition")
         generated = self.generated_token_ids
-        return GenerationResult(token_ids=torch.cat((self._input_ids, generated), dim=1),
-                                generated_token_ids=generated,
-                                stop_reason=self._completion_reason)
+        return GenerationResult(token_ids=self._ids(0, self._filled),
+                                generated_token_ids=generated, stop_reason=self._stop)
 
     def mark_finished(self, result: GenerationResult | None = None) -> None:
-        self._require_state(RequestState.RUNNING)
+        self._expect(RequestState.RUNNING)
         if result is not None:
-            self._generated = [int(t) for t in result.generated_token_ids[0].tolist()]
+            tokens = result.generated_token_ids[0].cpu().numpy().astype(np.int64)
+            self._buffer = np.concatenate((self._buffer[: self._prompt_len], tokens))
+            self._filled = int(self._buffer.size)
             self._result = result
-        self._state = RequestState.FINISHED
+        self._move(RequestState.FINISHED)
 
     def cancel(self) -> None:
-        if self._state not in (RequestState.WAITING, RequestState.RUNNING):
+        if self._state not in _SOURCES[RequestState.CANCELLED]:
             raise RuntimeError(f"cannot cancel request in state {self._state.value}")
-        self._state = RequestState.CANCELLED
+        self._move(RequestState.CANCELLED)
 
-    def _require_state(self, expected: RequestState) -> None:
-        if self._state is not expected:
-            raise RuntimeError(f"request must be {expected.value}, not {self._state.value}")
+    # ----------------------------------------------------------- helpers
 
-    def _as_ids(self, tokens: list[int]) -> torch.Tensor:
-        return torch.tensor([tokens], dtype=self._input_ids.dtype,
-                            device=self._input_ids.device).view(1, len(tokens))
+    def _move(self, target: RequestState) -> None:
+        sources = _SOURCES[target]
+        if self._state not in sources:
+            self._expect(sources[0])
+        self._state = target
+
+    def _expect(self, state: RequestState) -> None:
+        if self._state is not state:
+            raise RuntimeError(f"request must be {state.value}, not {self._state.value}")
+
+    def _token_from_tensor(self, token: torch.Tensor) -> int:
+        if token.shape != (1, 1):
+            raise ValueError("token_ids must have shape (1, 1)")
+        if token.dtype != self._prompt_ids.dtype:
+            raise TypeError("generated tokens must match the prompt dtype")
+        if token.device != self._prompt_ids.device:
+            raise ValueError("generated tokens must match the prompt device")
+        return int(token.item())
+
+    def _ids(self, begin: int, end: int) -> torch.Tensor:
+        values = torch.from_numpy(self._buffer[begin:end].copy())
+        return values.to(dtype=self._prompt_ids.dtype, device=self._prompt_ids.device).view(
+            1, end - begin)

@@ -1,16 +1,26 @@
 """Deterministic FIFO request scheduler (tokserve/scheduler/scheduler.py).
 
-Admission is first-in first-out under two limits: max_running_requests, and
-the paged pool's block count, against which every admitted request reserves
-ceil((prompt + max_new_tokens) / block_size) blocks until it completes
-(scheduler.py:58-89,136-159). The admission order, and with it every block id
-the engine allocates, is therefore a function of the submission order only.
+Admission is first-in first-out under two limits: free running slots
+(max_running_requests) and the paged pool's unreserved blocks, against which
+every admitted request reserves ceil((prompt + max_new_tokens) / block_size)
+blocks until it leaves (scheduler.py:75-104,146-168). Here one admission
+decision is a prefix computation over the head of the queue: the block needs
+of the first `free slots` waiting requests, their running sum, and the first
+position where that sum passes the unreserved blocks; everything before it is
+admitted in queue order, nothing after it (a blocked head request holds back
+the queue, as in the reference). Admission order, and with it every block id
+the engine allocates, is a function of the submission order only.
+
+The waiting queue is an insertion-ordered dict (FIFO order, O(1) cancellation
+by id); reservations are a dict plus their running total.
 """
 
 from __future__ import annotations
 
-from collections import deque
 from dataclasses import dataclass
+from itertools import islice
+
+import numpy as np
 
 from tokserve_amd.engine.paged.manager import PagedKVCacheManager
 from tokserve_amd.generation.types import GenerationResult
@@ -35,14 +45,17 @@ class RequestScheduler:
             raise ValueError("max_running_requests must be positive")
         self.max_running_requests = max_running_requests
         self.cache_manager = cache_manager
-        self._requests: dict[str, ScheduledRequest] = {}
-        self._waiting: deque[ScheduledRequest] = deque()
+        self._known: dict[str, ScheduledRequest] = {}
+        self._queue: dict[str, ScheduledRequest] = {}
         self._running: dict[str, ScheduledRequest] = {}
-        self._reserved: dict[str, int] = {}
+        self._holds: dict[str, int] = {}
+        self._held = 0
+
+    # ------------------------------------------------------------ views
 
     @property
     def waiting_requests(self) -> tuple[ScheduledRequest, ...]:
-        return tuple(self._waiting)
+        return tuple(self._queue.values())
 
     @property
     def running_requests(self) -> tuple[ScheduledRequest, ...]:
@@ -50,86 +63,81 @@ class RequestScheduler:
 
     @property
     def waiting_count(self) -> int:
-        return len(self._waiting)
+        return len(self._queue)
 
     @property
     def running_count(self) -> int:
         return len(self._running)
 
+    def get_request(self, request_id: str) -> ScheduledRequest:
+        request = self._known.get(request_id)
+        if request is None:
+            raise KeyError("unknown request_id")
+        return request
+
+    # ------------------------------------------------------- admission
+
     def submit(self, request: ScheduledRequest) -> None:
-        if request.request_id in self._requests:
+        if request.request_id in self._known:
             raise ValueError("request_id is already registered")
         if request.state is not RequestState.WAITING:
             raise ValueError("submitted request must be waiting")
-        self._requests[request.request_id] = request
-        self._waiting.append(request)
+        self._known[request.request_id] = request
+        self._queue[request.request_id] = request
 
     def schedule(self) -> ScheduleResult:
-        """Admit waiting requests in FIFO order while slots and blocks remain."""
+        """Admit the longest FIFO prefix of the queue that fits the free slots and blocks."""
 
         slots = self.max_running_requests - len(self._running)
-        blocks = self._unreserved_blocks()
-        admitted: list[ScheduledRequest] = []
-        while slots > 0 and self._waiting:
-            request = self._waiting[0]
-            needed = self._required_blocks(request)
-            if needed > blocks:
-                break
-            self._waiting.popleft()
+        head = list(islice(self._queue.values(), max(slots, 0)))
+        needs = np.fromiter((self._block_need(r) for r in head), dtype=np.int64, count=len(head))
+        fits = int(np.searchsorted(np.cumsum(needs), self._unheld_blocks(), side="right"))
+        admitted = head[:fits]
+        for request, need in zip(admitted, needs[:fits].tolist()):
+            del self._queue[request.request_id]
             request.mark_running()
             self._running[request.request_id] = request
-            if needed:
-                self._reserved[request.request_id] = needed
-                blocks -= needed
-            admitted.append(request)
-            slots -= 1
-        return ScheduleResult(tuple(admitted), len(self._waiting), len(self._running))
+            if need:
+                self._holds[request.request_id] = need
+                self._held += need
+        return ScheduleResult(tuple(admitted), len(self._queue), len(self._running))
+
+    def _block_need(self, request: ScheduledRequest) -> int:
+        new_tokens = request.generation_config.max_new_tokens
+        if self.cache_manager is None or new_tokens == 0:
+            return 0
+        size = self.cache_manager.storage.block_size
+        return -(-(request.sequence_length + new_tokens) // size)
+
+    def _unheld_blocks(self) -> int:
+        if self.cache_manager is None:
+            return 0
+        return max(0, self.cache_manager.allocator.num_blocks - self._held)
+
+    # ---------------------------------------------------------- leaving
 
     def complete(self, request_id: str, result: GenerationResult | None = None) -> None:
-        request = self._get_running(request_id)
-        self._release(request_id)
-        del self._running[request_id]
+        request = self._running.get(request_id)
+        if request is None:
+            raise RuntimeError("request is not running")
+        self._leave(request_id)
         request.mark_finished(result)
 
     def cancel(self, request_id: str) -> None:
         request = self.get_request(request_id)
         if request.state is RequestState.WAITING:
-            self._waiting = deque(r for r in self._waiting if r.request_id != request_id)
-            request.cancel()
-            return
-        if request.state is RequestState.RUNNING:
-            self._release(request_id)
-            del self._running[request_id]
-            request.cancel()
-            return
-        raise RuntimeError(f"cannot cancel request in state {request.state.value}")
+            del self._queue[request_id]
+        elif request.state is RequestState.RUNNING:
+            self._leave(request_id)
+        else:
+            raise RuntimeError(f"cannot cancel request in state {request.state.value}")
+        request.cancel()
 
-    def get_request(self, request_id: str) -> ScheduledRequest:
-        try:
-            return self._requests[request_id]
-        except KeyError as error:
-            raise KeyError("unknown request_id") from error
+    def _leave(self, request_id: str) -> None:
+        """A running request stops running: its hold and its cache go back to the pool."""
 
-    def _get_running(self, request_id: str) -> ScheduledRequest:
-        try:
-            return self._running[request_id]
-        except KeyError as error:
-            raise RuntimeError("request is not running") from error
-
-    def _required_blocks(self, request: ScheduledRequest) -> int:
-        if self.cache_manager is None or request.generation_config.max_new_tokens == 0:
-            return 0
-        total = len(request.prompt_tokens) + request.generation_config.max_new_tokens
-        size = self.cache_manager.storage.block_size
-        return (total + size - 1) // size
-
-    def _unreserved_blocks(self) -> int:
-        if self.cache_manager is None:
-            return 0
-        return max(0, self.cache_manager.allocator.num_blocks - sum(self._reserved.values()))
-
-    def _release(self, request_id: str) -> None:
-        self._reserved.pop(request_id, None)
+        self._held -= self._holds.pop(request_id, 0)
+        del self._running[request_id]
         manager = self.cache_manager
         if manager is not None and request_id in manager.active_sequence_ids:
             manager.release_sequence(request_id)
