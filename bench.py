@@ -104,6 +104,9 @@ def main() -> int:
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--no-secondary", action="store_true",
                         help="skip the mixed-step and packed norm/RoPE measurements")
+    parser.add_argument("--secondary", default="",
+                        help="comma-separated subset of the secondary measurements to run "
+                             "(default: all)")
     parser.add_argument("--no-e2e", action="store_true",
                         help="skip the end-to-end TinyLlama serving run")
     parser.add_argument("--copy-calibration", action="store_true",
@@ -136,9 +139,9 @@ def main() -> int:
             workspace=workspace, pages_per_split=args.pages_per_split, seq_order=order,
         )
 
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
+    # At least `--warmup` launches and at least 150 ms of back-to-back work: clocks
+    # leave their idle state only after ~50 ms of sustained load.
+    _settle(step, args.warmup)
     stream = torch.cuda.current_stream(device)
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
@@ -200,14 +203,24 @@ def main() -> int:
         },
     }
     if not args.no_secondary:
-        result["secondary"] = {
-            "mixed_step": measure_mixed(device, 20, 5),
-            "mixed_step_fp8_kv": measure_mixed(device, 20, 5, kv_dtype=torch.float8_e4m3fn),
-            "norm_rope": measure_norm_rope(device, 20, 5),
-            "small_fp32_step": measure_small_fp32_step(device, 50, 10),
-            "decode_fp8_kv": measure_decode_fp8(device, args.seed, 50, 10),
-            "decode_small_batches": measure_decode_small_batches(device, args.seed, 50, 10),
+        secondaries = {
+            "mixed_step": lambda: measure_mixed(device, 20, 5),
+            "mixed_step_fp8_kv": lambda: measure_mixed(device, 20, 5,
+                                                       kv_dtype=torch.float8_e4m3fn),
+            "norm_rope": lambda: measure_norm_rope(device, 20, 5),
+            "small_fp32_step": lambda: measure_small_fp32_step(device, 50, 10),
+            "decode_fp8_kv": lambda: measure_decode_fp8(device, args.seed, 50, 10),
+            "decode_small_batches": lambda: measure_decode_small_batches(device, args.seed, 50,
+                                                                         10),
+            "decode_serving_shape": lambda: measure_decode_serving_shape(device, args.seed, 50,
+                                                                         10),
         }
+        chosen = [n for n in args.secondary.split(",") if n] or list(secondaries)
+        unknown = set(chosen) - set(secondaries)
+        if unknown:
+            print(f"unknown secondary measurement(s): {sorted(unknown)}", file=sys.stderr)
+            return 2
+        result["secondary"] = {name: secondaries[name]() for name in chosen}
     if not args.no_e2e:
         e2e = measure_e2e(device, args.seed,
                           None if args.no_cpu_baseline else args.cpu_seconds)
@@ -299,6 +312,20 @@ def measure_mixed(device, steps: int, warmup: int, kv_dtype=None) -> dict:
     out_p = torch.empty_like(pre.query)
     out_d = torch.empty_like(dec.query)
     order = ops.longest_first(dec.contexts, device)
+    # The step's new K/V rows (every prefill token and every decode token, 8,432 rows),
+    # scattered through slot_mapping into their sequences' paged blocks before attention.
+    tables = torch.cat((pre.block_tables, dec.block_tables)).cpu()
+    positions = [p for ctx, ql in zip(pre.contexts + dec.contexts, pre.query_lens + dec.query_lens)
+                 for p in range(ctx - ql, ctx)]
+    rows = [b for b, ql in enumerate(pre.query_lens + dec.query_lens) for _ in range(ql)]
+    slots = torch.tensor([int(tables[b, p // 16]) * 16 + p % 16 for b, p in zip(rows, positions)],
+                         dtype=torch.int64, device=device)
+    rng = torch.Generator(device=device).manual_seed(3)
+    new_k = torch.randn((len(rows), 8, 128), generator=rng, device=device).to(torch.bfloat16)
+    new_v = torch.randn((len(rows), 8, 128), generator=rng, device=device).to(torch.bfloat16)
+
+    def append() -> None:
+        ops.kv_append(new_k, new_v, pre.key_cache, pre.value_cache, slots, 0, **scales)
 
     def prefill() -> None:
         ops.paged_attention_prefill(
@@ -312,9 +339,11 @@ def measure_mixed(device, steps: int, warmup: int, kv_dtype=None) -> dict:
             layer_index=0, max_seq_len=dec.max_seq_len, out=out_d, seq_order=order, **scales)
 
     def step() -> None:
+        append()
         prefill()
         decode()
 
+    ms_app = _time_ms(append, steps, warmup)
     ms_pre = _time_ms(prefill, steps, warmup)
     ms_dec = _time_ms(decode, steps, warmup)
     ms_step = _time_ms(step, steps, warmup)
@@ -326,11 +355,15 @@ def measure_mixed(device, steps: int, warmup: int, kv_dtype=None) -> dict:
         flops += 4 * hq * dh * visible
     dec_bytes = (sum(dec.contexts) * 8 * dh * 2 * dec.key_cache.element_size()
                  + 2 * dec.query.numel() * 2)
+    app_bytes = len(rows) * (2 * 8 * 128 * 2 + 2 * 8 * 128 * pre.key_cache.element_size() + 8)
     return {
         "workload": "mixed_llama3_8b: 16 x 512-token prefill chunks (prior U[0,2048]) + 240 "
                     "decodes (ctx U[256,4096]), Hq 32 / Hkv 8, Dh 128, block 16, bf16"
-                    + ("" if kv_dtype is None else "; fp8 e4m3 K/V pools"),
+                    + ("" if kv_dtype is None else "; fp8 e4m3 K/V pools")
+                    + "; step = KV append of the 8,432 new rows + prefill + decode attention",
         "ms_per_step": round(ms_step, 5),
+        "append_ms": round(ms_app, 5),
+        "append_gbps": round(app_bytes / (ms_app * 1e-3) / 1e9, 1),
         "prefill_ms": round(ms_pre, 5),
         "prefill_tflops": round(flops / (ms_pre * 1e-3) / 1e12, 2),
         "prefill_mfma_frac_of_2500_tflops": round(flops / (ms_pre * 1e-3) / 2.5e15, 4),
@@ -368,6 +401,41 @@ def measure_decode_fp8(device, seed: int, steps: int, warmup: int) -> dict:
         "algorithmic_bytes": nbytes,
         "gbps": round(nbytes / (ms * 1e-3) / 1e9, 1),
         "decode_tokens_per_s_one_layer": round(batch.num_seqs / (ms * 1e-3), 1),
+    }
+
+
+def measure_decode_serving_shape(device, seed: int, steps: int, warmup: int) -> dict:
+    """Decode attention at the end-to-end serving shape: 128 sequences of the TinyLlama
+    workload (prompts U[64, 1024] + 64 generated tokens), Hq 32 / Hkv 4, Dh 64, block 16,
+    bf16 (auto key splits, longest-first order)."""
+
+    import torch
+
+    from tokserve_amd import workloads
+    from tokserve_amd.kernels import ops
+
+    contexts = [len(spec.prompt) + 64 for spec in workloads.tinyllama_requests(seed=seed)]
+    batch = workloads.paged_batch(contexts, [1] * len(contexts), num_q_heads=32,
+                                  num_kv_heads=4, head_dim=64, block_size=16,
+                                  dtype=torch.bfloat16, device=device, seed=seed + 5,
+                                  pool_on_device_rng=True)
+    out = torch.empty_like(batch.query)
+    order = ops.longest_first(batch.contexts, device)
+
+    def step() -> None:
+        ops.paged_attention_decode(
+            batch.query, batch.key_cache, batch.value_cache, batch.block_tables,
+            batch.seq_lens, layer_index=0, max_seq_len=batch.max_seq_len, out=out,
+            seq_order=order)
+
+    ms = _time_ms(step, steps, warmup)
+    nbytes = algorithmic_bytes(batch)
+    return {
+        "workload": "decode at the e2e serving shape: 128 seqs, ctx = prompt U[64,1024] + 64, "
+                    "Hq 32 / Hkv 4, Dh 64, block 16, bf16",
+        "ms_per_step": round(ms, 5),
+        "algorithmic_bytes": nbytes,
+        "gbps": round(nbytes / (ms * 1e-3) / 1e9, 1),
     }
 
 
@@ -461,7 +529,15 @@ def measure_small_fp32_step(device, steps: int, warmup: int) -> dict:
 
 def measure_norm_rope(device, steps: int, warmup: int) -> dict:
     """RMSNorm (hidden 4096, fp32 weight -> fp32 out, the Triton wrapper's contract) and
-    RoPE (32 + 8 heads x 128, theta 5e5, in place) on a packed ragged bf16 stream."""
+    RoPE (32 + 8 heads x 128, theta 5e5, in place) on a packed ragged bf16 stream.
+
+    warm: the same buffers launch after launch (the ~212 / ~170 MB streams partly stay in
+    the 256 MB last-level cache). cold: launches rotate over 4 buffer sets (~850 / ~680 MB,
+    more than the cache), timed back to back, so every launch reads and writes HBM; also
+    the old per-launch flush measurement (a 512 MB read before each launch, each launch
+    bracketed by its own HIP events). Ceiling: torch's own elementwise kernels moving the
+    same bytes in the same directions (a bf16 -> fp32 conversion of the rows; copies of
+    Q and K), timed the same two ways."""
 
     import torch
 
@@ -470,40 +546,59 @@ def measure_norm_rope(device, steps: int, warmup: int) -> dict:
 
     data = workloads.norm_rope_packed(device, seed=0)
     n = data.hidden.shape[0]
-    out = torch.empty(data.hidden.shape, dtype=torch.float32, device=device)
+    sets = 4
+    hidden = [data.hidden] + [data.hidden.clone() for _ in range(sets - 1)]
+    outs = [torch.empty(data.hidden.shape, dtype=torch.float32, device=device)
+            for _ in range(sets)]
+    queries = [data.query] + [data.query.clone() for _ in range(sets - 1)]
+    keys = [data.key] + [data.key.clone() for _ in range(sets - 1)]
     table = ops.RotaryTable(128, theta=data.theta, max_position=4096 + 257,
                             dtype=torch.bfloat16, device=device)
-    q4 = data.query.permute(1, 0, 2).unsqueeze(0)
-    k4 = data.key.permute(1, 0, 2).unsqueeze(0)
 
-    def norm() -> None:
-        ops.rms_norm(data.hidden, data.weight, data.epsilon, out=out)
+    def norm(i: int):
+        return lambda: ops.rms_norm(hidden[i], data.weight, data.epsilon, out=outs[i])
 
-    def rope() -> None:
-        ops.rope(q4, k4, data.positions, table, query_out=q4, key_out=k4)
+    def rope(i: int):
+        q4 = queries[i].permute(1, 0, 2).unsqueeze(0)
+        k4 = keys[i].permute(1, 0, 2).unsqueeze(0)
+        return lambda: ops.rope(q4, k4, data.positions, table, query_out=q4, key_out=k4)
 
-    ms_norm = _time_ms(norm, steps, warmup)
-    ms_rope = _time_ms(rope, steps, warmup)
-    flush = _llc_flush_buffer(device)
-    ms_norm_cold = _time_ms_cold(norm, steps, flush)
-    ms_rope_cold = _time_ms_cold(rope, steps, flush)
-    del flush
+    def convert(i: int):
+        return lambda: outs[i].copy_(hidden[i])
+
+    def copy(i: int):
+        j = (i + 1) % sets
+        return lambda: (queries[i].copy_(queries[j]), keys[i].copy_(keys[j]))
+
+    def rotating(make):
+        fns = [make(i) for i in range(sets)]
+        return lambda: [fn() for fn in fns]
+
     norm_bytes = n * 4096 * (2 + 4) + 4096 * 4
     rope_bytes = n * (40 * 128 * 2 * 2 + 8)
-    return {
+    result = {
         "workload": f"norm_rope_packed: 64 seqs, {n} tokens (lengths U[1,256]), hidden 4096, "
                     "Q 32 x 128 / K 8 x 128, bf16",
-        "rmsnorm_ms": round(ms_norm, 5),
-        "rmsnorm_gbps": round(norm_bytes / (ms_norm * 1e-3) / 1e9, 1),
-        "rope_ms": round(ms_rope, 5),
-        "rope_gbps": round(rope_bytes / (ms_rope * 1e-3) / 1e9, 1),
-        "llc_flushed": {
-            "rmsnorm_ms": round(ms_norm_cold, 5),
-            "rmsnorm_gbps": round(norm_bytes / (ms_norm_cold * 1e-3) / 1e9, 1),
-            "rope_ms": round(ms_rope_cold, 5),
-            "rope_gbps": round(rope_bytes / (ms_rope_cold * 1e-3) / 1e9, 1),
-        },
     }
+    flush = _llc_flush_buffer(device)
+    for name, make, nbytes in (("rmsnorm", norm, norm_bytes), ("rope", rope, rope_bytes),
+                               ("torch_convert_same_bytes_as_rmsnorm", convert, norm_bytes),
+                               ("torch_copy_same_bytes_as_rope", copy, rope_bytes)):
+        warm = _time_ms(make(0), steps, warmup)
+        cold = _time_ms(rotating(make), steps, warmup) / sets
+        entry = {"warm_ms": round(warm, 5), "warm_gbps": round(nbytes / (warm * 1e-3) / 1e9, 1),
+                 "cold_ms": round(cold, 5), "cold_gbps": round(nbytes / (cold * 1e-3) / 1e9, 1)}
+        if not name.startswith("torch"):
+            flushed = _time_ms_cold(make(0), steps, flush)
+            entry["per_launch_flushed_ms"] = round(flushed, 5)
+            entry["per_launch_flushed_gbps"] = round(nbytes / (flushed * 1e-3) / 1e9, 1)
+        result[name] = entry
+    del flush
+    for name, ref in (("rmsnorm", "torch_convert_same_bytes_as_rmsnorm"),
+                      ("rope", "torch_copy_same_bytes_as_rope")):
+        result[name]["cold_frac_of_same_bytes_torch"] = round(
+            result[ref]["cold_ms"] / result[name]["cold_ms"], 3)
+    return result
 
 
 def _e2e_engine(model, specs, device, block_size: int = 16, kv_dtype=None):

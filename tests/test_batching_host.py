@@ -187,9 +187,9 @@ def test_failed_batch_leaves_manager_and_allocator_unchanged() -> None:
 
 
 def test_exhausted_pool_mid_batch_rolls_back_every_reservation() -> None:
-    """The third prefill finds the pool empty after the first two took their blocks, and a
-    decode had begun no append yet: every block goes back, new sequences are dropped, the
-    pending appends of existing ones are aborted."""
+    """Three prefills and a decode need more blocks than the pool holds: the iteration's
+    one allocation fails after the prefills opened their sequences; they are dropped and
+    the pool and the existing sequence are untouched."""
 
     model, manager = _model(), _manager(6, 2)
     executor = StubExecutor(model, manager)

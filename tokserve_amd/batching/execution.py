@@ -54,6 +54,7 @@ class _Checked:
     no_tokens: tuple[ScheduledRequest, ...]   # prefills with max_new_tokens == 0
     prefill: tuple[ScheduledRequest, ...]
     decode: tuple[ScheduledRequest, ...]
+    decode_caches: tuple                       # each decode request's sequence cache
     decode_lengths: tuple[int, ...]            # cached positions of each decode sequence
 
 
@@ -101,32 +102,36 @@ class BatchExecutor:
         for request in runs:
             if request.sequence_length > limit:
                 raise ValueError("sequence length exceeds max_position_embeddings")
-        lengths = []
+        caches, lengths = [], []
+        get = self.manager.get_sequence
         for request in decode:
-            cache = self.manager.get_sequence(request.request_id)
-            if cache.current_length < 1:
+            cache = get(request.request_id)
+            length = cache.current_length
+            if length < 1:
                 raise ValueError("paged decode requires a populated cache")
-            if cache.current_length >= cache.max_sequence_length:
+            if length >= cache.max_sequence_length:
                 raise ValueError("paged cache capacity exceeded")
-            lengths.append(cache.current_length)
+            caches.append(cache)
+            lengths.append(length)
         return _Checked(
             no_tokens=tuple(r for r in prefill if not r.generation_config.max_new_tokens),
-            prefill=runs, decode=tuple(decode), decode_lengths=tuple(lengths))
+            prefill=runs, decode=tuple(decode), decode_caches=tuple(caches),
+            decode_lengths=tuple(lengths))
 
     # ----------------------------------------------------------- phase 2
 
     def _reserve(self, reservation: StepReservation, checked: _Checked):
         limit = self.model.config.max_position_embeddings
-        pre_work = []
-        for request in checked.prefill:
-            cache = reservation.open(request.request_id, max_sequence_length=limit)
-            prompt = request.prompt_array
-            pre_work.append(SequenceWork(prompt, 0, reservation.extend(cache, prompt.size)))
-        dec_work = [
-            SequenceWork((request.last_token,), length,
-                         reservation.extend(self.manager.get_sequence(request.request_id), 1))
-            for request, length in zip(checked.decode, checked.decode_lengths)
-        ]
+        appends = [(reservation.open(request.request_id, max_sequence_length=limit),
+                    request.prompt_array.size) for request in checked.prefill]
+        appends.extend((cache, 1) for cache in checked.decode_caches)
+        tables = reservation.extend_all(appends)
+        n_pre = len(checked.prefill)
+        pre_work = [SequenceWork(request.prompt_array, 0, table)
+                    for request, table in zip(checked.prefill, tables)]
+        dec_work = [SequenceWork((request.last_token,), length, table)
+                    for request, length, table in zip(checked.decode, checked.decode_lengths,
+                                                      tables[n_pre:])]
         return pre_work, dec_work
 
     def _forward(self, prefill: list[SequenceWork], decode: list[SequenceWork],

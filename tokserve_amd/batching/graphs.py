@@ -81,9 +81,13 @@ class DecodeGraphs:
         layout, total = self._layout(b, w)
         out = np.zeros(total, dtype=np.uint8)
         starts = np.fromiter((wk.start for wk in works), dtype=np.int64, count=b)
+        # Every sequence's block ids in one flat array, scattered into the (B, W) table.
+        widths = np.fromiter((len(wk.block_ids) for wk in works), dtype=np.int64, count=b)
+        flat = np.concatenate([np.asarray(wk.block_ids) for wk in works])
+        rows = np.repeat(np.arange(b), widths)
+        cols = np.arange(flat.size) - np.repeat(np.cumsum(widths) - widths, widths)
         tables = np.zeros((b, w), dtype=np.int32)
-        for i, wk in enumerate(works):
-            tables[i, : len(wk.block_ids)] = wk.block_ids
+        tables[rows, cols] = flat
         lens = (starts + 1).astype(np.int32)
         values = {
             "token_ids": np.fromiter((wk.tokens[0] for wk in works), dtype=np.int64, count=b),

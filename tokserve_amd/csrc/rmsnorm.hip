@@ -7,14 +7,16 @@
 // and the Triton kernel (tokserve/kernels/_triton_rmsnorm.py:30-35): fp32
 // reduction, normalised value rounded to the input dtype, then one product
 // with the weight. One 256-thread workgroup per row; the row stays in
-// registers (16-byte loads, one HBM read and one write per element).
+// registers (one HBM read and one write per element; each thread's chunk is sized so
+// the wider of its load and its store is 16 bytes, keeping every wave access one
+// contiguous span).
 #include "common.hpp"
 
 namespace tks {
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int kMaxChunks = 4;  // 16-byte chunks per thread kept in registers
+constexpr int kMaxChunks = 8;  // chunks per thread kept in registers
 
 template <typename TI, typename TW, typename TO>
 struct NormArgs {
@@ -42,69 +44,92 @@ __device__ __forceinline__ float block_sum(float v, float *red) {
   return t;
 }
 
-// Loads VI elements of type T starting at p into floats (VI * sizeof(T) == 16 or VI == 1).
-template <typename T, int N>
-__device__ __forceinline__ void load_n(const T *p, float *f) {
-  if constexpr (N * sizeof(T) == 16) {
+// E elements of T at p (16-byte aligned groups) to and from floats, as one vector
+// access of E * sizeof(T) bytes (8, 16 or 32 bytes; other sizes element by element).
+template <typename T, int E>
+__device__ __forceinline__ void load_elems(const T *p, float *f) {
+  constexpr int kBytes = E * static_cast<int>(sizeof(T));
+  if constexpr (kBytes == 16) {
     unpack<T>(ld16(p), f);
-  } else if constexpr (N * sizeof(T) == 32) {
+  } else if constexpr (kBytes == 32) {
     unpack<T>(ld16(p), f);
     unpack<T>(ld16(p + 16 / sizeof(T)), f + 16 / sizeof(T));
+  } else if constexpr (kBytes == 8) {
+    const uint2 v = *reinterpret_cast<const uint2 *>(p);
+    float both[16 / sizeof(T)];
+    unpack<T>(make_uint4(v.x, v.y, 0u, 0u), both);
+#pragma unroll
+    for (int i = 0; i < E; ++i) f[i] = both[i];
   } else {
 #pragma unroll
-    for (int i = 0; i < N; ++i) f[i] = to_float(p[i]);
+    for (int i = 0; i < E; ++i) f[i] = to_float(p[i]);
   }
 }
-template <typename T, int N>
-__device__ __forceinline__ void store_n(T *p, const float *f) {
-  if constexpr (N * sizeof(T) == 16) {
+template <typename T, int E>
+__device__ __forceinline__ void store_elems(T *p, const float *f) {
+  constexpr int kBytes = E * static_cast<int>(sizeof(T));
+  if constexpr (kBytes == 16) {
     st16(p, pack<T>(f));
-  } else if constexpr (N * sizeof(T) == 32) {
+  } else if constexpr (kBytes == 32) {
     st16(p, pack<T>(f));
     st16(p + 16 / sizeof(T), pack<T>(f + 16 / sizeof(T)));
+  } else if constexpr (kBytes == 8) {
+    float both[16 / sizeof(T)] = {};
+#pragma unroll
+    for (int i = 0; i < E; ++i) both[i] = f[i];
+    const uint4 v = pack<T>(both);
+    *reinterpret_cast<uint2 *>(p) = make_uint2(v.x, v.y);
   } else {
 #pragma unroll
-    for (int i = 0; i < N; ++i) p[i] = from_float<T>(f[i]);
+    for (int i = 0; i < E; ++i) p[i] = from_float<T>(f[i]);
   }
 }
 
-// Vector path: hidden % (16 / sizeof(TI)) == 0 and hidden <= kThreads * kMaxChunks * V.
-template <typename TI, typename TW, typename TO, bool RESID>
+// Elements per thread chunk: as many as make the widest of the input and output
+// accesses 16 bytes, so every load and every store instruction of a wave covers one
+// contiguous span (fp32 output of a bf16 row: 8-byte loads, 16-byte stores).
+template <typename TI, typename TO>
+constexpr int chunk_elems() {
+  return 16 / static_cast<int>(sizeof(TI) > sizeof(TO) ? sizeof(TI) : sizeof(TO));
+}
+
+// Vector path: hidden % E == 0 and hidden <= kThreads * KC * E (KC chunks per thread).
+template <typename TI, typename TW, typename TO, bool RESID, int KC>
 __global__ __launch_bounds__(kThreads) void rms_norm_vec_kernel(NormArgs<TI, TW, TO> a) {
 #pragma clang fp contract(off)
-  constexpr int V = Vec<TI>::N;
+  constexpr int E = chunk_elems<TI, TO>();
   __shared__ float red[kThreads / 64];
   const int64_t row = blockIdx.x;
-  const int chunks = a.hidden / V;
-  float x[kMaxChunks][V];
+  const int chunks = a.hidden / E;
+  float x[KC][E];
   float ss = 0.f;
 #pragma unroll
-  for (int k = 0; k < kMaxChunks; ++k) {
+  for (int k = 0; k < KC; ++k) {
     const int c = threadIdx.x + k * kThreads;
     if (c < chunks) {
-      load_n<TI, V>(a.in + row * a.in_rs + c * V, x[k]);
+      load_elems<TI, E>(a.in + row * a.in_rs + c * E, x[k]);
       if constexpr (RESID) {
-        float r[V];
-        load_n<TI, V>(a.res + row * a.res_rs + c * V, r);
+        float r[E];
+        load_elems<TI, E>(a.res + row * a.res_rs + c * E, r);
 #pragma unroll
-        for (int j = 0; j < V; ++j) x[k][j] = round_through<TI>(x[k][j] + r[j]);
-        store_n<TI, V>(a.res_out + row * a.res_out_rs + c * V, x[k]);
+        for (int j = 0; j < E; ++j) x[k][j] = round_through<TI>(x[k][j] + r[j]);
+        store_elems<TI, E>(a.res_out + row * a.res_out_rs + c * E, x[k]);
       }
 #pragma unroll
-      for (int j = 0; j < V; ++j) ss += x[k][j] * x[k][j];
+      for (int j = 0; j < E; ++j) ss += x[k][j] * x[k][j];
     }
   }
   const float total = block_sum(ss, red);
   const float inv = 1.0f / sqrtf(total / static_cast<float>(a.hidden) + a.eps);
 #pragma unroll
-  for (int k = 0; k < kMaxChunks; ++k) {
+  for (int k = 0; k < KC; ++k) {
     const int c = threadIdx.x + k * kThreads;
     if (c < chunks) {
-      float w[V], y[V];
-      load_n<TW, V>(a.w + c * V, w);
+      float w[E], y[E];
+      load_elems<TW, E>(a.w + c * E, w);
 #pragma unroll
-      for (int j = 0; j < V; ++j) y[j] = w[j] * round_through<TI>(x[k][j] * inv);
-      store_n<TO, V>(a.out + row * a.out_rs + c * V, y);
+      for (int j = 0; j < E; ++j) y[j] = w[j] * round_through<TI>(x[k][j] * inv);
+      store_elems<TO, E>(a.out + row * a.out_rs + c * E, y);
     }
   }
 }
@@ -142,21 +167,27 @@ int32_t launch(const void *in, int64_t in_rs, const void *res, int64_t res_rs, v
                          res_rs, static_cast<TI *>(res_out), res_out_rs,
                          static_cast<const TW *>(w), static_cast<TO *>(out), out_rs, hidden,
                          eps};
-  constexpr int V = Vec<TI>::N;
-  // The weight and output are accessed V elements at a time too.
-  constexpr bool wo_vec_ok = (V * sizeof(TW)) % 16 == 0 && (V * sizeof(TO)) % 16 == 0;
+  constexpr int E = chunk_elems<TI, TO>();
   const bool resid = res != nullptr;
-  bool vec = wo_vec_ok && hidden % V == 0 && hidden <= kThreads * kMaxChunks * V &&
-             in_rs % V == 0 && out_rs % V == 0 && aligned16(in) && aligned16(w) &&
-             aligned16(out);
+  bool vec = hidden % E == 0 && hidden <= kThreads * kMaxChunks * E && in_rs % E == 0 &&
+             out_rs % E == 0 && aligned16(in) && aligned16(w) && aligned16(out);
   if (resid)
-    vec = vec && res_rs % V == 0 && res_out_rs % V == 0 && aligned16(res) && aligned16(res_out);
+    vec = vec && res_rs % E == 0 && res_out_rs % E == 0 && aligned16(res) && aligned16(res_out);
   const dim3 grid(static_cast<unsigned>(rows));
   if (vec) {
-    if (resid)
-      rms_norm_vec_kernel<TI, TW, TO, true><<<grid, kThreads, 0, s>>>(a);
-    else
-      rms_norm_vec_kernel<TI, TW, TO, false><<<grid, kThreads, 0, s>>>(a);
+    const int per_thread = static_cast<int>(ceil_div(hidden / E, kThreads));
+#define TKS_VEC(KC)                                                                        \
+  {                                                                                        \
+    if (resid)                                                                             \
+      rms_norm_vec_kernel<TI, TW, TO, true, KC><<<grid, kThreads, 0, s>>>(a);              \
+    else                                                                                   \
+      rms_norm_vec_kernel<TI, TW, TO, false, KC><<<grid, kThreads, 0, s>>>(a);             \
+  }
+    if (per_thread <= 1) TKS_VEC(1)
+    else if (per_thread <= 2) TKS_VEC(2)
+    else if (per_thread <= 4) TKS_VEC(4)
+    else TKS_VEC(8)
+#undef TKS_VEC
   } else {
     if (resid)
       rms_norm_any_kernel<TI, TW, TO, true><<<grid, kThreads, 0, s>>>(a);

@@ -104,20 +104,26 @@ __global__ __launch_bounds__(kThreads) void rope_kernel(RopeTensor q, RopeTensor
   const T *crow = cos_cache + pos * half;
   const T *srow = sin_cache + pos * half;
   const int items = (q.heads + k.heads) * chunks;
+  if (kThreads % chunks == 0) {
+    // Every item a thread visits has the same chunk: its table values are read once.
+    const int c = (threadIdx.x % chunks) * V;
+    float cf[V], sf[V];
+    load_table<T, V>(crow, srow, c, cf, sf);
+    for (int it = threadIdx.x; it < items; it += kThreads) {
+      const int h = it / chunks;
+      const RopeTensor &x = h < q.heads ? q : k;
+      const int hh = h < q.heads ? h : h - q.heads;
+      const T *src = static_cast<const T *>(x.in) + b * x.sb + hh * x.sh + t * x.st + c;
+      T *dst = static_cast<T *>(x.out) + b * x.osb + hh * x.osh + t * x.ost + c;
+      rotate<T, V>(src, dst, cf, sf, half);
+    }
+    return;
+  }
   for (int it = threadIdx.x; it < items; it += kThreads) {
     const int h = it / chunks;
     const int c = (it - h * chunks) * V;
     float cf[V], sf[V];
-    if constexpr (V * sizeof(T) == 16) {
-      unpack<T>(ld16(crow + c), cf);
-      unpack<T>(ld16(srow + c), sf);
-    } else {
-#pragma unroll
-      for (int j = 0; j < V; ++j) {
-        cf[j] = to_float(crow[c + j]);
-        sf[j] = to_float(srow[c + j]);
-      }
-    }
+    load_table<T, V>(crow, srow, c, cf, sf);
     const RopeTensor &x = h < q.heads ? q : k;
     const int hh = h < q.heads ? h : h - q.heads;
     const T *src = static_cast<const T *>(x.in) + b * x.sb + hh * x.sh + t * x.st + c;

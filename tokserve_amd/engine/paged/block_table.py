@@ -62,8 +62,16 @@ class SequenceBlockTable:
         new = np.asarray(physical_block_ids, dtype=np.int64).reshape(-1)
         if (new < 0).any():
             raise ValueError("physical_block_id must be nonnegative")
-        if np.unique(new).size != new.size or np.isin(new, self.view()).any():
+        held = set(self.view().tolist())
+        held_new = set(new.tolist())
+        if len(held_new) != new.size or not held.isdisjoint(held_new):
             raise ValueError("physical block is already in this block table")
+        self.extend_fresh(new)
+
+    def extend_fresh(self, new: np.ndarray) -> None:
+        """extend() for ids straight from the pool's allocator, which never hands out an id
+        that some table holds: no membership checks."""
+
         needed = self._used + new.size
         if needed > self._store.size:
             grown = np.empty(max(needed, 2 * self._store.size), dtype=np.int64)

@@ -21,6 +21,8 @@ from tokserve_amd.engine.paged.storage import PagedKVStorage
 
 __all__ = ["PagedKVCacheManager", "StepReservation"]
 
+_NONE = np.empty(0, dtype=np.int64)
+
 
 class PagedKVCacheManager:
     """Sequence caches over one allocator and one K/V storage pool."""
@@ -102,6 +104,26 @@ class StepReservation:
         blocks = cache.reserve(count)
         self._appending.append(cache)
         return blocks
+
+    def extend_all(self, appends: list[tuple[SequencePagedKVCache, int]]) -> list[np.ndarray]:
+        """Begin an append on every (cache, positions) pair, in order. Every check runs
+        first; then the blocks of all of them come from the pool in one lowest-first
+        allocation, dealt out in order, so each cache gets exactly the ids it would get
+        appending one after another. Returns each cache's live block ids."""
+
+        for cache, count in appends:
+            cache.check_append(count)
+        shorts = [cache.blocks_short(count) for cache, count in appends]
+        total = sum(shorts)
+        fresh = self.manager.allocator.take_lowest(total) if total else None
+        tables = []
+        offset = 0
+        for (cache, count), short in zip(appends, shorts):
+            cache.open_append(count, fresh[offset : offset + short] if short else _NONE)
+            offset += short
+            self._appending.append(cache)
+            tables.append(cache.block_table.view())
+        return tables
 
     def commit(self) -> None:
         for cache in self._appending:

@@ -26,6 +26,8 @@ from tokserve_amd.engine.paged.storage import PagedKVStorage
 
 __all__ = ["SequencePagedKVCache"]
 
+_NO_BLOCKS = np.empty(0, dtype=np.int64)
+
 
 @dataclass
 class _Append:
@@ -87,19 +89,35 @@ class SequencePagedKVCache:
     def begin_append(self, sequence_length: int) -> None:
         """Reserve physical slots for `sequence_length` new positions."""
 
+        self.check_append(sequence_length)
+        short = self.blocks_short(sequence_length)
+        self.open_append(sequence_length,
+                         self.allocator.take_lowest(short) if short > 0 else _NO_BLOCKS)
+
+    def check_append(self, sequence_length: int) -> None:
+        """Raise what begin_append would raise before taking any block."""
+
         self._active()
         if self._append is not None:
             raise RuntimeError("an append is already in progress")
         if sequence_length < 1:
             raise ValueError("sequence_length must be positive")
-        end = self._valid + sequence_length
-        if end > self.max_sequence_length:
+        if self._valid + sequence_length > self.max_sequence_length:
             raise ValueError("sequence exceeds max_sequence_length")
+
+    def blocks_short(self, sequence_length: int) -> int:
+        """Blocks an append of `sequence_length` positions takes from the pool."""
+
         table = self.block_table
-        kept = table.num_blocks
-        short = -(-end // table.block_size) - kept
-        if short > 0:
-            table.extend(self.allocator.take_lowest(short))
+        return max(0, -(-(self._valid + sequence_length) // table.block_size) - table.num_blocks)
+
+    def open_append(self, sequence_length: int, fresh_blocks: np.ndarray) -> None:
+        """Begin a checked append whose blocks_short() new blocks the caller took from
+        this pool's allocator (a batch takes all of its sequences' blocks at once)."""
+
+        kept = self.block_table.num_blocks
+        if fresh_blocks.size:
+            self.block_table.extend_fresh(fresh_blocks)
         self._append = _Append(start=self._valid, count=sequence_length, kept_blocks=kept)
 
     def reserve(self, sequence_length: int) -> np.ndarray:

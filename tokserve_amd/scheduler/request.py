@@ -8,10 +8,11 @@ RUNNING, the request first completes its prefill, then takes one token per
 step until EOS or max_new_tokens: the stop rule is one function of the token
 just taken and the count.
 
-Tokens (prompt and generated) live in one growable int64 NumPy buffer on the
-host: the batched executor reads a whole iteration's tokens back in one copy
-and appends plain ints, and the (1, n) tensor views the reference API exposes
-are built from the buffer on the prompt's device when asked for.
+The prompt is kept as a read-only int64 NumPy array (the packed metadata
+builder concatenates prompts without conversion) and the generated tokens as a
+host list of ints (the batched executor reads a whole iteration's tokens back
+in one copy and appends plain ints); the (1, n) tensors the reference API
+exposes are built on the prompt's device when asked for.
 """
 
 from __future__ import annotations
@@ -73,12 +74,9 @@ class ScheduledRequest:
         self.request_id = request_id
         self.generation_config = generation_config
         self._prompt_ids = input_ids.clone()
-        prompt = input_ids[0].cpu().numpy().astype(np.int64)
-        self._prompt_len = int(prompt.size)
-        self._buffer = np.empty(self._prompt_len + max(generation_config.max_new_tokens, 1),
-                                dtype=np.int64)
-        self._buffer[: self._prompt_len] = prompt
-        self._filled = self._prompt_len
+        self._prompt = input_ids[0].cpu().numpy().astype(np.int64)
+        self._prompt.flags.writeable = False
+        self._generated: list[int] = []
         self._state = RequestState.WAITING
         self._prefilled = False
         self._stop: StopReason | None = None
@@ -96,29 +94,27 @@ class ScheduledRequest:
 
     @property
     def prompt_array(self) -> np.ndarray:
-        """The prompt as int64 (a read-only view into the token buffer)."""
+        """The prompt as int64 (read-only)."""
 
-        view = self._buffer[: self._prompt_len]
-        view.flags.writeable = False
-        return view
+        return self._prompt
 
     @property
     def prompt_tokens(self) -> tuple[int, ...]:
-        return tuple(self._buffer[: self._prompt_len].tolist())
+        return tuple(self._prompt.tolist())
 
     @property
     def generated_tokens(self) -> tuple[int, ...]:
-        return tuple(self._buffer[self._prompt_len : self._filled].tolist())
+        return tuple(self._generated)
 
     @property
     def generated_token_ids(self) -> torch.Tensor:
-        return self._ids(self._prompt_len, self._filled)
+        return self._ids(self._generated)
 
     @property
     def last_token(self) -> int:
         """The most recently generated token (the next decode input)."""
 
-        return int(self._buffer[self._filled - 1])
+        return self._generated[-1]
 
     @property
     def state(self) -> RequestState:
@@ -135,21 +131,21 @@ class ScheduledRequest:
     @property
     def decode_ready(self) -> bool:
         return (self._state is RequestState.RUNNING and self._prefilled
-                and self._filled > self._prompt_len and self._stop is None)
+                and bool(self._generated) and self._stop is None)
 
     @property
     def next_input_token(self) -> torch.Tensor:
         if not self.decode_ready:
             raise RuntimeError("request is not decode-ready")
-        return self._ids(self._filled - 1, self._filled)
+        return self._ids(self._generated[-1:])
 
     @property
     def sequence_length(self) -> int:
-        return self._filled
+        return self._prompt.size + len(self._generated)
 
     @property
     def num_generated_tokens(self) -> int:
-        return self._filled - self._prompt_len
+        return len(self._generated)
 
     @property
     def completion_reason(self) -> StopReason | None:
@@ -183,26 +179,22 @@ class ScheduledRequest:
             raise RuntimeError("prefill must complete before generating tokens")
         if self._stop is not None:
             raise RuntimeError("request has already completed generation")
-        if self._filled == self._buffer.size:
-            self._buffer = np.concatenate((self._buffer, np.empty_like(self._buffer)))
-        self._buffer[self._filled] = token
-        self._filled += 1
-        self._stop = _stop_reason(int(token), self.num_generated_tokens, self.generation_config)
+        token = int(token)
+        self._generated.append(token)
+        self._stop = _stop_reason(token, len(self._generated), self.generation_config)
 
     def build_result(self) -> GenerationResult:
         self._expect(RequestState.RUNNING)
         if self._stop is None:
             raise RuntimeError("request has not reached a completion condition")
         generated = self.generated_token_ids
-        return GenerationResult(token_ids=self._ids(0, self._filled),
+        return GenerationResult(token_ids=torch.cat((self._prompt_ids, generated), dim=1),
                                 generated_token_ids=generated, stop_reason=self._stop)
 
     def mark_finished(self, result: GenerationResult | None = None) -> None:
         self._expect(RequestState.RUNNING)
         if result is not None:
-            tokens = result.generated_token_ids[0].cpu().numpy().astype(np.int64)
-            self._buffer = np.concatenate((self._buffer[: self._prompt_len], tokens))
-            self._filled = int(self._buffer.size)
+            self._generated = [int(t) for t in result.generated_token_ids[0].tolist()]
             self._result = result
         self._move(RequestState.FINISHED)
 
@@ -232,7 +224,6 @@ class ScheduledRequest:
             raise ValueError("generated tokens must match the prompt device")
         return int(token.item())
 
-    def _ids(self, begin: int, end: int) -> torch.Tensor:
-        values = torch.from_numpy(self._buffer[begin:end].copy())
-        return values.to(dtype=self._prompt_ids.dtype, device=self._prompt_ids.device).view(
-            1, end - begin)
+    def _ids(self, tokens: list[int]) -> torch.Tensor:
+        return torch.tensor([tokens], dtype=self._prompt_ids.dtype,
+                            device=self._prompt_ids.device).view(1, len(tokens))

@@ -89,7 +89,9 @@ class RequestScheduler:
         """Admit the longest FIFO prefix of the queue that fits the free slots and blocks."""
 
         slots = self.max_running_requests - len(self._running)
-        head = list(islice(self._queue.values(), max(slots, 0)))
+        if slots <= 0 or not self._queue:
+            return ScheduleResult((), len(self._queue), len(self._running))
+        head = list(islice(self._queue.values(), slots))
         needs = np.fromiter((self._block_need(r) for r in head), dtype=np.int64, count=len(head))
         fits = int(np.searchsorted(np.cumsum(needs), self._unheld_blocks(), side="right"))
         admitted = head[:fits]
