@@ -31,8 +31,12 @@ namespace tks {
 namespace {
 
 constexpr int kWaves = 4;
+// s_waitcnt immediate: vmcnt 0, expcnt and lgkmcnt left at their maxima (no wait).
+constexpr int kWaitVmcntZero = 0x0F70;
 // Register pages per wave: the page being consumed and the next one in flight
 // (3 or 4 measured no faster, for bf16 and for fp8 pages, and cost occupancy).
+// (3 or 4 pages measured no faster at Dh 64 either, also at batches of two waves
+// per SIMD: there the page loop is bound by its own instruction latency.)
 constexpr int kRing = 2;
 
 template <int DH, int G>
@@ -371,6 +375,12 @@ __global__ __launch_bounds__(64 * kWaves) void decode_mfma_kernel(DecodeArgs a) 
   for (int c0 = w_begin; c0 < w_end; c0 += 64) {
     const int n = min(w_end, c0 + 64) - c0;
     const int blk_reg = lane < n ? bt_row[c0 + lane] : 0;
+    // Wait for the block ids here, while no page load is in flight (the previous
+    // chunk's ring has drained). Without this the compiler, which cannot place this
+    // load in the page loop's count of outstanding loads, waits for every load in
+    // flight at each loop iteration before it reads a block id, and the register
+    // ring never holds more than the one page being consumed.
+    __builtin_amdgcn_s_waitcnt(kWaitVmcntZero);
     raw kb[D][NC], vb[D][4];
 #pragma unroll
     for (int j = 0; j < D - 1; ++j)
