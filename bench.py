@@ -207,6 +207,7 @@ def main() -> int:
             "mixed_step": lambda: measure_mixed(device, 20, 5),
             "mixed_step_fp8_kv": lambda: measure_mixed(device, 20, 5,
                                                        kv_dtype=torch.float8_e4m3fn),
+            "prefill_long": lambda: measure_prefill_long(device),
             "norm_rope": lambda: measure_norm_rope(device, 20, 5),
             "small_fp32_step": lambda: measure_small_fp32_step(device, 50, 10),
             "decode_fp8_kv": lambda: measure_decode_fp8(device, args.seed, 50, 10),
@@ -370,6 +371,92 @@ def measure_mixed(device, steps: int, warmup: int, kv_dtype=None) -> dict:
         "decode_ms": round(ms_dec, 5),
         "decode_gbps": round(dec_bytes / (ms_dec * 1e-3) / 1e9, 1),
     }
+
+
+def _clock_power() -> dict | None:
+    """The GPU's current shader clock (MHz, the starred level of pp_dpm_sclk) and socket
+    power and power cap (W, hwmon power1_input / power1_cap), read from sysfs at the
+    moment of the call; None where the files are absent."""
+
+    import glob
+    import re
+
+    for dev in sorted(glob.glob("/sys/class/drm/card*/device")):
+        try:
+            levels = Path(dev, "pp_dpm_sclk").read_text()
+        except OSError:
+            continue
+        current = re.search(r"(\d+)\s*[Mm]hz\s*\*", levels)
+        result = {"gfx_clock_mhz": int(current.group(1)) if current else None}
+        for name, key in (("power1_input", "socket_power_w"), ("power1_cap", "power_cap_w")):
+            for path in glob.glob(f"{dev}/hwmon/hwmon*/{name}"):
+                try:
+                    result[key] = round(int(Path(path).read_text()) / 1e6, 1)
+                except (OSError, ValueError):
+                    pass
+        return result
+    return None
+
+
+def measure_prefill_long(device, seconds: float = 1.0) -> dict:
+    """Long causal prefill (2 sequences x 8,192 tokens from position 0, Hq 32 / Hkv 8,
+    Dh 128, block 16, bf16) over `seconds` of back-to-back launches, with the GPU's
+    clocks and socket power sampled half way through: the MFMA rate the kernel reaches
+    once the clocks have settled under its sustained load, and the clock that rate is
+    reached at."""
+
+    import threading
+
+    import torch
+
+    from tokserve_amd import workloads
+    from tokserve_amd.kernels import ops
+
+    contexts, qlens = [8192, 8192], [8192, 8192]
+    pb = workloads.paged_batch(contexts, qlens, num_q_heads=32, num_kv_heads=8, head_dim=128,
+                               block_size=16, dtype=torch.bfloat16, device=device, seed=1,
+                               pool_on_device_rng=True)
+    out = torch.empty_like(pb.query)
+
+    def prefill() -> None:
+        ops.paged_attention_prefill(
+            pb.query, pb.key_cache, pb.value_cache, pb.block_tables, pb.seq_lens,
+            pb.cu_seqlens_q, layer_index=0, max_query_len=8192, max_seq_len=8192, out=out)
+
+    _settle(prefill, 5)
+    sample: dict = {}
+    probe = threading.Timer(seconds / 2, lambda: sample.update(_clock_power() or {}))
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    launches = 0
+    begin = time.perf_counter()
+    probe.start()
+    start.record()
+    while time.perf_counter() - begin < seconds:
+        for _ in range(10):
+            prefill()
+        launches += 10
+        torch.cuda.synchronize()
+    end.record()
+    torch.cuda.synchronize()
+    probe.join()
+    ms = start.elapsed_time(end) / launches
+    flops = sum(4 * 32 * 128 * (ql * (c - ql) + ql * (ql + 1) // 2) for c, ql in zip(contexts, qlens))
+    tflops = flops / (ms * 1e-3) / 1e12
+    result = {
+        "workload": "2 x 8,192-token causal prefill from position 0, Hq 32 / Hkv 8, Dh 128, "
+                    "block 16, bf16",
+        "launches": launches,
+        "ms": round(ms, 5),
+        "tflops": round(tflops, 1),
+        "mfma_frac_of_2500_tflops": round(tflops / 2500.0, 4),
+    }
+    if sample.get("gfx_clock_mhz"):
+        # The 2.5 PFLOP/s dense bf16 peak assumes the 2,400 MHz maximum clock.
+        result["mfma_frac_of_peak_at_sampled_clock"] = round(
+            tflops / (2500.0 * sample["gfx_clock_mhz"] / 2400.0), 4)
+    result.update(sample)
+    return result
 
 
 def measure_decode_fp8(device, seed: int, steps: int, warmup: int) -> dict:
