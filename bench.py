@@ -707,7 +707,7 @@ def measure_norm_rope(device, steps: int, warmup: int) -> dict:
     return result
 
 
-def _e2e_engine(model, specs, device, block_size: int = 16, kv_dtype=None):
+def _e2e_engine(model, specs, device, block_size: int = 16, kv_dtype=None, overlap=True):
     import torch
 
     from tokserve_amd import workloads
@@ -728,7 +728,7 @@ def _e2e_engine(model, specs, device, block_size: int = 16, kv_dtype=None):
         prompt = torch.tensor([spec.prompt], dtype=torch.int64, device=device)
         scheduler.submit(ScheduledRequest(spec.request_id, prompt,
                                           GenerationConfig(max_new_tokens=spec.max_new_tokens)))
-    return ContinuousBatchEngine(model, scheduler, manager)
+    return ContinuousBatchEngine(model, scheduler, manager, overlap_decode=overlap)
 
 
 def measure_e2e(device, seed: int, cpu_seconds: float | None, kv_dtype=None,
@@ -760,14 +760,21 @@ def measure_e2e(device, seed: int, cpu_seconds: float | None, kv_dtype=None,
     warm = workloads.tinyllama_requests(seed=seed + 1, max_new_tokens=2)
     _e2e_engine(model, warm, device, kv_dtype=kv_dtype).run_until_idle()
     torch.cuda.synchronize()
-    engine = _e2e_engine(model, specs, device, kv_dtype=kv_dtype)
-    step_s = []
-    start = time.perf_counter()
-    while engine.scheduler.waiting_count or engine.scheduler.running_count:
-        t0 = time.perf_counter()
-        engine.step()
-        step_s.append(time.perf_counter() - t0)
-    wall = time.perf_counter() - start
+
+    def serve(overlap: bool):
+        engine = _e2e_engine(model, specs, device, kv_dtype=kv_dtype, overlap=overlap)
+        step_s = []
+        start = time.perf_counter()
+        while engine.scheduler.waiting_count or engine.scheduler.running_count:
+            t0 = time.perf_counter()
+            engine.step()
+            step_s.append(time.perf_counter() - t0)
+        return engine, step_s, time.perf_counter() - start
+
+    # Decode iteration i+1 queued before iteration i's tokens are read back (the
+    # engine's overlap_decode), then the same run one iteration at a time.
+    engine, step_s, wall = serve(True)
+    _, _, wall_sequential = serve(False)
     generated = sum(r.num_generated_tokens for r in engine.results)
     decode_steps = step_s[1:]
     # Device time of one replay of the largest captured decode graph (the engine has
@@ -782,13 +789,15 @@ def measure_e2e(device, seed: int, cpu_seconds: float | None, kv_dtype=None,
     result = {
         "workload": "e2e_tinyllama: TinyLlama-1.1B shape (22 layers, hidden 2048, 32/4 heads, "
                     "Dh 64, MLP 5632, vocab 32000), random init, " + dtype_name + "; 128 requests, prompts "
-                    "U[64,1024], 128 greedy tokens, block 16, max_running 128" + pools,
+                    "U[64,1024], 128 greedy tokens, block 16, max_running 128" + pools
+                    + "; decode iteration i+1 queued before iteration i is read back",
         "requests": len(specs),
         "prompt_tokens": sum(len(s.prompt) for s in specs),
         "generated_tokens": generated,
         "iterations": len(step_s),
         "wall_s": round(wall, 4),
         "tokens_per_s": round(generated / wall, 1),
+        "tokens_per_s_one_iteration_at_a_time": round(generated / wall_sequential, 1),
         "prefill_step_s": round(step_s[0], 4),
         "decode_step_ms_mean": round(1e3 * sum(decode_steps) / max(len(decode_steps), 1), 3),
         "decode_step_ms_median": round(1e3 * sorted(decode_steps)[len(decode_steps) // 2], 3)

@@ -78,11 +78,11 @@ def test_full_recompute_and_paged_generation_agree(device) -> None:
 
 
 def _run_both(model, device, specs, *, max_running, num_blocks, block_size, kv_dtype=None,
-              scales=(1.0, 1.0)):
+              scales=(1.0, 1.0), overlap=False):
     manager = _manager(model, device, num_blocks=num_blocks, block_size=block_size,
                        dtype=model.embed_tokens.weight.dtype, kv_dtype=kv_dtype, scales=scales)
     scheduler = RequestScheduler(max_running_requests=max_running, cache_manager=manager)
-    engine = ContinuousBatchEngine(model, scheduler, manager)
+    engine = ContinuousBatchEngine(model, scheduler, manager, overlap_decode=overlap)
     released = {}
     original = manager.release_sequence
 
@@ -122,8 +122,9 @@ def test_engine_ragged_known_answers_on_gpu(device) -> None:
     assert manager.allocator.allocated_count == 0
 
 
+@pytest.mark.parametrize("overlap", [False, True])
 @pytest.mark.parametrize("seed", [0, 1])
-def test_engine_random_workload_tokens_and_records_identical(device, seed) -> None:
+def test_engine_random_workload_tokens_and_records_identical(device, seed, overlap) -> None:
     g = torch.Generator().manual_seed(100 + seed)
     specs = []
     for i in range(16):
@@ -132,7 +133,7 @@ def test_engine_random_workload_tokens_and_records_identical(device, seed) -> No
         specs.append((f"q{i}", prompt, int(torch.randint(0, 9, (1,), generator=g))))
     model = _fixture_model(device)
     engine, _, _, released, reference, expected = _run_both(
-        model, device, specs, max_running=5, num_blocks=14, block_size=4)
+        model, device, specs, max_running=5, num_blocks=14, block_size=4, overlap=overlap)
     assert [tuple(r.__dict__.values()) for r in engine.history] == \
         [tuple(r.__dict__.values()) for r in expected]
     for rid, prompt, n in specs:
@@ -339,8 +340,9 @@ def test_engine_fp8_kv_pools_fp32_tokens_identical(device, scales) -> None:
     ((("A", [1, 2], 3), ("B", [3], 1), ("C", [4], 1)), 3, 3),
     ((("A", [1, 2], 4), ("B", [3], 2), ("C", [4, 5, 6], 2), ("D", [7], 1)), 2, 16),
 ])
+@pytest.mark.parametrize("overlap", [False, True])
 def test_engine_reference_scenarios_tokens_identical(device, specs, max_running,
-                                                     num_blocks) -> None:
+                                                     num_blocks, overlap) -> None:
     """The request mixes of tests/integration/test_continuous_batch_engine.py:117-166 and
     test_continuous_batch_pressure.py:60-244 (block size 2; the pools of 3 blocks make later
     requests wait for capacity) run through the GPU engine with the fixture model: every
@@ -350,7 +352,7 @@ def test_engine_reference_scenarios_tokens_identical(device, specs, max_running,
     model = _fixture_model(device)
     engine, scheduler, manager, released, reference, expected = _run_both(
         model, device, list(specs), max_running=max_running, num_blocks=num_blocks,
-        block_size=2)
+        block_size=2, overlap=overlap)
     assert [tuple(r.__dict__.values()) for r in engine.history] == \
         [tuple(r.__dict__.values()) for r in expected]
     for rid, prompt, n in specs:
@@ -362,3 +364,127 @@ def test_engine_reference_scenarios_tokens_identical(device, specs, max_running,
         assert result.token_ids.tolist() == alone.token_ids.tolist(), rid
     assert manager.active_sequence_ids == ()
     assert manager.allocator.free_count == num_blocks
+
+
+class _Hooks:
+    """Records the metrics hooks in call order."""
+
+    def __init__(self) -> None:
+        self.events: list[tuple] = []
+
+    def request_admitted(self, request_id):
+        self.events.append(("admitted", request_id))
+
+    def prefill_started(self, request_id):
+        self.events.append(("prefill_started", request_id))
+
+    def prefill_finished(self, request_id):
+        self.events.append(("prefill_finished", request_id))
+
+    def token_produced(self, request_id):
+        self.events.append(("token", request_id))
+
+    def complete_request(self, request_id, completion_reason):
+        self.events.append(("complete", request_id, completion_reason))
+
+    def record_iteration(self, *, prefill_requests, decode_requests):
+        self.events.append(("iteration", prefill_requests, decode_requests))
+
+
+def _engine(model, device, *, max_running, num_blocks, block_size, overlap):
+    manager = _manager(model, device, num_blocks=num_blocks, block_size=block_size)
+    scheduler = RequestScheduler(max_running_requests=max_running, cache_manager=manager)
+    hooks = _Hooks()
+    engine = ContinuousBatchEngine(model, scheduler, manager, metrics=hooks,
+                                   overlap_decode=overlap)
+    released = {}
+    original = manager.release_sequence
+
+    def record(sequence_id):
+        released[sequence_id] = manager.get_sequence(sequence_id).block_ids
+        original(sequence_id)
+
+    manager.release_sequence = record
+    return engine, hooks, released
+
+
+def _submit(engine, device, rid, prompt, n):
+    engine.scheduler.submit(ScheduledRequest(rid, torch.tensor([prompt], device=device),
+                                             GenerationConfig(max_new_tokens=n)))
+
+
+def _outcome(engine, hooks, released, ids):
+    requests = {rid: engine.scheduler.get_request(rid) for rid in ids}
+    tokens = {rid: (r.state.value, None if r.result is None
+                    else r.result.generated_token_ids[0].tolist()) for rid, r in requests.items()}
+    return ([tuple(r.__dict__.values()) for r in engine.history], tokens, hooks.events,
+            released, engine.cache_manager.allocator.free_count)
+
+
+@pytest.mark.parametrize("max_running", [8, 3])
+def test_overlapped_decode_equals_sequential_and_oracle(device, max_running) -> None:
+    """Six requests with staggered max_new_tokens: with overlap_decode the engine queues
+    iteration i+1 before reading iteration i back wherever the next plan is known (all
+    admitted, none finishing), and falls back where it is not. Records, tokens, the hook
+    sequence, released block ids and the final pool equal the sequential engine's, and
+    records and tokens equal the oracle engine's."""
+
+    model = _fixture_model(device)
+    specs = [("a", [1, 2, 3], 5), ("b", [4, 5, 6, 7, 8], 12), ("c", [9], 9),
+             ("d", [10, 11, 12, 13, 14, 15, 16], 16), ("e", [17, 18], 12), ("f", [19] * 6, 3)]
+    outcomes = []
+    queued = []
+    for overlap in (False, True):
+        engine, hooks, released = _engine(model, device, max_running=max_running,
+                                          num_blocks=40, block_size=4, overlap=overlap)
+        launches = []
+        launch = engine.executor.launch_decode
+
+        def counted(decode, *, token_source=None, launch=launch, launches=launches):
+            launches.append(token_source is not None)
+            return launch(decode, token_source=token_source)
+
+        engine.executor.launch_decode = counted
+        for spec in specs:
+            _submit(engine, device, *spec)
+        engine.run_until_idle()
+        outcomes.append(_outcome(engine, hooks, released, [spec[0] for spec in specs]))
+        queued.append(sum(launches))
+    assert outcomes[0] == outcomes[1]
+    assert queued[0] == 0 and queued[1] > 0
+    state = {k: v.detach().cpu() for k, v in model.state_dict().items()}
+    config = {k: getattr(model.config, k) for k in FIXTURE["config"]}
+    reference = oracle_engine.Engine(state, config, num_blocks=40, block_size=4,
+                                     max_running=max_running)
+    for rid, prompt, n in specs:
+        reference.submit(oracle_engine.Request(rid, list(prompt), n))
+    expected = reference.run()
+    assert outcomes[1][0] == [tuple(r.__dict__.values()) for r in expected]
+    for rid, _, _ in specs:
+        assert outcomes[1][1][rid] == ("finished", reference.finished[rid].generated), rid
+
+
+def test_overlapped_decode_discards_a_queued_iteration_when_the_scheduler_changes(device) -> None:
+    """A submission and a cancellation between steps, each while an iteration is queued:
+    the queued iteration is discarded (its positions and blocks return) and the step runs
+    as the sequential engine's does."""
+
+    model = _fixture_model(device)
+    outcomes = []
+    for overlap in (False, True):
+        engine, hooks, released = _engine(model, device, max_running=4, num_blocks=24,
+                                          block_size=4, overlap=overlap)
+        for spec in (("a", [1, 2, 3], 10), ("b", [4, 5], 10), ("c", [6, 7, 8, 9], 10)):
+            _submit(engine, device, *spec)
+        for _ in range(3):
+            engine.step()
+        assert (engine._queued is not None) == overlap
+        _submit(engine, device, "d", [10, 11], 4)       # waits, then is admitted
+        for _ in range(2):
+            engine.step()
+        assert (engine._queued is not None) == overlap
+        engine.scheduler.cancel("b")                    # a queued sequence goes away
+        engine.run_until_idle()
+        outcomes.append(_outcome(engine, hooks, released, "abcd"))
+        assert engine.cache_manager.allocator.free_count == 24
+    assert outcomes[0] == outcomes[1]

@@ -8,13 +8,28 @@ step's IterationRecord (admitted, prefill, decode, completed and still-active
 ids) and the metrics hooks are the reference's: request_admitted per admitted
 request, the executor's prefill/token hooks, complete_request per completed
 request and record_iteration per step (engine.py:65-131).
+
+With overlap_decode=True, decode-only iterations of greedy requests run as a
+launch and a finish (BatchExecutor.launch_decode / finish), and when the
+next iteration is already known at launch time, it is queued on the GPU
+before this one's tokens are read back: the next plan is this plan again
+when nothing waits for admission, every running request decodes, none has
+an EOS token and none reaches max_new_tokens in this iteration. Its token
+ids come straight from this iteration's device tokens, so the host's
+bookkeeping of iteration i (token readback, hooks, retirement, record) runs
+while the GPU computes iteration i+1. Records, hooks, tokens and block ids
+are those of the sequential engine; what differs is only visible between
+two step() calls: the queued iteration's positions are reserved (an open
+append per sequence, and any new block it needed). A step that finds the
+scheduler changed since (a submission, a cancellation) discards the queued
+iteration, returning those positions and blocks, and runs sequentially.
 """
 
 from __future__ import annotations
 
 from dataclasses import dataclass
 
-from tokserve_amd.batching.execution import BatchExecutor
+from tokserve_amd.batching.execution import BatchExecutor, LaunchedDecode
 from tokserve_amd.batching.plan import IterationPlan, build_iteration_plan
 from tokserve_amd.engine.model import LlamaModel
 from tokserve_amd.engine.paged.manager import PagedKVCacheManager
@@ -48,16 +63,19 @@ class ContinuousBatchEngine:
     """Advances dynamically changing requests one iteration at a time."""
 
     def __init__(self, model: LlamaModel, scheduler: RequestScheduler,
-                 cache_manager: PagedKVCacheManager, *, metrics=None) -> None:
+                 cache_manager: PagedKVCacheManager, *, metrics=None,
+                 overlap_decode: bool = False) -> None:
         if scheduler.cache_manager is not cache_manager:
             raise ValueError("scheduler and engine must share the cache manager")
         self.model = model
         self.scheduler = scheduler
         self.cache_manager = cache_manager
         self.metrics = metrics
+        self.overlap_decode = overlap_decode
         self.executor = BatchExecutor(model, cache_manager)
         self._history: list[IterationRecord] = []
         self._results: list[GenerationResult] = []
+        self._queued: LaunchedDecode | None = None
 
     @property
     def history(self) -> tuple[IterationRecord, ...]:
@@ -70,9 +88,52 @@ class ContinuousBatchEngine:
     def step(self) -> IterationRecord:
         admitted = self._admit()
         plan = build_iteration_plan(self.scheduler.running_requests)
-        self.executor.execute(plan.prefill_requests, plan.decode_requests, metrics=self.metrics)
-        retired = self._retire()
+        launched = self._take_queued(admitted, plan)
+        if launched is None and self.overlap_decode and not plan.prefill_requests \
+                and self.executor.can_launch(plan.decode_requests):
+            launched = self.executor.launch_decode(plan.decode_requests)
+        if launched is None:
+            completed = self.executor.execute(plan.prefill_requests, plan.decode_requests,
+                                              metrics=self.metrics)
+        else:
+            self.executor.commit(launched)
+            if self._next_plan_is(plan):
+                try:
+                    self._queued = self.executor.launch_decode(plan.decode_requests,
+                                                               token_source=launched.tokens)
+                except Exception:  # the next step runs it again and raises there
+                    self._queued = None
+            completed = self.executor.finish(launched, metrics=self.metrics)
+        retired = self._retire(completed)
         return self._record(admitted, plan, retired)
+
+    def _take_queued(self, admitted, plan: IterationPlan) -> LaunchedDecode | None:
+        """The iteration queued by the previous step, if it is still this step's plan."""
+
+        queued, self._queued = self._queued, None
+        if queued is None:
+            return None
+        same = (not admitted and not plan.prefill_requests
+                and len(queued.requests) == len(plan.decode_requests)
+                and all(a is b for a, b in zip(queued.requests, plan.decode_requests)))
+        if same:
+            return queued
+        self.executor.discard(queued)
+        return None
+
+    def _next_plan_is(self, plan: IterationPlan) -> bool:
+        """Whether the iteration after this one is this plan again (see the module
+        docstring), so that it can be queued now."""
+
+        decode = plan.decode_requests
+        if self.scheduler.waiting_count or len(decode) != self.scheduler.running_count:
+            return False
+        for request in decode:
+            config = request.generation_config
+            if config.eos_token_id is not None or \
+                    request.num_generated_tokens + 1 >= config.max_new_tokens:
+                return False
+        return True
 
     def _admit(self) -> tuple[ScheduledRequest, ...]:
         admitted = self.scheduler.schedule().admitted_requests
@@ -81,8 +142,13 @@ class ContinuousBatchEngine:
                 self.metrics.request_admitted(request.request_id)
         return admitted
 
-    def _retire(self) -> list[ScheduledRequest]:
-        finished = [r for r in self.scheduler.running_requests if r.completion_reason is not None]
+    def _retire(self, completed: tuple[str, ...]) -> list[ScheduledRequest]:
+        """Complete, in running order, the requests the iteration finished."""
+
+        if not completed:
+            return []
+        done = set(completed)
+        finished = [r for r in self.scheduler.running_requests if r.request_id in done]
         for request in finished:
             result = request.build_result()
             self.scheduler.complete(request.request_id, result)

@@ -26,6 +26,15 @@ An iteration runs in three phases:
              forward that served the whole iteration.)
 Requests with max_new_tokens == 0 complete at prefill without a forward or
 hooks, as in the reference.
+
+A decode-only iteration of greedy requests can also run split in two
+(launch_decode, then finish): launch checks, reserves and queues the graph
+replay with an asynchronous copy of the greedy tokens to pinned host memory,
+and keeps the reservation open; commit makes the reserved positions valid;
+finish waits for the copy and applies phase 3. Between launch and finish the
+host is free, and a launch may take its token ids from the previous launch's
+device tokens, so the engine can queue iteration i+1 before it reads back
+iteration i.
 """
 
 from __future__ import annotations
@@ -44,7 +53,7 @@ from tokserve_amd.generation.sampling import select_next_token
 from tokserve_amd.kernels import ops
 from tokserve_amd.scheduler.request import RequestState, ScheduledRequest
 
-__all__ = ["BatchExecutor", "execute_prefill", "execute_decode"]
+__all__ = ["BatchExecutor", "LaunchedDecode", "execute_prefill", "execute_decode"]
 
 
 @dataclass(frozen=True)
@@ -58,6 +67,21 @@ class _Checked:
     decode_lengths: tuple[int, ...]            # cached positions of each decode sequence
 
 
+@dataclass
+class LaunchedDecode:
+    """A decode-only iteration queued on the GPU whose tokens are not read yet."""
+
+    checked: _Checked
+    reservation: StepReservation
+    tokens: torch.Tensor         # (B,) int64 greedy tokens, on the device
+    host: torch.Tensor           # pinned (>= B,) int64: their copy, valid once `ready` is
+    ready: torch.cuda.Event
+
+    @property
+    def requests(self) -> tuple[ScheduledRequest, ...]:
+        return self.checked.decode
+
+
 class BatchExecutor:
     """Runs planned prefill and decode requests of one iteration as one packed forward."""
 
@@ -69,6 +93,8 @@ class BatchExecutor:
         self.builder = PackedBatchBuilder(manager.storage.device, manager.storage.block_size)
         graphs = DecodeGraphs(model, manager.storage)
         self.graphs = graphs if use_graphs and graphs.supported() else None
+        self._token_host: list[torch.Tensor | None] = [None, None]
+        self._token_turn = 0
 
     def execute(self, prefill: Sequence[ScheduledRequest], decode: Sequence[ScheduledRequest],
                 *, metrics=None) -> tuple[str, ...]:
@@ -82,6 +108,58 @@ class BatchExecutor:
                 tokens = self._forward(pre_work, dec_work, [*checked.prefill, *checked.decode])
                 reservation.commit()
         return self._apply(prefill, checked, tokens, metrics)
+
+    # ------------------------------------------------- split decode iteration
+
+    def can_launch(self, decode: Sequence[ScheduledRequest]) -> bool:
+        """Whether these decode requests can run as launch_decode / finish."""
+
+        return (self.graphs is not None and bool(decode)
+                and not any(r.generation_config.do_sample for r in decode))
+
+    def launch_decode(self, decode: Sequence[ScheduledRequest], *,
+                      token_source: torch.Tensor | None = None) -> LaunchedDecode:
+        """Phases 1 and 2 of a decode-only iteration up to the queued replay; the
+        reservation stays open (commit or discard it). token_source: the (B,) device
+        tokens to feed, in `decode` order, instead of each request's last token."""
+
+        checked = self._check((), decode)
+        reservation = self.manager.reservation()
+        try:
+            _, dec_work = self._reserve(reservation, checked)
+            _, greedy = self.graphs.run(dec_work, token_source=token_source)
+            b = len(dec_work)
+            turn = self._token_turn
+            self._token_turn ^= 1
+            host = self._token_host[turn]
+            if host is None or host.numel() < b:
+                host = torch.empty(max(b, 256), dtype=torch.int64, pin_memory=True)
+                self._token_host[turn] = host
+            host[:b].copy_(greedy.view(-1), non_blocking=True)
+            ready = torch.cuda.Event()
+            ready.record()
+        except BaseException:
+            reservation.rollback()
+            raise
+        return LaunchedDecode(checked, reservation, greedy.view(-1), host, ready)
+
+    @staticmethod
+    def commit(launched: LaunchedDecode) -> None:
+        launched.reservation.commit()
+
+    @staticmethod
+    def discard(launched: LaunchedDecode) -> None:
+        """Undo a launch that will not be finished: its positions and blocks go back
+        (the K/V it writes lands past every sequence's valid length)."""
+
+        launched.reservation.rollback()
+
+    def finish(self, launched: LaunchedDecode, *, metrics=None) -> tuple[str, ...]:
+        """Phase 3 of a launched iteration (after commit): its tokens and hooks."""
+
+        launched.ready.synchronize()
+        tokens = launched.host[: len(launched.checked.decode)].tolist()
+        return self._apply((), launched.checked, tokens, metrics)
 
     # ----------------------------------------------------------- phase 1
 

@@ -20,6 +20,13 @@ growing sequences reuse a graph for many steps.
 The first iteration of a new shape runs eagerly (which also allocates the
 decode workspace, the RoPE table and the fused weights outside the capture),
 then the same metadata is captured; the capture records and does not execute.
+
+Two pinned staging buffers alternate, each reused only once the copy out of
+it has completed (an event per buffer), so the host can fill the next
+iteration's metadata while the previous one's copy and replay are still
+queued. An iteration's token ids may come from a device tensor instead of
+the host (the previous iteration's greedy tokens, copied device to device
+after the metadata): the host then need not have read them back yet.
 """
 
 from __future__ import annotations
@@ -51,7 +58,9 @@ class DecodeGraphs:
         self.width_quantum = width_quantum
         self.max_graphs = max_graphs
         self._graphs: dict[tuple[int, int], _Captured] = {}
-        self._staging: torch.Tensor | None = None
+        self._staging: list[torch.Tensor | None] = [None, None]
+        self._staged: list[torch.cuda.Event | None] = [None, None]
+        self._turn = 0
 
     def supported(self) -> bool:
         return self.device.type == "cuda"
@@ -112,15 +121,31 @@ class DecodeGraphs:
             prefill_block_tables=empty32.view(0, 1), prefill_max_query_len=0,
             prefill_max_seq_len=0, decode_max_seq_len=w * self.block_size, **views)
 
-    def _upload(self, host: np.ndarray, static: torch.Tensor) -> None:
+    def _upload(self, host: np.ndarray, static: torch.Tensor, b: int,
+                token_source: torch.Tensor | None) -> None:
+        turn = self._turn
+        self._turn ^= 1
         n = host.nbytes
-        if self._staging is None or self._staging.numel() < n:
-            self._staging = torch.empty(max(n, 1 << 16), dtype=torch.uint8, pin_memory=True)
-        self._staging[:n].numpy()[:] = host
-        static[:n].copy_(self._staging[:n], non_blocking=True)
+        if self._staged[turn] is not None:
+            self._staged[turn].synchronize()  # the copy out of this buffer has run
+        staging = self._staging[turn]
+        if staging is None or staging.numel() < n:
+            staging = torch.empty(max(n, 1 << 16), dtype=torch.uint8, pin_memory=True)
+            self._staging[turn] = staging
+        staging[:n].numpy()[:] = host
+        static[:n].copy_(staging[:n], non_blocking=True)
+        if self._staged[turn] is None:
+            self._staged[turn] = torch.cuda.Event()
+        self._staged[turn].record()
+        if token_source is not None:
+            # token_ids is the first section of the layout
+            static[: 8 * b].view(torch.int64).copy_(token_source, non_blocking=True)
 
-    def run(self, works: list[SequenceWork]) -> tuple[torch.Tensor, torch.Tensor]:
-        """Logits (B, V) and greedy tokens (B,) of one decode-only iteration."""
+    def run(self, works: list[SequenceWork], *,
+            token_source: torch.Tensor | None = None) -> tuple[torch.Tensor, torch.Tensor]:
+        """Logits (B, V) and greedy tokens (B,) of one decode-only iteration.
+        token_source: (B,) int64 device tensor of the token ids, in place of the works'
+        tokens (read on the stream, after everything queued before this call)."""
 
         b = len(works)
         w = self.width_for(works)
@@ -128,12 +153,12 @@ class DecodeGraphs:
         host = self._host_bytes(works, w)
         captured = self._graphs.get(key)
         if captured is not None:
-            self._upload(host, captured.static)
+            self._upload(host, captured.static, b, token_source)
             captured.graph.replay()
             return captured.logits, captured.tokens
         _, total = self._layout(b, w)
         static = torch.zeros(total, dtype=torch.uint8, device=self.device)
-        self._upload(host, static)
+        self._upload(host, static, b, token_source)
         batch = self._batch(static, b, w)
         logits = self.model.forward_packed(batch, self.storage)  # eager: this step's result
         tokens = ops.greedy_argmax(logits).view(-1)

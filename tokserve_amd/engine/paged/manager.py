@@ -133,7 +133,8 @@ class StepReservation:
 
     def rollback(self) -> None:
         for cache in reversed(self._appending):
-            cache.abort_append()
+            if cache.is_live:  # a sequence released meanwhile gave its blocks back itself
+                cache.abort_append()
         self._appending.clear()
         for sequence_id in reversed(self._opened):
             self.manager.release_sequence(sequence_id)

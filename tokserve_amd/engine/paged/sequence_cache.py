@@ -77,6 +77,12 @@ class SequencePagedKVCache:
         return 0 if append is None else append.count
 
     @property
+    def is_live(self) -> bool:
+        """False once release() has run."""
+
+        return self._live
+
+    @property
     def num_blocks(self) -> int:
         return self._active().block_table.num_blocks
 
