@@ -92,6 +92,141 @@ def cpu_baseline(batch, target_seconds: float) -> dict:
     }
 
 
+def _cpu_threads() -> int:
+    import torch
+
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    return cores
+
+
+def _cpu_median(fn, target_seconds: float) -> tuple[float, int]:
+    """Median seconds of fn() on the host after one untimed call: at least 3 runs, more
+    until target_seconds have passed."""
+
+    fn()
+    times: list[float] = []
+    start = time.perf_counter()
+    while len(times) < 3 or time.perf_counter() - start < target_seconds:
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    times.sort()
+    return times[len(times) // 2], len(times)
+
+
+def cpu_small_fp32_step(target_seconds: float) -> dict:
+    """The fp32 decode step of measure_small_fp32_step through the oracle (the reference's
+    torch backend, request by request): RMSNorm, RoPE of each new Q/K at its position, the
+    slot write, then the paged decode of every sequence."""
+
+    import torch
+
+    from oracle import paged, torch_path
+    from tokserve_amd import workloads
+
+    cores = _cpu_threads()
+    batch = workloads.decode_fp32_small("cpu", seed=0)
+    g = torch.Generator().manual_seed(1)
+    hidden = torch.randn(8, 512, generator=g)
+    weight = 1.0 + 0.02 * torch.randn(512, generator=g)
+    new_k = torch.randn(8, 2, 64, generator=g)
+    new_v = torch.randn(8, 2, 64, generator=g)
+    key_cache, value_cache = batch.key_cache.clone(), batch.value_cache.clone()
+
+    def step() -> None:
+        torch_path.rms_norm(hidden, weight, 1e-5)
+        rotated = []
+        for b, ctx in enumerate(batch.contexts):
+            q, k = torch_path.apply_rope(batch.query[b][None, :, None, :],
+                                         new_k[b][None, :, None, :], torch.tensor([ctx - 1]),
+                                         theta=10_000.0)
+            block, offset = int(batch.block_tables[b, (ctx - 1) // 16]), (ctx - 1) % 16
+            key_cache[0, block, :, offset, :] = k[0, :, 0, :]
+            value_cache[0, block, :, offset, :] = new_v[b]
+            rotated.append(q[0, :, 0, :])
+        paged.decode_batch(torch.stack(rotated), key_cache, value_cache, batch.block_tables,
+                           batch.seq_lens, 0)
+
+    seconds, runs = _cpu_median(step, target_seconds)
+    return {"value": round(seconds * 1e6, 1), "unit": "us per step", "cores": cores,
+            "kind": "port",
+            "sample": f"the whole step, median of {runs} runs on {cores} host threads"}
+
+
+def cpu_norm_rope(target_seconds: float) -> dict:
+    """The packed RMSNorm and RoPE of measure_norm_rope through the oracle (the reference's
+    torch ops, bf16 in, fp32 weight): GB/s of the same algorithmic bytes."""
+
+    from oracle import torch_path
+    from tokserve_amd import workloads
+
+    cores = _cpu_threads()
+    data = workloads.norm_rope_packed("cpu", seed=0)
+    n = data.hidden.shape[0]
+    query = data.query.permute(1, 0, 2).unsqueeze(0)  # (1, Hq, N, Dh)
+    key = data.key.permute(1, 0, 2).unsqueeze(0)
+    norm_s, norm_runs = _cpu_median(
+        lambda: torch_path.rms_norm(data.hidden, data.weight, data.epsilon), target_seconds / 2)
+    rope_s, rope_runs = _cpu_median(
+        lambda: torch_path.apply_rope(query, key, data.positions, theta=data.theta),
+        target_seconds / 2)
+    norm_bytes = n * 4096 * (2 + 4) + 4096 * 4
+    rope_bytes = n * (40 * 128 * 2 * 2 + 8)
+    return {"rmsnorm_gbps": round(norm_bytes / norm_s / 1e9, 2),
+            "rope_gbps": round(rope_bytes / rope_s / 1e9, 2), "unit": "GB/s", "cores": cores,
+            "kind": "port",
+            "sample": f"the whole {n}-token stream, medians of {norm_runs} / {rope_runs} runs "
+                      f"on {cores} host threads"}
+
+
+def cpu_mixed(target_seconds: float) -> dict:
+    """The mixed step's attention through the oracle (the reference's torch backend, bf16,
+    request by request) on a sample of its requests: 2 of the 16 prefill chunks and 16 of
+    the 240 decodes, drawn from the workload's own generator; the full step's time is
+    projected from the sample's TFLOP/s and GB/s."""
+
+    import torch
+
+    from oracle import paged
+    from tokserve_amd import workloads
+
+    cores = _cpu_threads()
+    gen = torch.Generator().manual_seed(0)
+    priors = workloads.uniform_ints(16, 0, 2048, gen)
+    decode_ctx = workloads.uniform_ints(240, 256, 4096, gen)
+    chunks, decodes = 2, 16
+    contexts = [p + 512 for p in priors[:chunks]] + decode_ctx[:decodes]
+    batch = workloads.paged_batch(contexts, [512] * chunks + [1] * decodes, num_q_heads=32,
+                                  num_kv_heads=8, head_dim=128, block_size=16,
+                                  dtype=torch.bfloat16, device="cpu", seed=7)
+    n_pre = 512 * chunks
+    pre_s, pre_runs = _cpu_median(
+        lambda: paged.prefill_batch(batch.query[:n_pre], batch.key_cache, batch.value_cache,
+                                    batch.block_tables[:chunks], batch.seq_lens[:chunks],
+                                    batch.cu_seqlens_q[: chunks + 1], 0), target_seconds / 2)
+    dec_s, dec_runs = _cpu_median(
+        lambda: paged.decode_batch(batch.query[n_pre:], batch.key_cache, batch.value_cache,
+                                   batch.block_tables[chunks:], batch.seq_lens[chunks:], 0),
+        target_seconds / 2)
+
+    def flops(prior_list):
+        return sum(4 * 32 * 128 * (512 * p + 512 * 513 // 2) for p in prior_list)
+
+    def kv_bytes(ctx_list):
+        return sum(c * 8 * 128 * 2 * 2 for c in ctx_list)
+
+    tflops = flops(priors[:chunks]) / pre_s / 1e12
+    gbps = kv_bytes(decode_ctx[:decodes]) / dec_s / 1e9
+    step_ms = (flops(priors) / (tflops * 1e12) + kv_bytes(decode_ctx) / (gbps * 1e9)) * 1e3
+    return {"value": round(step_ms, 1), "unit": "ms per step (projected)",
+            "prefill_tflops": round(tflops, 4), "decode_gbps": round(gbps, 3), "cores": cores,
+            "kind": "port",
+            "sample": f"{chunks} of the 16 prefill chunks (median of {pre_runs} runs) and "
+                      f"{decodes} of the 240 decodes (median of {dec_runs}) on {cores} host "
+                      "threads; the full step projected from their rates"}
+
+
 def main() -> int:
     parser = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     parser.add_argument("--gpus", type=int, default=1)
@@ -222,6 +357,13 @@ def main() -> int:
             print(f"unknown secondary measurement(s): {sorted(unknown)}", file=sys.stderr)
             return 2
         result["secondary"] = {name: secondaries[name]() for name in chosen}
+        if not args.no_cpu_baseline:
+            cpu = {"small_fp32_step": lambda: cpu_small_fp32_step(2.0),
+                   "norm_rope": lambda: cpu_norm_rope(4.0),
+                   "mixed_step": lambda: cpu_mixed(6.0)}
+            for name in chosen:
+                if name in cpu:
+                    result["secondary"][name]["cpu_baseline"] = cpu[name]()
     if not args.no_e2e:
         e2e = measure_e2e(device, args.seed,
                           None if args.no_cpu_baseline else args.cpu_seconds)
