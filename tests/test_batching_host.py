@@ -279,3 +279,104 @@ def test_reference_keyword_interfaces_and_module_paths() -> None:
         rope.apply_rope(torch.ones(1, 2, 3, 8), torch.ones(1, 1, 3, 8), positions[:3],
                         theta=10_000.0)
     assert build_iteration_plan([]).is_empty
+
+
+class _Ready:
+    def synchronize(self) -> None:
+        pass
+
+
+class LengthTokens(StubExecutor):
+    """Token = (sequence length after the append) % 5, through both the packed forward and
+    the split launch (launch_decode / finish) that the engine's overlap_decode uses, which
+    runs here on the CPU with the same reservations as on the GPU."""
+
+    def _forward(self, prefill, decode, requests):
+        self.builder.build(prefill, decode)
+        return [(w.start + len(w.tokens)) % 5 for w in (*prefill, *decode)]
+
+    def can_launch(self, decode) -> bool:
+        return bool(decode)
+
+    def launch_decode(self, decode, *, token_source=None):
+        self.queued_launches = getattr(self, "queued_launches", 0) + (token_source is not None)
+        checked = self._check((), decode)
+        reservation = self.manager.reservation()
+        try:
+            self._reserve(reservation, checked)
+        except BaseException:
+            reservation.rollback()
+            raise
+        tokens = torch.tensor([(length + 1) % 5 for length in checked.decode_lengths])
+        return execution.LaunchedDecode(checked, reservation, tokens, tokens, _Ready())
+
+
+def _overlap_run(overlap, specs, *, max_running, num_blocks, block_size, eos=None,
+                 between=None, ids=None):
+    recorder = Recorder()
+    model = _model()
+    manager = _manager(num_blocks, block_size)
+    scheduler = RequestScheduler(max_running_requests=max_running, cache_manager=manager)
+    engine = ContinuousBatchEngine(model, scheduler, manager, metrics=recorder,
+                                   overlap_decode=overlap)
+    engine.executor = LengthTokens(model, manager)
+    released = {}
+    original = manager.release_sequence
+
+    def record(sequence_id):
+        released[sequence_id] = manager.get_sequence(sequence_id).block_ids
+        original(sequence_id)
+
+    manager.release_sequence = record
+    _submit(scheduler, specs, eos=eos)
+    step = 0
+    while scheduler.waiting_count or scheduler.running_count:
+        engine.step()
+        step += 1
+        if between is not None:
+            between(step, scheduler)
+    ids = [rid for rid, _, _ in specs] if ids is None else ids
+    tokens = {rid: (scheduler.get_request(rid).state.value,
+                    scheduler.get_request(rid).generated_tokens) for rid in ids}
+    outcome = ([tuple(r.__dict__.values()) for r in engine.history], recorder.events,
+               released, tokens, manager.allocator.free_count)
+    return outcome, getattr(engine.executor, "queued_launches", 0)
+
+
+LONG = (("A", [1, 2, 3], 9), ("B", [4, 5, 6, 7], 6), ("C", [8], 12), ("D", [9, 10], 4))
+
+
+@pytest.mark.parametrize(("max_running", "eos"), [(4, None), (2, None), (4, 3)])
+def test_overlapped_decode_keeps_records_hooks_and_blocks(max_running, eos) -> None:
+    """overlap_decode queues iteration i+1 before finishing iteration i wherever the next
+    plan is fixed; records, hook order, tokens, released block ids and the final pool
+    equal the one-at-a-time engine's. With an EOS token nothing is queued."""
+
+    sequential, queued_off = _overlap_run(False, LONG, max_running=max_running, num_blocks=24,
+                                          block_size=2, eos=eos)
+    overlapped, queued_on = _overlap_run(True, LONG, max_running=max_running, num_blocks=24,
+                                         block_size=2, eos=eos)
+    assert overlapped == sequential
+    assert queued_off == 0
+    assert (queued_on > 0) == (eos is None)
+
+
+def test_overlapped_decode_discards_on_submission_and_cancellation() -> None:
+    """A submission and then a cancellation between steps while an iteration is queued."""
+
+    def between(step, scheduler):
+        if step == 3:
+            scheduler.submit(ScheduledRequest("E", torch.tensor([[11, 12]]),
+                                              GenerationConfig(max_new_tokens=3)))
+        if step == 6 and scheduler.get_request("C").state.value == "running":
+            scheduler.cancel("C")
+
+    ids = [rid for rid, _, _ in LONG] + ["E"]
+    sequential, _ = _overlap_run(False, LONG, max_running=4, num_blocks=30, block_size=2,
+                                 between=between, ids=ids)
+    overlapped, queued = _overlap_run(True, LONG, max_running=4, num_blocks=30, block_size=2,
+                                      between=between, ids=ids)
+    assert overlapped == sequential
+    assert queued > 0
+    assert overlapped[3]["C"][0] == "cancelled" and overlapped[3]["E"][0] == "finished"
+    assert overlapped[4] == 30
