@@ -207,7 +207,8 @@ def test_e2e_config_bf16_records_blocks_logits_and_graphs(device) -> None:
       orders, over 22 layers (logits reach |x| ~ 2.5, where one bf16 step is 0.0156);
       measured: 77 of 128,000 logits beyond 2e-2, the worst 0.03125. Both are also
       printed against the fp32-arithmetic forward of the same weights.
-    * Decode HIP graphs on and off give identical tokens.
+    * Decode HIP graphs on and off, and the engine's decode overlap, give identical tokens
+      (and the overlap identical records).
     * Greedy-token agreement with the oracle is reported: near-ties between the top
       logits of a random-init model make exact agreement a matter of luck in bf16."""
 
@@ -270,6 +271,17 @@ def test_e2e_config_bf16_records_blocks_logits_and_graphs(device) -> None:
                                           GenerationConfig(max_new_tokens=n)))
     eager.run_until_idle()
     assert engine.executor.graphs is not None and engine.executor.graphs._graphs
+    assert tokens == {rid: scheduler.get_request(rid).result.generated_token_ids[0].tolist()
+                      for rid, _, _ in specs}
+    manager = _manager(model, device, num_blocks=blocks, block_size=16, dtype=torch.bfloat16)
+    scheduler = RequestScheduler(max_running_requests=128, cache_manager=manager)
+    overlapped = ContinuousBatchEngine(model, scheduler, manager, overlap_decode=True)
+    for rid, prompt, n in specs:
+        scheduler.submit(ScheduledRequest(rid, torch.tensor([prompt], device=device),
+                                          GenerationConfig(max_new_tokens=n)))
+    overlapped.run_until_idle()
+    assert [tuple(r.__dict__.values()) for r in overlapped.history] == \
+        [tuple(r.__dict__.values()) for r in engine.history]
     assert tokens == {rid: scheduler.get_request(rid).result.generated_token_ids[0].tolist()
                       for rid, _, _ in specs}
     agree = sum(a == b for rid, _, _ in specs
