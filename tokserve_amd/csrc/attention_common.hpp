@@ -40,15 +40,39 @@ __device__ __forceinline__ float nan_max(float a, float b) { return __builtin_el
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 // Merged output element of one (row, head, dim) from n_splits partials at w.
-// The partials are read kMergeBatch splits at a time, every load of a batch
-// issued before the first is used, so a merge costs about two memory latencies
-// per batch (max, then sums) rather than two per split; the arithmetic runs in
-// split order either way.
-constexpr int kMergeBatch = 8;
+// Up to kMergeBatch splits are read in one batch (every load issued before the
+// first is used), so such a merge costs one memory latency; longer ones read
+// kMergeBatch splits at a time, the maxima first and then the sums. The
+// arithmetic runs in split order either way.
+constexpr int kMergeBatch = 16;
 __device__ __forceinline__ float merge_splits(const float *__restrict__ ws_m,
                                               const float *__restrict__ ws_l,
                                               const float *__restrict__ ws_acc, int64_t w,
                                               int n_splits, int head_dim, int d, float *inv_l) {
+  if (n_splits <= kMergeBatch) {
+    float mv[kMergeBatch], lv[kMergeBatch], av[kMergeBatch];
+#pragma unroll
+    for (int u = 0; u < kMergeBatch; ++u) {
+      const bool in = u < n_splits;
+      mv[u] = in ? ws_m[w + u] : -INFINITY;
+      lv[u] = in ? ws_l[w + u] : 0.f;
+      av[u] = in ? ws_acc[(w + u) * head_dim + d] : 0.f;
+    }
+    float M = -INFINITY;
+#pragma unroll
+    for (int u = 0; u < kMergeBatch; ++u) M = fmaxf(M, mv[u]);
+    float L = 0.f, o = 0.f;
+#pragma unroll
+    for (int u = 0; u < kMergeBatch; ++u) {
+      if (u < n_splits) {
+        const float e = exp2f(mv[u] - M);
+        L += e * lv[u];
+        o += e * av[u];
+      }
+    }
+    *inv_l = 1.f / L;
+    return o;
+  }
   float M = -INFINITY;
   for (int s0 = 0; s0 < n_splits; s0 += kMergeBatch) {
     float mv[kMergeBatch];

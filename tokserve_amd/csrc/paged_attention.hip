@@ -348,7 +348,7 @@ __global__ __launch_bounds__(256) void decode_pages_kernel(
 // ------------------------------------------------------------------------
 
 template <typename T>
-__global__ __launch_bounds__(64) void merge_splits_kernel(
+__global__ __launch_bounds__(128) void merge_splits_kernel(
     const int32_t *__restrict__ seq_lens, int32_t key_cap, int32_t block_size,
     int32_t pages_per_split, int32_t max_splits, int32_t num_q_heads, int32_t head_dim,
     const float *__restrict__ ws_m, const float *__restrict__ ws_l,
@@ -360,7 +360,7 @@ __global__ __launch_bounds__(64) void merge_splits_kernel(
   const int n_splits = min((n_pages + pages_per_split - 1) / pages_per_split, max_splits);
   if (n_splits == 0) return;  // the split kernel wrote the zero row
   const int64_t w = ((int64_t)row * num_q_heads + qh) * max_splits;
-  for (int d = threadIdx.x; d < head_dim; d += 64) {
+  for (int d = threadIdx.x; d < head_dim; d += blockDim.x) {
     float inv;
     const float o = merge_splits(ws_m, ws_l, ws_acc, w, n_splits, head_dim, d, &inv);
     out[row * o_rs + (int64_t)qh * o_hs + d] = from_float<T>(o * inv);
@@ -569,11 +569,12 @@ int32_t decode_impl(const void *query, int64_t q_seq_stride, int64_t q_head_stri
   }
   if (st != TKS_OK || max_splits == 1) return st;
   const dim3 grid(num_q_heads, num_seqs);
-#define TKS_MERGE(TYPE)                                                                      \
-  merge_splits_kernel<TYPE><<<grid, 64, 0, s>>>(seq_lens, key_cap, block_size, pps,           \
-                                                max_splits, num_q_heads, head_dim, w.m, w.l, \
-                                                w.acc, static_cast<TYPE *>(out),             \
-                                                out_seq_stride, out_head_stride)
+  const int threads = head_dim > 64 ? 128 : 64;  // one thread per output element
+#define TKS_MERGE(TYPE)                                                                         \
+  merge_splits_kernel<TYPE><<<grid, threads, 0, s>>>(seq_lens, key_cap, block_size, pps,        \
+                                                     max_splits, num_q_heads, head_dim, w.m, w.l, \
+                                                     w.acc, static_cast<TYPE *>(out),             \
+                                                     out_seq_stride, out_head_stride)
   switch (dtype) {
     case TKS_FLOAT32: TKS_MERGE(float); break;
     case TKS_FLOAT16: TKS_MERGE(_Float16); break;
