@@ -197,6 +197,11 @@ struct PageIO<T, fp8e4m3_t> {
   static __device__ __forceinline__ raw zero() { return make_uint2(0, 0); }
 };
 
+template <bool B>
+struct BoolConst {
+  static constexpr bool value = B;
+};
+
 template <typename T, typename KV, int DH, int G>
 __global__ __launch_bounds__(64 * kWaves) void decode_mfma_kernel(DecodeArgs a) {
   using S = DecodeShape<DH, G>;
@@ -204,7 +209,7 @@ __global__ __launch_bounds__(64 * kWaves) void decode_mfma_kernel(DecodeArgs a) 
   using M = Mfma<T>;
   using IO = PageIO<T, KV>;
   using raw = typename IO::raw;
-  __shared__ __attribute__((aligned(16))) float p_s[kWaves][G][BS];
+  __shared__ __attribute__((aligned(16))) float p_s[kWaves][16][BS];  // rows >= G: padding
   __shared__ __attribute__((aligned(16))) float alpha_s[kWaves][G];
   __shared__ __attribute__((aligned(16))) float m_s[kWaves][G];
   __shared__ __attribute__((aligned(16))) float l_s[kWaves][G];
@@ -265,12 +270,17 @@ __global__ __launch_bounds__(64 * kWaves) void decode_mfma_kernel(DecodeArgs a) 
 #pragma unroll
     for (int d = 0; d < 8; ++d) acc[j][d] = 0.f;
   // Per row i of this lane (head (grp*4 + i) % G, token r): m = reference max
-  // in log2 units (-inf before the first key), l = this lane's share of the sum.
-  float m[4], l[4];
+  // in log2 units (-inf before the first key), l = this lane's share of the sum;
+  // thr = m + 8 (a score above it moves the reference) and mref = the value
+  // subtracted before exp2 (m, or 0 while m is -inf), both updated only when
+  // the reference moves.
+  float m[4], l[4], thr[4], mref[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     m[i] = -INFINITY;
     l[i] = 0.f;
+    thr[i] = -INFINITY;
+    mref[i] = 0.f;
   }
   const float scale_log2 = a.scale_log2;
 
@@ -296,18 +306,31 @@ __global__ __launch_bounds__(64 * kWaves) void decode_mfma_kernel(DecodeArgs a) 
   };
 
   using pair = typename IO::pair;
-  auto consume = [&](const raw (&kr)[NC], const raw (&vr)[4], int p) {
+  // vr is the ring's page: rows past the sequence's last key are zeroed in place
+  // (the slot is reloaded before its next use). Only a wave's last page can be
+  // the sequence's last page, so the page loop's steady state passes
+  // kCheckEnd = false and skips the check; its drain passes true.
+  auto consume = [&](auto check_end, const raw (&kr)[NC], raw (&vr)[4], int p) {
+    constexpr bool kCheckEnd = decltype(check_end)::value;
     typename M::f4 s4 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int c = 0; c < NC; ++c) s4 = M::run(qa[c], IO::k_operand(kr[c]), s4);
-    const bool valid = p * BS + r < len;
     float sv[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) sv[i] = s4[i] * scale_log2;
+    // The sequence's last page (uniform): keys past len score -inf, and their V
+    // rows, whatever the pool holds there, are zeroed, since 0 * NaN is NaN.
+    if (kCheckEnd && (p + 1) * BS > len) {
+      const bool valid = p * BS + r < len;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) sv[i] = valid ? sv[i] : -INFINITY;
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        if (p * BS + tg * 4 + j >= len) vr[j] = IO::zero();
+    }
     bool over = false;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      sv[i] = valid ? s4[i] * scale_log2 : -INFINITY;
-      over = over || sv[i] > m[i] + 8.f;
-    }
+    for (int i = 0; i < 4; ++i) over = over || sv[i] > thr[i];
     // A score more than 8 above its row's reference (every row on the first
     // page): row maxima, new references, l rescaled here and the P.V
     // accumulators below (alpha through LDS).
@@ -316,36 +339,27 @@ __global__ __launch_bounds__(64 * kWaves) void decode_mfma_kernel(DecodeArgs a) 
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const float mx = row16_max(sv[i]);
-        const bool bump = mx > m[i] + 8.f;
+        const bool bump = mx > thr[i];
         const float alpha = bump ? fast_exp2(m[i] - mx) : 1.f;
         m[i] = bump ? mx : m[i];
+        thr[i] = m[i] + 8.f;
+        mref[i] = m[i] == -INFINITY ? 0.f : m[i];
         l[i] *= alpha;
         const int h = grp * 4 + i;
         if (h < G && r == 0) alpha_s[wave][h] = alpha;
       }
     }
+    // Rows past G (lane groups replicating heads) land in padding rows of p_s.
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      // m is -inf only while every score so far is (then p = 0).
-      const float pv = fast_exp2(sv[i] - (m[i] == -INFINITY ? 0.f : m[i]));
+      const float pv = fast_exp2(sv[i] - mref[i]);
       l[i] += pv;
-      const int h = grp * 4 + i;
-      if (h < G) p_s[wave][h][r] = pv;
+      p_s[wave][grp * 4 + i][r] = pv;
     }
     wave_lds_sync();
-    raw vz[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) vz[j] = vr[j];
-    if ((p + 1) * BS > len) {
-      // The sequence's last page: rows past the last key hold whatever the pool
-      // has there. Their probabilities are 0, and 0 * NaN would not be.
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-        if (p * BS + tg * 4 + j >= len) vz[j] = IO::zero();
-    }
     pair vp[2][8];
-    IO::v_pairs(vz[0], vz[1], vp[0]);
-    IO::v_pairs(vz[2], vz[3], vp[1]);
+    IO::v_pairs(vr[0], vr[1], vp[0]);
+    IO::v_pairs(vr[2], vr[3], vp[1]);
 #pragma unroll
     for (int j = 0; j < HPL; ++j) {
       const int h = hg * HPL + j;
@@ -390,7 +404,7 @@ __global__ __launch_bounds__(64 * kWaves) void decode_mfma_kernel(DecodeArgs a) 
 #pragma unroll
       for (int j = 0; j < D; ++j) {
         load_page(blk_reg, i + j + D - 1, kb[(j + D - 1) % D], vb[(j + D - 1) % D]);
-        consume(kb[j], vb[j], c0 + i + j);
+        consume(BoolConst<false>{}, kb[j], vb[j], c0 + i + j);
       }
     }
     // Fewer than 2D - 1 pages left; those before i + D - 1 are already loaded.
@@ -399,7 +413,7 @@ __global__ __launch_bounds__(64 * kWaves) void decode_mfma_kernel(DecodeArgs a) 
       if (i + j < n) {
         if (i + j + D - 1 < n)
           load_page(blk_reg, i + j + D - 1, kb[(j + D - 1) % D], vb[(j + D - 1) % D]);
-        consume(kb[j % D], vb[j % D], c0 + i + j);
+        consume(BoolConst<true>{}, kb[j % D], vb[j % D], c0 + i + j);
       }
     }
   }
