@@ -849,28 +849,37 @@ def measure_norm_rope(device, steps: int, warmup: int) -> dict:
     return result
 
 
-def _e2e_engine(model, specs, device, block_size: int = 16, kv_dtype=None, overlap=True):
-    import torch
-
+def _e2e_engine(model, specs, device, block_size: int = 16, kv_dtype=None, overlap=True,
+                num_blocks: int | None = None):
     from tokserve_amd import workloads
     from tokserve_amd.batching.engine import ContinuousBatchEngine
     from tokserve_amd.engine.paged.manager import PagedKVCacheManager
-    from tokserve_amd.generation.types import GenerationConfig
-    from tokserve_amd.scheduler.request import ScheduledRequest
     from tokserve_amd.scheduler.scheduler import RequestScheduler
 
     config = model.config
     manager = PagedKVCacheManager(
-        num_layers=config.num_hidden_layers, num_blocks=workloads.pool_blocks(specs, block_size),
+        num_layers=config.num_hidden_layers,
+        num_blocks=num_blocks or workloads.pool_blocks(specs, block_size),
         num_key_value_heads=config.num_key_value_heads, block_size=block_size,
         head_dim=config.head_dim, device=device, dtype=model.embed_tokens.weight.dtype,
         kv_dtype=kv_dtype)
     scheduler = RequestScheduler(max_running_requests=128, cache_manager=manager)
+    engine = ContinuousBatchEngine(model, scheduler, manager, overlap_decode=overlap)
+    _submit(engine, specs, device)
+    return engine
+
+
+def _submit(engine, specs, device, prefix: str = "") -> None:
+    import torch
+
+    from tokserve_amd.generation.types import GenerationConfig
+    from tokserve_amd.scheduler.request import ScheduledRequest
+
     for spec in specs:
         prompt = torch.tensor([spec.prompt], dtype=torch.int64, device=device)
-        scheduler.submit(ScheduledRequest(spec.request_id, prompt,
-                                          GenerationConfig(max_new_tokens=spec.max_new_tokens)))
-    return ContinuousBatchEngine(model, scheduler, manager, overlap_decode=overlap)
+        engine.scheduler.submit(ScheduledRequest(
+            prefix + spec.request_id, prompt,
+            GenerationConfig(max_new_tokens=spec.max_new_tokens)))
 
 
 def measure_e2e(device, seed: int, cpu_seconds: float | None, kv_dtype=None,
@@ -896,28 +905,36 @@ def measure_e2e(device, seed: int, cpu_seconds: float | None, kv_dtype=None,
     dtype = torch.bfloat16 if dtype is None else dtype
     model = model.to(dtype).eval()
     specs = workloads.tinyllama_requests(seed=seed)
-    # Warm-up at the timed run's shapes (a full-size prefill iteration and two decode
-    # iterations of another request set): library GEMM kernels for those shapes load
-    # here, not in the timed run.
-    warm = workloads.tinyllama_requests(seed=seed + 1, max_new_tokens=2)
-    _e2e_engine(model, warm, device, kv_dtype=kv_dtype).run_until_idle()
-    torch.cuda.synchronize()
+    # The server's warm-up: each engine first serves another request set of the same
+    # shape (prompts U[64, 1024] of other token ids, 128 tokens each) to completion, so
+    # the library GEMM kernels are loaded and the decode HIP graphs of every (batch,
+    # block-table width) the timed set meets are captured, as a server does once at
+    # start-up. Then the timed set is submitted to the same engine: fresh requests,
+    # every token computed, the pool's blocks all free again.
+    warm = workloads.tinyllama_requests(seed=seed + 1)
+    blocks = max(workloads.pool_blocks(warm, 16), workloads.pool_blocks(specs, 16))
 
     def serve(overlap: bool):
-        engine = _e2e_engine(model, specs, device, kv_dtype=kv_dtype, overlap=overlap)
+        engine = _e2e_engine(model, warm, device, kv_dtype=kv_dtype, overlap=overlap,
+                             num_blocks=blocks)
+        engine.run_until_idle()
+        torch.cuda.synchronize()
+        first, done = len(engine.history), len(engine.results)
+        _submit(engine, specs, device, prefix="timed-")
         step_s = []
         start = time.perf_counter()
         while engine.scheduler.waiting_count or engine.scheduler.running_count:
             t0 = time.perf_counter()
             engine.step()
             step_s.append(time.perf_counter() - t0)
-        return engine, step_s, time.perf_counter() - start
+        wall = time.perf_counter() - start
+        return engine.history[first:], engine.results[done:], engine, step_s, wall
 
     # Decode iteration i+1 queued before iteration i's tokens are read back (the
     # engine's overlap_decode), then the same run one iteration at a time.
-    engine, step_s, wall = serve(True)
-    _, _, wall_sequential = serve(False)
-    generated = sum(r.num_generated_tokens for r in engine.results)
+    history, results, engine, step_s, wall = serve(True)
+    *_, wall_sequential = serve(False)
+    generated = sum(r.num_generated_tokens for r in results)
     decode_steps = step_s[1:]
     # Device time of one replay of the largest captured decode graph (the engine has
     # finished; a replay rewrites the last step's K/V with the same values).
@@ -932,7 +949,9 @@ def measure_e2e(device, seed: int, cpu_seconds: float | None, kv_dtype=None,
         "workload": "e2e_tinyllama: TinyLlama-1.1B shape (22 layers, hidden 2048, 32/4 heads, "
                     "Dh 64, MLP 5632, vocab 32000), random init, " + dtype_name + "; 128 requests, prompts "
                     "U[64,1024], 128 greedy tokens, block 16, max_running 128" + pools
-                    + "; decode iteration i+1 queued before iteration i is read back",
+                    + "; decode iteration i+1 queued before iteration i is read back; "
+                    "timed on an engine warmed by another 128-request set of the same shape "
+                    "(decode graphs captured once, as at server start-up)",
         "requests": len(specs),
         "prompt_tokens": sum(len(s.prompt) for s in specs),
         "generated_tokens": generated,
@@ -946,7 +965,7 @@ def measure_e2e(device, seed: int, cpu_seconds: float | None, kv_dtype=None,
         if decode_steps else None,
         "decode_graph_replay_ms": None if replay_ms is None else round(replay_ms, 4),
         "decode_tokens_per_s": round(
-            sum(len(r.decode_ids) for r in engine.history[1:]) / max(sum(decode_steps), 1e-9), 1),
+            sum(len(r.decode_ids) for r in history[1:]) / max(sum(decode_steps), 1e-9), 1),
     }
     if cpu_seconds is not None:
         result["cpu_baseline"] = e2e_cpu_baseline(model, specs, cpu_seconds)
