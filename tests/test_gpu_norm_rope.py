@@ -158,6 +158,40 @@ def test_greedy_argmax_matches_torch(device, dtype) -> None:
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize(("vocab", "width"), [(32003, 32003), (32000, 32005), (9, 9), (2049, 2056),
+                                            (40000, 40000)])
+def test_greedy_argmax_chunked_and_element_paths(device, dtype, vocab, width) -> None:
+    """Rows read in 16-byte chunks (aligned starts and strides) and element by element
+    (any other stride), a vocabulary tail past the last whole chunk, ties between
+    entries that different threads and chunks read, NaN in the tail."""
+
+    g = torch.Generator().manual_seed(vocab + width)
+    base = torch.randn(6, width, generator=g).to(dtype)
+    logits = base.to(device)[:, :vocab]
+    host = base[:, :vocab]
+    host[0, vocab - 1] = host[0, 1] = 60.0                      # tie: first index wins
+    if vocab > 48:
+        host[1, 48] = host[1, 8] = 70.0                         # tie across threads' chunks
+    if vocab > 36000:
+        host[5, 35000] = host[5, 30] = 80.0                     # tie across load batches
+    host[2, vocab - 1] = float("nan")                           # NaN in the tail
+    host[3, 0] = float("nan")
+    host[3, vocab - 1] = float("nan")                           # first NaN wins
+    host[4, :] = float("-inf")                                  # all -inf: index 0
+    logits.copy_(host.to(device))
+    expected = torch_path.select_greedy(host)
+    actual = ops.greedy_argmax(logits)
+    torch.cuda.synchronize()
+    assert torch.equal(actual.cpu(), expected)
+    assert int(actual[0]) == 1 and int(actual[2]) == vocab - 1
+    assert int(actual[3]) == 0 and int(actual[4]) == 0
+    if vocab > 48:
+        assert int(actual[1]) == 8
+    if vocab > 36000:
+        assert int(actual[5]) == 30
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
 @pytest.mark.parametrize(("hq", "hkv", "dh", "bs"), [(32, 8, 128, 16), (32, 4, 64, 16),
                                                      (4, 2, 10, 3)])
 def test_rope_kv_append_equals_rope_then_append(device, dtype, hq, hkv, dh, bs) -> None:
