@@ -142,6 +142,40 @@ int32_t tks_paged_attention_decode(const void *query, int64_t q_seq_stride, int6
                                    tks_stream_t stream);
 
 /* ------------------------------------------------------------------------
+ * RoPE, the KV append and decode attention of a decode step in one call.
+ * Replaces, for one new token per sequence, the reference's apply_rope
+ * (tokserve/engine/rope.py:106-153) of the query and key, write_layer
+ * (tokserve/engine/paged/sequence_cache.py:86-131) and triton_paged_attention
+ * (tokserve/kernels/paged_attention.py:11-88), which its decode step runs in turn
+ * per request (tokserve/engine/attention.py:247-335); in this library, the same as
+ * tks_rope_kv_append then tks_paged_attention_decode:
+ *   - sequence b's query row (read only; strides q_seq_stride, q_head_stride) is
+ *     rotated at positions[b] with the cos/sin tables of tks_rope;
+ *   - its new key row (rotated) and value row (strides k_*, v_*, [num_seqs,
+ *     num_kv_heads, head_dim]) are written to pool slot slot_mapping[b] of
+ *     layer_index, which must address position seq_lens[b] - 1 of sequence b
+ *     (a negative slot appends nothing);
+ *   - out receives the attention of the rotated query over keys 0..seq_lens[b]-1,
+ *     as tks_paged_attention_decode computes it (same workspace rule).
+ * Results are bit-identical to the two calls. For bf16/fp16 pools on the MFMA
+ * decode kernel the query is rotated in registers and the new rows are written and
+ * used by the workgroup that reads the sequence's last page: one launch (plus the
+ * split merge). Other shapes run the two calls, with the rotated queries staged
+ * in `out`.
+ */
+int32_t tks_rope_append_paged_decode(
+    const void *query, int64_t q_seq_stride, int64_t q_head_stride, const void *key,
+    int64_t k_seq_stride, int64_t k_head_stride, const void *value, int64_t v_seq_stride,
+    int64_t v_head_stride, const int64_t *positions, const void *cos_cache,
+    const void *sin_cache, int64_t cache_len, const int64_t *slot_mapping, void *key_cache,
+    void *value_cache, int32_t num_layers, int64_t num_blocks, int32_t num_kv_heads,
+    int32_t block_size, int32_t head_dim, int32_t layer_index, const int32_t *block_tables,
+    int32_t block_table_stride, const int32_t *seq_lens, const int32_t *seq_order,
+    int32_t num_seqs, int32_t num_q_heads, int32_t max_seq_len, float scale,
+    int32_t pages_per_split, void *out, int64_t out_seq_stride, int64_t out_head_stride,
+    void *workspace, int64_t workspace_bytes, int32_t dtype, tks_stream_t stream);
+
+/* ------------------------------------------------------------------------
  * Decode attention that allocates nothing: tks_paged_attention_decode with the
  * split-K partials in a static device buffer the library owns instead of a
  * caller workspace. No counterpart in the reference (whose kernels allocate

@@ -4,9 +4,10 @@ per-sequence forward, recorded with a dispatch mode (the analogue of the referen
 call-count check that its custom kernels ran, tests/gpu/test_tiled_attention_end_to_end.py:237-290).
 
 Per layer a packed iteration makes two RMSNorm launches (the first layer's input norm
-without a residual), one RoPE + KV append, one attention launch (prefill or decode),
-one SiLU*mul; the final norm and one greedy argmax close it. No softmax, matmul-based
-attention or gather of the pools runs in torch.
+without a residual), one SiLU*mul, and either one RoPE + KV append and one prefill
+attention launch (an iteration with prefill tokens) or one fused RoPE + KV append +
+decode attention call (a decode-only iteration); the final norm and one greedy argmax
+close it. No softmax, matmul-based attention or gather of the pools runs in torch.
 """
 
 from collections import Counter
@@ -78,15 +79,16 @@ def test_packed_iterations_launch_only_library_kernels(device, dtype) -> None:
         executor.execute((), running)
     torch.cuda.synchronize()
 
-    for calls, attention in ((prefill, "paged_attention_prefill"),
-                             (decode, "paged_attention_decode")):
+    pre, dec = _ours(prefill.count), _ours(decode.count)
+    assert pre["rope_kv_append_"] + pre["rope_kv_append"] == LAYERS, pre
+    assert pre["paged_attention_prefill"] == LAYERS, pre
+    assert pre["paged_attention_decode"] + pre["rope_append_paged_decode"] == 0, pre
+    assert dec["rope_append_paged_decode"] == LAYERS, dec
+    assert dec["rope_kv_append_"] + dec["rope_kv_append"] == 0, dec
+    assert dec["paged_attention_prefill"] + dec["paged_attention_decode"] == 0, dec
+    for calls in (prefill, decode):
         ours = _ours(calls.count)
         assert ours["rms_norm"] == 2 * LAYERS + 1, ours
-        assert ours["rope_kv_append_"] + ours["rope_kv_append"] == LAYERS, ours
-        assert ours[attention] == LAYERS, ours
-        other = ("paged_attention_decode" if attention == "paged_attention_prefill"
-                 else "paged_attention_prefill")
-        assert ours[other] == 0, ours
         assert ours["silu_mul"] == LAYERS, ours
         assert ours["greedy_argmax"] == 1, ours
         assert ours["paged_gather"] == 0, ours

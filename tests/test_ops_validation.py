@@ -72,6 +72,7 @@ def test_every_operator_is_registered_with_its_writes_marked() -> None:
         "rope_": {"query", "key"},
         "rope_kv_append": {"key_cache", "value_cache", "query_out", "key_out"},
         "rope_kv_append_": {"query", "key_cache", "value_cache", "key_out"},
+        "rope_append_paged_decode": {"key_cache", "value_cache", "out", "workspace"},
         "greedy_argmax": {"out"},
         "silu_mul": {"out"},
         "vector_add": {"out"},

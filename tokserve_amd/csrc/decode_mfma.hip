@@ -26,6 +26,7 @@
 // block ids sit in one VGPR (broadcast with readlane), so nothing in the page
 // loop waits on a dependent memory access.
 #include "attention_common.hpp"
+#include "rope_common.hpp"
 
 namespace tks {
 namespace {
@@ -202,7 +203,46 @@ struct BoolConst {
   static constexpr bool value = B;
 };
 
-template <typename T, typename KV, int DH, int G>
+template <typename T>
+__device__ __forceinline__ uint4 v8_bits(typename Mfma<T>::v8 v) {
+  uint4 r;
+  __builtin_memcpy(&r, &v, 16);
+  return r;
+}
+
+// The fused append's pool write: sequence b's new key row rotated at its position,
+// and its value row, into pool slot a.slots[b] of KV head kvh (a negative or
+// out-of-pool slot writes nothing). Called by one workgroup per (sequence, KV head).
+template <typename T, int DH, int BS>
+__device__ __forceinline__ void append_new_rows(const DecodeArgs &a, int b, int kvh) {
+  constexpr int HALF = DH / 2;
+  const int64_t slot = a.slots[b];
+  if (slot < 0 || slot >= a.pool.num_blocks * BS) return;
+  const int t = threadIdx.x;
+  const T *kn = static_cast<const T *>(a.k_new) + b * a.kn_ss + (int64_t)kvh * a.kn_hs;
+  const T *vn = static_cast<const T *>(a.v_new) + b * a.vn_ss + (int64_t)kvh * a.vn_hs;
+  const int64_t blk = slot / BS;
+  const int64_t row = a.pool.layer_base + blk * a.pool.block_stride +
+                      (int64_t)kvh * a.pool.head_stride + (slot - blk * BS) * DH;
+  if (t < HALF / 8) {
+    const int64_t pos = min(max(a.positions[b], (int64_t)0), a.table_len - 1);
+    float cf[8], sf[8], o1[8], o2[8];
+    load_table<T, 8>(static_cast<const T *>(a.cos_t) + pos * HALF,
+                     static_cast<const T *>(a.sin_t) + pos * HALF, t * 8, cf, sf);
+    rotate_values<T, 8>(kn + t * 8, cf, sf, HALF, o1, o2);
+    store_pair<T, 8>(static_cast<T *>(const_cast<void *>(a.kc)) + row + t * 8, o1, o2, HALF);
+  } else if (t < HALF / 8 + DH / 8) {
+    const int c = (t - HALF / 8) * 8;
+    st16(static_cast<T *>(const_cast<void *>(a.vc)) + row + c, ld16(vn + c));
+  }
+}
+
+// ROPE: RoPE and the KV append of the sequence's new token fused in (DecodeArgs).
+// Every workgroup rotates its query rows in registers; the new key row is rotated
+// and the value row copied to the pool by the workgroup that reads the sequence's
+// last page, which also substitutes both rows for what it loads of that page, so
+// no workgroup reads pool memory written in the same launch.
+template <typename T, typename KV, int DH, int G, bool ROPE>
 __global__ __launch_bounds__(64 * kWaves) void decode_mfma_kernel(DecodeArgs a) {
   using S = DecodeShape<DH, G>;
   constexpr int BS = S::BS, NC = S::NC, LPR = S::LPR, TG = S::TG, HPL = S::HPL;
@@ -233,9 +273,13 @@ __global__ __launch_bounds__(64 * kWaves) void decode_mfma_kernel(DecodeArgs a) 
   const int p_begin = split * a.pages_per_split;
   T *out = static_cast<T *>(a.out);
   if (p_begin >= n_pages) {
-    if (split == 0)  // empty sequence: defined all-zero output
+    if (split == 0) {  // empty sequence: defined all-zero output
       for (int i = threadIdx.x; i < G * DH; i += 64 * kWaves)
         out[b * a.o_ss + (int64_t)(kvh * G + i / DH) * a.o_hs + i % DH] = from_float<T>(0.f);
+      if constexpr (ROPE) {
+        if (n_pages == 0) append_new_rows<T, DH, BS>(a, b, kvh);
+      }
+    }
     return;
   }
   const int p_end = min(n_pages, p_begin + a.pages_per_split);
@@ -256,6 +300,42 @@ __global__ __launch_bounds__(64 * kWaves) void decode_mfma_kernel(DecodeArgs a) 
                   grp * (kSlab ? NC * 8 : 8);
 #pragma unroll
     for (int c = 0; c < NC; ++c) qa[c] = as_v8<T>(ld16(qp + c * kQStep));
+  }
+
+  // Fused RoPE + append: this lane's query chunks c and c + NC/2 hold dims d and
+  // d + Dh/2 (d = c*32 + grp*8 ..), a rotation pair; the new key row's chunks of the
+  // same dims (for the lanes of the row's token) and the new value row's chunk dc
+  // (for the lanes of its token group) are kept for the last page.
+  raw krot[NC], vnew = IO::zero();
+  bool patch = false;
+  const int new_off = ROPE ? (len - 1) % BS : 0;
+  if constexpr (ROPE) {
+    static_assert(!kSlab, "the fused append writes pools in the model dtype");
+    constexpr int HALF = DH / 2;
+    const int64_t pos = min(max(a.positions[b], (int64_t)0), a.table_len - 1);
+    const T *crow = static_cast<const T *>(a.cos_t) + pos * HALF;
+    const T *srow = static_cast<const T *>(a.sin_t) + pos * HALF;
+    const T *kn = static_cast<const T *>(a.k_new) + b * a.kn_ss + (int64_t)kvh * a.kn_hs;
+    const T *vn = static_cast<const T *>(a.v_new) + b * a.vn_ss + (int64_t)kvh * a.vn_hs;
+    const int64_t slot = a.slots[b];
+    patch = slot >= 0 && slot < a.pool.num_blocks * BS;
+#pragma unroll
+    for (int c = 0; c < NC / 2; ++c) {
+      const int d = c * 32 + grp * 8;
+      float cf[8], sf[8], x1[8], x2[8], o1[8], o2[8];
+      load_table<T, 8>(crow, srow, d, cf, sf);
+      unpack<T>(v8_bits<T>(qa[c]), x1);
+      unpack<T>(v8_bits<T>(qa[c + NC / 2]), x2);
+      rotate_math<T, 8>(x1, x2, cf, sf, o1, o2);
+      qa[c] = as_v8<T>(pack<T>(o1));
+      qa[c + NC / 2] = as_v8<T>(pack<T>(o2));
+      rotate_values<T, 8>(kn + d, cf, sf, HALF, o1, o2);
+      krot[c] = pack<T>(o1);
+      krot[c + NC / 2] = pack<T>(o2);
+    }
+    vnew = ld16(vn + dc * 8);
+    // The workgroup of the last page writes the new rows to the pool slot.
+    if ((n_pages - 1) / a.pages_per_split == split) append_new_rows<T, DH, BS>(a, b, kvh);
   }
 
   const KV *kc = static_cast<const KV *>(a.kc) + a.pool.layer_base + (int64_t)kvh * a.pool.head_stride;
@@ -310,6 +390,19 @@ __global__ __launch_bounds__(64 * kWaves) void decode_mfma_kernel(DecodeArgs a) 
   // (the slot is reloaded before its next use). Only a wave's last page can be
   // the sequence's last page, so the page loop's steady state passes
   // kCheckEnd = false and skips the check; its drain passes true.
+  // The fused append's new rows in place of what was loaded of the sequence's last
+  // page (only a wave's last page can be it: the page loop's drain).
+  auto substitute_new_rows = [&](raw (&kr)[NC], raw (&vr)[4], int p) {
+    if (patch && p == n_pages - 1) {
+      if (r == new_off) {
+#pragma unroll
+        for (int c = 0; c < NC; ++c) kr[c] = krot[c];
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        if (tg * 4 + j == new_off) vr[j] = vnew;
+    }
+  };
   auto consume = [&](auto check_end, const raw (&kr)[NC], raw (&vr)[4], int p) {
     constexpr bool kCheckEnd = decltype(check_end)::value;
     typename M::f4 s4 = {0.f, 0.f, 0.f, 0.f};
@@ -413,6 +506,7 @@ __global__ __launch_bounds__(64 * kWaves) void decode_mfma_kernel(DecodeArgs a) 
       if (i + j < n) {
         if (i + j + D - 1 < n)
           load_page(blk_reg, i + j + D - 1, kb[(j + D - 1) % D], vb[(j + D - 1) % D]);
+        if constexpr (ROPE) substitute_new_rows(kb[j % D], vb[j % D], c0 + i + j);
         consume(BoolConst<true>{}, kb[j % D], vb[j % D], c0 + i + j);
       }
     }
@@ -474,16 +568,16 @@ __global__ __launch_bounds__(64 * kWaves) void decode_mfma_kernel(DecodeArgs a) 
   }
 }
 
-template <typename T, typename KV>
+template <typename T, typename KV, bool ROPE = false>
 int32_t launch_typed(const DecodeArgs &a, int32_t num_seqs, int32_t num_kv_heads, int32_t G,
                      int32_t head_dim, hipStream_t s) {
   // KV heads vary fastest (consecutive workgroups, dealt round-robin over the
   // XCDs, carry equal work), splits slowest.
   const dim3 grid(num_kv_heads, num_seqs, a.max_splits);
-#define TKS_DECODE(DH, GG)                                              \
-  if (head_dim == DH && G == GG) {                                      \
-    decode_mfma_kernel<T, KV, DH, GG><<<grid, 64 * kWaves, 0, s>>>(a);  \
-    return check_launch();                                              \
+#define TKS_DECODE(DH, GG)                                                    \
+  if (head_dim == DH && G == GG) {                                            \
+    decode_mfma_kernel<T, KV, DH, GG, ROPE><<<grid, 64 * kWaves, 0, s>>>(a);  \
+    return check_launch();                                                    \
   }
   TKS_DECODE(128, 4)
   TKS_DECODE(128, 8)
@@ -509,6 +603,14 @@ bool decode_mfma_supported(int32_t dtype, int32_t head_dim, int32_t group) {
 int32_t launch_decode_mfma(const DecodeArgs &a, int32_t dtype, int32_t num_seqs,
                            int32_t num_kv_heads, int32_t group, int32_t head_dim,
                            hipStream_t stream, bool fp8_pools) {
+  if (a.positions != nullptr) {
+    if (fp8_pools) return TKS_ERR_VALUE;
+    return dtype == TKS_BFLOAT16
+               ? launch_typed<bf16_t, bf16_t, true>(a, num_seqs, num_kv_heads, group, head_dim,
+                                                    stream)
+               : launch_typed<_Float16, _Float16, true>(a, num_seqs, num_kv_heads, group,
+                                                        head_dim, stream);
+  }
   if (fp8_pools)
     return dtype == TKS_BFLOAT16
                ? launch_typed<bf16_t, fp8e4m3_t>(a, num_seqs, num_kv_heads, group, head_dim, stream)

@@ -511,6 +511,19 @@ extern "C" int64_t tks_paged_attention_decode_workspace_bytes(int32_t num_seqs,
 
 namespace {
 
+// RoPE and the KV append of each sequence's new token, fused into a decode launch
+// (tks_rope_append_paged_decode).
+struct RopeAppend {
+  const void *key;
+  int64_t k_ss, k_hs;
+  const void *value;
+  int64_t v_ss, v_hs;
+  const int64_t *positions;
+  const void *cos_cache, *sin_cache;
+  int64_t cache_len;
+  const int64_t *slot_mapping;
+};
+
 int32_t decode_impl(const void *query, int64_t q_seq_stride, int64_t q_head_stride,
                     const void *key_cache, const void *value_cache, int32_t num_layers,
                     int64_t num_blocks, int32_t num_kv_heads, int32_t block_size,
@@ -520,7 +533,7 @@ int32_t decode_impl(const void *query, int64_t q_seq_stride, int64_t q_head_stri
                     int32_t max_seq_len, float scale, int32_t pages_per_split, void *out,
                     int64_t out_seq_stride, int64_t out_head_stride, void *workspace,
                     int64_t workspace_bytes, bool fp8_pools, float k_scale, float v_scale,
-                    int32_t dtype, tks_stream_t stream) {
+                    int32_t dtype, tks_stream_t stream, const RopeAppend *ra = nullptr) {
   if (!valid_dtype(dtype)) return TKS_ERR_TYPE;
   if (!pool_ok(num_layers, num_blocks, num_kv_heads, block_size, head_dim) || num_seqs < 0 ||
       num_q_heads <= 0 || num_q_heads % num_kv_heads != 0 || max_seq_len < 0 ||
@@ -549,14 +562,56 @@ int32_t decode_impl(const void *query, int64_t q_seq_stride, int64_t q_head_stri
   hipStream_t s = static_cast<hipStream_t>(stream);
   const float scale_log2 = scale * kLog2e * k_scale;
 
+  const bool mfma = mfma_eligible(dtype, block_size, head_dim, G, query, q_seq_stride,
+                                  q_head_stride, key_cache, value_cache, out, out_seq_stride,
+                                  out_head_stride);
+  if (ra != nullptr) {
+    // Fused when the MFMA kernel runs with its rows in 16-byte chunks and keeps two
+    // waves per SIMD with the extra registers (all but Dh 128 with G 8); otherwise
+    // the RoPE + append launch writes the rotated queries into `out`, which the
+    // decode then reads as its query (each workgroup reads its rows before it, or
+    // the merge, writes them).
+    const bool fused = mfma && !fp8_pools && !(head_dim == 128 && G == 8) &&
+                       aligned16(ra->key) && aligned16(ra->value) && aligned16(ra->cos_cache) &&
+                       aligned16(ra->sin_cache) && ra->k_ss % 8 == 0 && ra->k_hs % 8 == 0 &&
+                       ra->v_ss % 8 == 0 && ra->v_hs % 8 == 0;
+    if (!fused) {
+      const int32_t st0 = tks_rope_kv_append(
+          query, out, q_seq_stride, q_head_stride, out_seq_stride, out_head_stride, num_q_heads,
+          ra->key, nullptr, ra->k_ss, ra->k_hs, 0, 0, ra->value, ra->v_ss, ra->v_hs,
+          num_kv_heads, num_seqs, head_dim, ra->positions, ra->cos_cache, ra->sin_cache,
+          ra->cache_len, const_cast<void *>(key_cache), const_cast<void *>(value_cache),
+          num_layers, num_blocks, block_size, layer_index, ra->slot_mapping, dtype, stream);
+      if (st0 != TKS_OK) return st0;
+      return decode_impl(out, out_seq_stride, out_head_stride, key_cache, value_cache,
+                         num_layers, num_blocks, num_kv_heads, block_size, head_dim, layer_index,
+                         block_tables, block_table_stride, seq_lens, seq_order, num_seqs,
+                         num_q_heads, max_seq_len, scale, pages_per_split, out, out_seq_stride,
+                         out_head_stride, workspace, workspace_bytes, fp8_pools, k_scale, v_scale,
+                         dtype, stream);
+    }
+  }
+
   int32_t st;
-  if (mfma_eligible(dtype, block_size, head_dim, G, query, q_seq_stride, q_head_stride,
-                    key_cache, value_cache, out, out_seq_stride, out_head_stride)) {
+  if (mfma) {
     DecodeArgs a{query,      q_seq_stride, q_head_stride, key_cache,   value_cache,
                  pool,       block_tables, block_table_stride, seq_lens, seq_order, num_q_heads,
                  scale_log2, pps,          max_splits,    key_cap,     out,
                  out_seq_stride, out_head_stride, w.m,    w.l,         w.acc,
                  v_scale};
+    if (ra != nullptr) {
+      a.positions = ra->positions;
+      a.cos_t = ra->cos_cache;
+      a.sin_t = ra->sin_cache;
+      a.table_len = ra->cache_len;
+      a.k_new = ra->key;
+      a.kn_ss = ra->k_ss;
+      a.kn_hs = ra->k_hs;
+      a.v_new = ra->value;
+      a.vn_ss = ra->v_ss;
+      a.vn_hs = ra->v_hs;
+      a.slots = ra->slot_mapping;
+    }
     st = launch_decode_mfma(a, dtype, num_seqs, num_kv_heads, G, head_dim, s, fp8_pools);
   } else {
     const int kv_elem = fp8_pools ? 1 : elem_bytes(dtype);
@@ -741,6 +796,31 @@ extern "C" int32_t tks_paged_attention_decode(
                      block_table_stride, seq_lens, seq_order, num_seqs, num_q_heads, max_seq_len,
                      scale, pages_per_split, out, out_seq_stride, out_head_stride, workspace,
                      workspace_bytes, false, 1.f, 1.f, dtype, stream);
+}
+
+extern "C" int32_t tks_rope_append_paged_decode(
+    const void *query, int64_t q_seq_stride, int64_t q_head_stride, const void *key,
+    int64_t k_seq_stride, int64_t k_head_stride, const void *value, int64_t v_seq_stride,
+    int64_t v_head_stride, const int64_t *positions, const void *cos_cache,
+    const void *sin_cache, int64_t cache_len, const int64_t *slot_mapping, void *key_cache,
+    void *value_cache, int32_t num_layers, int64_t num_blocks, int32_t num_kv_heads,
+    int32_t block_size, int32_t head_dim, int32_t layer_index, const int32_t *block_tables,
+    int32_t block_table_stride, const int32_t *seq_lens, const int32_t *seq_order,
+    int32_t num_seqs, int32_t num_q_heads, int32_t max_seq_len, float scale,
+    int32_t pages_per_split, void *out, int64_t out_seq_stride, int64_t out_head_stride,
+    void *workspace, int64_t workspace_bytes, int32_t dtype, tks_stream_t stream) {
+  if (!valid_dtype(dtype)) return TKS_ERR_TYPE;
+  if (head_dim < 2 || head_dim % 2 != 0 || cache_len <= 0 || num_seqs < 0) return TKS_ERR_VALUE;
+  if (num_seqs > 0 && (!key || !value || !positions || !cos_cache || !sin_cache || !slot_mapping))
+    return TKS_ERR_VALUE;
+  const RopeAppend ra{key,       k_seq_stride, k_head_stride, value,     v_seq_stride,
+                      v_head_stride, positions, cos_cache,  sin_cache, cache_len,
+                      slot_mapping};
+  return decode_impl(query, q_seq_stride, q_head_stride, key_cache, value_cache, num_layers,
+                     num_blocks, num_kv_heads, block_size, head_dim, layer_index, block_tables,
+                     block_table_stride, seq_lens, seq_order, num_seqs, num_q_heads, max_seq_len,
+                     scale, pages_per_split, out, out_seq_stride, out_head_stride, workspace,
+                     workspace_bytes, false, 1.f, 1.f, dtype, stream, &ra);
 }
 
 extern "C" int32_t tks_paged_attention_decode_fp8(

@@ -10,7 +10,7 @@
 // One workgroup per token: the table row is read once and shared by all
 // Hq + Hkv heads; each lane rotates one 16-byte chunk of the first half
 // together with its partner chunk of the second half.
-#include "common.hpp"
+#include "rope_common.hpp"
 
 namespace tks {
 namespace {
@@ -29,68 +29,12 @@ struct RopeTensor {
   int32_t heads;
 };
 
-// Rotates one chunk pair of x into o1 (dims c..c+V) and o2 (dims c+D/2..).
-template <typename T, int V>
-__device__ __forceinline__ void rotate_values(const T *x, const float *c, const float *s,
-                                              int half, float *o1, float *o2) {
-#pragma clang fp contract(off)
-  float x1[V], x2[V];
-  if constexpr (V * sizeof(T) == 16) {
-    unpack<T>(ld16(x), x1);
-    unpack<T>(ld16(x + half), x2);
-  } else {
-#pragma unroll
-    for (int j = 0; j < V; ++j) {
-      x1[j] = to_float(x[j]);
-      x2[j] = to_float(x[half + j]);
-    }
-  }
-#pragma unroll
-  for (int j = 0; j < V; ++j) {
-    const float a1 = round_through<T>(x1[j] * c[j]);
-    const float b1 = round_through<T>(-x2[j] * s[j]);
-    const float a2 = round_through<T>(x2[j] * c[j]);
-    const float b2 = round_through<T>(x1[j] * s[j]);
-    o1[j] = a1 + b1;
-    o2[j] = a2 + b2;
-  }
-}
-
-template <typename T, int V>
-__device__ __forceinline__ void store_pair(T *y, const float *o1, const float *o2, int half) {
-  if constexpr (V * sizeof(T) == 16) {
-    st16(y, pack<T>(o1));
-    st16(y + half, pack<T>(o2));
-  } else {
-#pragma unroll
-    for (int j = 0; j < V; ++j) {
-      y[j] = from_float<T>(o1[j]);
-      y[half + j] = from_float<T>(o2[j]);
-    }
-  }
-}
-
 template <typename T, int V>
 __device__ __forceinline__ void rotate(const T *x, T *y, const float *c, const float *s,
                                        int half) {
   float o1[V], o2[V];
   rotate_values<T, V>(x, c, s, half, o1, o2);
   store_pair<T, V>(y, o1, o2, half);
-}
-
-template <typename T, int V>
-__device__ __forceinline__ void load_table(const T *crow, const T *srow, int c, float *cf,
-                                           float *sf) {
-  if constexpr (V * sizeof(T) == 16) {
-    unpack<T>(ld16(crow + c), cf);
-    unpack<T>(ld16(srow + c), sf);
-  } else {
-#pragma unroll
-    for (int j = 0; j < V; ++j) {
-      cf[j] = to_float(crow[c + j]);
-      sf[j] = to_float(srow[c + j]);
-    }
-  }
 }
 
 template <typename T, int V>

@@ -556,6 +556,82 @@ def rope_kv_append(
     return query_out
 
 
+def rope_append_paged_decode(
+    query: torch.Tensor,
+    key: torch.Tensor,
+    value: torch.Tensor,
+    positions: torch.Tensor,
+    table: RotaryTable,
+    key_cache: torch.Tensor,
+    value_cache: torch.Tensor,
+    slot_mapping: torch.Tensor,
+    block_tables: torch.Tensor,
+    seq_lens: torch.Tensor,
+    *,
+    layer_index: int,
+    max_seq_len: int,
+    scale: float | None = None,
+    out: torch.Tensor | None = None,
+    workspace: torch.Tensor | None = None,
+    pages_per_split: int = 0,
+    seq_order: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """A decode step's RoPE, KV append and attention in one call: query (B, Hq, Dh) is
+    rotated at positions (B,) (read only), the rotated key and the value rows (B, Hkv, Dh)
+    go to pool slots slot_mapping (B,), which must address position seq_lens[b] - 1, and
+    out (B, Hq, Dh) receives the attention over seq_lens[b] keys.
+
+    Bit-identical to rope_kv_append() followed by paged_attention_decode() with the
+    same arguments (one launch on the MFMA decode kernel). Pools in the rows' dtype.
+    """
+
+    require_hip("rope_append_paged_decode", query, key, value, positions, key_cache,
+                value_cache, slot_mapping, block_tables, seq_lens)
+    num_layers, num_blocks, num_kv_heads, block_size, head_dim = _pool_shape(
+        key_cache, value_cache
+    )
+    if is_fp8_pool(key_cache):
+        raise ValueError("rope_append_paged_decode needs pools in the rows' dtype")
+    if query.ndim != 3 or key.ndim != 3 or value.shape != key.shape:
+        raise ValueError("query (B, Hq, Dh), key and value (B, Hkv, Dh) expected")
+    num_seqs, num_q_heads, _ = query.shape
+    if key.shape != (num_seqs, num_kv_heads, head_dim) or query.shape[2] != head_dim:
+        raise ValueError("key and value rows must match the pool's (Hkv, Dh)")
+    if len({query.dtype, key.dtype, value.dtype, key_cache.dtype, table.dtype}) != 1:
+        raise ValueError("query, key, value, pools and the rotary table must share a dtype")
+    if head_dim != table.head_dim:
+        raise ValueError("head_dim must match the rotary table")
+    if num_q_heads % num_kv_heads != 0:
+        raise ValueError("query head count must be divisible by KV head count")
+    if positions.shape != (num_seqs,) or slot_mapping.shape != (num_seqs,):
+        raise ValueError("positions and slot_mapping must have shape (B,)")
+    pos = positions if positions.dtype == torch.int64 else positions.to(torch.int64)
+    pos = pos.contiguous()
+    slots = _int_tensor(slot_mapping, torch.int64, "slot_mapping")
+    for name, t in (("query", query), ("key", key), ("value", value)):
+        if t.stride(-1) != 1:
+            raise ValueError(f"{name} must be contiguous in head_dim")
+    tables = _int_tensor(block_tables, torch.int32, "block_tables")
+    lens = _int_tensor(seq_lens, torch.int32, "seq_lens")
+    if tables.ndim != 2 or tables.shape[0] != num_seqs or lens.shape != (num_seqs,):
+        raise ValueError("block_tables (B, max_blocks) and seq_lens (B,) must match query")
+    if out is None:
+        out = torch.empty(query.shape, dtype=query.dtype, device=query.device)
+    if out.shape != query.shape or out.dtype != query.dtype or out.stride(-1) != 1:
+        raise ValueError("out must match query and be contiguous in head_dim")
+    if scale is None:
+        scale = 1.0 / sqrt(head_dim)
+    order = None
+    if seq_order is not None:
+        order = _int_tensor(seq_order, torch.int32, "seq_order")
+        if order.shape != (num_seqs,):
+            raise ValueError("seq_order must have shape (B,)")
+    _ops.rope_append_paged_decode(query, key, value, pos, table.cos, table.sin, slots, key_cache,
+                                  value_cache, tables, lens, order, layer_index, max_seq_len,
+                                  float(scale), pages_per_split, out, workspace)
+    return out
+
+
 # ----------------------------------------------------------------------------
 # Greedy selection
 

@@ -91,6 +91,13 @@ SCHEMAS = {
         "Tensor cos, Tensor sin, Tensor(b!) key_cache, Tensor(c!) value_cache, "
         "Tensor slot_mapping, int layer_index, Tensor(d!)? key_out) -> ()"
     ),
+    "rope_append_paged_decode": (
+        "rope_append_paged_decode(Tensor query, Tensor key, Tensor value, Tensor positions, "
+        "Tensor cos, Tensor sin, Tensor slot_mapping, Tensor(a!) key_cache, "
+        "Tensor(b!) value_cache, Tensor block_tables, Tensor seq_lens, Tensor? seq_order, "
+        "int layer_index, int max_seq_len, float scale, int pages_per_split, Tensor(c!) out, "
+        "Tensor(d!)? workspace) -> ()"
+    ),
     "greedy_argmax": "greedy_argmax(Tensor logits, Tensor(a!) out) -> ()",
     "silu_mul": "silu_mul(Tensor gate_up, Tensor(a!) out) -> ()",
     "vector_add": "vector_add(Tensor x, Tensor y, Tensor(a!) out) -> ()",
@@ -112,6 +119,8 @@ ENTRY_POINTS = {
     "rope_": ("tks_rope",),
     "rope_kv_append": ("tks_rope_kv_append",),
     "rope_kv_append_": ("tks_rope_kv_append",),
+    "rope_append_paged_decode": ("tks_rope_append_paged_decode",
+                                 "tks_paged_attention_decode_workspace_bytes"),
     "greedy_argmax": ("tks_argmax",),
     "silu_mul": ("tks_silu_mul",),
     "vector_add": ("tks_vector_add",),
@@ -321,6 +330,29 @@ def _rope_kv_append_inplace(query, key, value, positions, cos, sin, key_cache, v
                            value_cache, slot_mapping, layer_index, key_out)
 
 
+def _rope_append_paged_decode(query, key, value, positions, cos, sin, slot_mapping, key_cache,
+                              value_cache, block_tables, seq_lens, seq_order, layer_index,
+                              max_seq_len, scale, pages_per_split, out, workspace_tensor):
+    num_layers, num_blocks, num_kv_heads, block_size, head_dim = _pool_dims(key_cache)
+    if workspace_tensor is None:
+        nbytes = decode_workspace_bytes(query.shape[0], query.shape[1], num_kv_heads, head_dim,
+                                        block_size, max_seq_len, pages_per_split)
+        workspace_tensor = workspace(query.device, nbytes, "decode")
+    status = _lib.load().tks_rope_append_paged_decode(
+        query.data_ptr(), query.stride(0), query.stride(1),
+        key.data_ptr(), key.stride(0), key.stride(1),
+        value.data_ptr(), value.stride(0), value.stride(1),
+        positions.data_ptr(), cos.data_ptr(), sin.data_ptr(), cos.shape[0],
+        slot_mapping.data_ptr(), key_cache.data_ptr(), value_cache.data_ptr(),
+        num_layers, num_blocks, num_kv_heads, block_size, head_dim, layer_index,
+        block_tables.data_ptr(), block_tables.shape[1], seq_lens.data_ptr(), _lib.ptr(seq_order),
+        query.shape[0], query.shape[1], max_seq_len, scale, pages_per_split,
+        out.data_ptr(), out.stride(0), out.stride(1),
+        _lib.ptr(workspace_tensor), 0 if workspace_tensor is None else workspace_tensor.numel(),
+        _code(query), _stream(query))
+    _lib.check(status, "rope_append_paged_decode")
+
+
 def _greedy_argmax(logits, out):
     status = _lib.load().tks_argmax(logits.data_ptr(), logits.stride(0), logits.shape[0],
                                     logits.shape[1], out.data_ptr(), _code(logits),
@@ -352,6 +384,7 @@ KERNELS = {
     "rope_": _rope_inplace,
     "rope_kv_append": _rope_kv_append,
     "rope_kv_append_": _rope_kv_append_inplace,
+    "rope_append_paged_decode": _rope_append_paged_decode,
     "greedy_argmax": _greedy_argmax,
     "silu_mul": _silu_mul,
     "vector_add": _vector_add,
