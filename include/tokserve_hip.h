@@ -303,6 +303,23 @@ int32_t tks_paged_attention_prefill_fp8(
     int64_t out_head_stride, void *workspace, int64_t workspace_bytes, float k_scale,
     float v_scale, int32_t dtype, tks_stream_t stream);
 
+/* A decode step's RoPE, quantizing KV append and attention in one call
+ * (tks_rope_append_paged_decode on fp8 pools): bit-identical to
+ * tks_rope_kv_append_fp8 followed by tks_paged_attention_decode_fp8 with the same
+ * arguments. */
+int32_t tks_rope_append_paged_decode_fp8(
+    const void *query, int64_t q_seq_stride, int64_t q_head_stride, const void *key,
+    int64_t k_seq_stride, int64_t k_head_stride, const void *value, int64_t v_seq_stride,
+    int64_t v_head_stride, const int64_t *positions, const void *cos_cache,
+    const void *sin_cache, int64_t cache_len, const int64_t *slot_mapping, void *key_cache,
+    void *value_cache, int32_t num_layers, int64_t num_blocks, int32_t num_kv_heads,
+    int32_t block_size, int32_t head_dim, int32_t layer_index, const int32_t *block_tables,
+    int32_t block_table_stride, const int32_t *seq_lens, const int32_t *seq_order,
+    int32_t num_seqs, int32_t num_q_heads, int32_t max_seq_len, float scale,
+    int32_t pages_per_split, void *out, int64_t out_seq_stride, int64_t out_head_stride,
+    void *workspace, int64_t workspace_bytes, float k_scale, float v_scale, int32_t dtype,
+    tks_stream_t stream);
+
 /* ------------------------------------------------------------------------
  * RMSNorm over the last dimension.
  * Replaces triton_rms_norm (tokserve/kernels/rmsnorm.py:6-45, kernel
@@ -366,6 +383,23 @@ int32_t tks_rope_kv_append(const void *query, void *query_out, int64_t q_ts, int
                            void *value_cache, int32_t num_layers, int64_t num_blocks,
                            int32_t block_size, int32_t layer_index,
                            const int64_t *slot_mapping, int32_t dtype, tks_stream_t stream);
+
+/* tks_rope_kv_append on fp8 pools (the e4m3 pool variant described with
+ * tks_kv_append_fp8): the rotated key row, held at `dtype` precision, and the value
+ * row are written as e4m3(clamp(x / scale)) with k_scale / v_scale. Bit-identical to
+ * tks_rope followed by tks_kv_append_fp8 of the rotated keys.
+ */
+int32_t tks_rope_kv_append_fp8(const void *query, void *query_out, int64_t q_ts, int64_t q_hs,
+                               int64_t qo_ts, int64_t qo_hs, int32_t num_q_heads,
+                               const void *key, void *key_out, int64_t k_ts, int64_t k_hs,
+                               int64_t ko_ts, int64_t ko_hs, const void *value, int64_t v_ts,
+                               int64_t v_hs, int32_t num_kv_heads, int64_t num_tokens,
+                               int32_t head_dim, const int64_t *positions,
+                               const void *cos_cache, const void *sin_cache, int64_t cache_len,
+                               void *key_cache, void *value_cache, int32_t num_layers,
+                               int64_t num_blocks, int32_t block_size, int32_t layer_index,
+                               const int64_t *slot_mapping, float k_scale, float v_scale,
+                               int32_t dtype, tks_stream_t stream);
 
 /* ------------------------------------------------------------------------
  * Greedy token selection: first index of the row maximum (NaN counts as the

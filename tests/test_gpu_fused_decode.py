@@ -4,8 +4,10 @@ on the same inputs: the pools after the call and the outputs are bit-identical, 
 query is left as it was. Covered: the fused MFMA launch (bf16 / fp16, Dh 64 and 128,
 several GQA groups, with and without key splits, partly filled and exactly full last
 pages, a new token that opens a page), the two-call path it takes elsewhere (fp32 on the
-generic kernel, Dh 128 with G 8), a negative slot (nothing appended) and an empty
-sequence (its row is appended, its output is zero).
+generic kernel, new rows not in 16-byte chunks), a negative slot (nothing appended) and an empty
+sequence (its row is appended, its output is zero). Over fp8 (e4m3) pools the same
+against tks_rope_kv_append_fp8 then tks_paged_attention_decode_fp8, and the fp8
+RoPE + append launch against tks_rope then the quantizing tks_kv_append_fp8.
 """
 
 import pytest
@@ -22,15 +24,19 @@ CASES = [
     (torch.bfloat16, 32, 8, 128, [1, 16, 17, 31, 32, 33, 200, 1025, 4096, 4097]),
     (torch.float16, 16, 8, 128, [5, 48, 49, 700]),
     (torch.bfloat16, 16, 16, 128, [300, 17, 1]),
-    (torch.bfloat16, 32, 4, 128, [90, 900]),       # G 8 at Dh 128: the two-call path
+    (torch.bfloat16, 32, 4, 128, [90, 900]),       # G 8 at Dh 128
     (torch.float32, 8, 2, 64, [16, 17, 513, 100]),  # fp32: generic kernel, two calls
 ]
 
 
-def _inputs(device, dtype, hq, hkv, dh, contexts, seed):
+FP8 = torch.float8_e4m3fn
+
+
+def _inputs(device, dtype, hq, hkv, dh, contexts, seed, kv_dtype=None, scales=(1.0, 1.0)):
     batch = workloads.paged_batch(contexts, [1] * len(contexts), num_q_heads=hq,
                                   num_kv_heads=hkv, head_dim=dh, block_size=16, dtype=dtype,
-                                  device=device, seed=seed)
+                                  device=device, seed=seed, kv_dtype=kv_dtype,
+                                  k_scale=scales[0], v_scale=scales[1])
     b = len(contexts)
     g = torch.Generator().manual_seed(seed + 3)
     qkv = torch.randn(b, (hq + 2 * hkv) * dh, generator=g).to(dtype).to(device)
@@ -120,6 +126,110 @@ def test_fused_decode_step_empty_sequence_still_appends(device, dtype) -> None:
     assert torch.equal(actual.cpu().view(torch.int16), expected.cpu().view(torch.int16))
     assert not actual[0].any() and not actual[3].any()
     assert torch.equal(batch.key_cache, kc_ref) and torch.equal(batch.value_cache, vc_ref)
+
+
+FP8_CASES = [
+    # dtype, Hq, Hkv, Dh, contexts, (k_scale, v_scale)
+    (torch.bfloat16, 32, 4, 64, [64 + 37 * i for i in range(24)], (0.5, 0.25)),
+    (torch.bfloat16, 32, 8, 128, [1, 16, 17, 31, 32, 33, 200, 1025, 4096, 4097], (1.0, 1.0)),
+    (torch.float16, 16, 8, 128, [5, 48, 49, 700], (2.0, 0.75)),
+    (torch.bfloat16, 32, 4, 128, [90, 900, 33], (0.125, 4.0)),   # G 8 at Dh 128
+    (torch.float32, 8, 2, 64, [16, 17, 513, 100], (0.5, 2.0)),   # fp32: two calls
+]
+
+
+@pytest.mark.parametrize("case", range(len(FP8_CASES)))
+@pytest.mark.parametrize("pages_per_split", [0, 2])
+def test_fused_decode_step_over_fp8_pools(device, case, pages_per_split) -> None:
+    dtype, hq, hkv, dh, contexts, scales = FP8_CASES[case]
+    batch, query, key, value, positions, slots, table = _inputs(
+        device, dtype, hq, hkv, dh, contexts, seed=40 + case, kv_dtype=FP8, scales=scales)
+    kw = dict(k_scale=scales[0], v_scale=scales[1])
+    order = ops.longest_first(batch.contexts, device)
+    query_before = query.clone()
+    kc_ref, vc_ref = batch.key_cache.clone(), batch.value_cache.clone()
+    q_ref = query.clone()
+    ops.rope_kv_append(q_ref, key, value, positions, table, kc_ref, vc_ref, slots, 0, **kw)
+    expected = ops.paged_attention_decode(
+        q_ref, kc_ref, vc_ref, batch.block_tables, batch.seq_lens, layer_index=0,
+        max_seq_len=batch.max_seq_len, pages_per_split=pages_per_split, seq_order=order, **kw)
+    actual = ops.rope_append_paged_decode(
+        query, key, value, positions, table, batch.key_cache, batch.value_cache, slots,
+        batch.block_tables, batch.seq_lens, layer_index=0, max_seq_len=batch.max_seq_len,
+        pages_per_split=pages_per_split, seq_order=order, **kw)
+    torch.cuda.synchronize()
+    bits = torch.int32 if dtype == torch.float32 else torch.int16
+    assert torch.equal(actual.cpu().view(bits), expected.cpu().view(bits))
+    assert torch.equal(batch.key_cache.view(torch.uint8), kc_ref.view(torch.uint8))
+    assert torch.equal(batch.value_cache.view(torch.uint8), vc_ref.view(torch.uint8))
+    assert torch.equal(query, query_before)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("dh", [64, 128, 40])
+def test_rope_kv_append_over_fp8_pools_equals_rope_then_quantizing_append(device, dtype,
+                                                                          dh) -> None:
+    n, hq, hkv, scales = 37, 8, 2, (0.375, 1.5)
+    g = torch.Generator().manual_seed(dh)
+    pool_shape = (2, 8, hkv, 16, dh)
+    kc = (torch.randn(pool_shape, generator=g) * 3).to(FP8).to(device)
+    vc = (torch.randn(pool_shape, generator=g) * 3).to(FP8).to(device)
+    q = (torch.randn(n, hq, dh, generator=g) * 4).to(dtype).to(device)
+    k = (torch.randn(n, hkv, dh, generator=g) * 4).to(dtype).to(device)
+    v = (torch.randn(n, hkv, dh, generator=g) * 4).to(dtype).to(device)
+    k[3, 1, 5] = float("nan")
+    v[4, 0, 7] = -float("nan")
+    k[5, 0, 0] = 1e4                                   # past the e4m3 range after scaling
+    pos = torch.randint(0, 500, (n,), generator=g).to(device)
+    slots = torch.randperm(8 * 16, generator=g)[:n].to(torch.int64)
+    slots[6] = -1
+    slots = slots.to(device)
+    table = ops.RotaryTable(dh, theta=10_000.0, max_position=512, dtype=dtype, device=device)
+    kw = dict(k_scale=scales[0], v_scale=scales[1])
+
+    q_ref, k_ref = q.clone(), k.clone()
+    ops.rope(q_ref.transpose(0, 1).unsqueeze(0), k_ref.transpose(0, 1).unsqueeze(0), pos,
+             table, query_out=q_ref.transpose(0, 1).unsqueeze(0),
+             key_out=k_ref.transpose(0, 1).unsqueeze(0))
+    kc_ref, vc_ref = kc.clone(), vc.clone()
+    ops.kv_append(k_ref, v, kc_ref, vc_ref, slots, 1, **kw)
+
+    q_out = torch.empty_like(q)
+    k_out = torch.empty_like(k)
+    ops.rope_kv_append(q, k, v, pos, table, kc, vc, slots, 1, query_out=q_out, key_out=k_out,
+                       **kw)
+    torch.cuda.synchronize()
+    bits = torch.int32 if dtype == torch.float32 else torch.int16
+    assert torch.equal(q_out.cpu().view(bits), q_ref.cpu().view(bits))
+    assert torch.equal(k_out.cpu().view(bits), k_ref.cpu().view(bits))
+    assert torch.equal(kc.view(torch.uint8), kc_ref.view(torch.uint8))
+    assert torch.equal(vc.view(torch.uint8), vc_ref.view(torch.uint8))
+
+
+@pytest.mark.parametrize("kv_dtype", [None, FP8])
+def test_fused_decode_step_unaligned_new_rows_take_two_launches(device, kv_dtype) -> None:
+    hq, hkv, dh, contexts = 16, 4, 64, [70, 5, 300]
+    batch, query, _, _, positions, slots, table = _inputs(
+        device, torch.bfloat16, hq, hkv, dh, contexts, seed=31, kv_dtype=kv_dtype)
+    b = len(contexts)
+    rows = torch.randn(b, 2 * hkv * dh + 1, generator=torch.Generator().manual_seed(5))
+    rows = rows.to(torch.bfloat16).to(device)
+    key = rows[:, 1 : 1 + hkv * dh].view(b, hkv, dh)   # 2-byte aligned only
+    value = rows[:, 1 + hkv * dh :].view(b, hkv, dh)
+    kw = dict(k_scale=0.5, v_scale=2.0) if kv_dtype is not None else {}
+    kc_ref, vc_ref = batch.key_cache.clone(), batch.value_cache.clone()
+    q_ref = query.clone()
+    ops.rope_kv_append(q_ref, key, value, positions, table, kc_ref, vc_ref, slots, 0, **kw)
+    expected = ops.paged_attention_decode(q_ref, kc_ref, vc_ref, batch.block_tables,
+                                          batch.seq_lens, layer_index=0,
+                                          max_seq_len=batch.max_seq_len, **kw)
+    actual = ops.rope_append_paged_decode(
+        query, key, value, positions, table, batch.key_cache, batch.value_cache, slots,
+        batch.block_tables, batch.seq_lens, layer_index=0, max_seq_len=batch.max_seq_len, **kw)
+    torch.cuda.synchronize()
+    assert torch.equal(actual.cpu().view(torch.int16), expected.cpu().view(torch.int16))
+    assert torch.equal(batch.key_cache.view(torch.uint8), kc_ref.view(torch.uint8))
+    assert torch.equal(batch.value_cache.view(torch.uint8), vc_ref.view(torch.uint8))
 
 
 def test_fused_decode_step_argument_errors(device) -> None:

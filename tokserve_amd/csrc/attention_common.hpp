@@ -160,13 +160,15 @@ struct DecodeArgs {
   // RoPE + KV append fused into the decode (launch_decode_mfma with rope = true):
   // sequence b's query is rotated in registers at positions[b] (q itself is not
   // written); its new key row (rotated) and value row go to pool slot slots[b]
-  // (negative: none), written by the workgroup that reads the sequence's last page.
+  // (negative: none), written by the workgroup that reads the sequence's last page
+  // (over e4m3 pools quantized with k_scale and v_scale).
   const int64_t *positions = nullptr;
   const void *cos_t = nullptr, *sin_t = nullptr;  // [table_len, Dh / 2] in the model dtype
   int64_t table_len = 0;
   const void *k_new = nullptr, *v_new = nullptr;
   int64_t kn_ss = 0, kn_hs = 0, vn_ss = 0, vn_hs = 0;
   const int64_t *slots = nullptr;
+  float k_scale = 1.f;  // e4m3 pools: the new key row is stored as e4m3(key / k_scale)
 };
 
 struct PrefillArgs {

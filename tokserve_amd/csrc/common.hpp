@@ -202,6 +202,41 @@ __device__ __forceinline__ void unpack<fp8e4m3_t>(uint4 v, float *out) {
   fp8x4_to_float(v.w, out + 12);
 }
 
+// e4m3 codes of x[i] / scale for N values (a multiple of 4) already held at the row
+// dtype's precision, four codes per word (element 0 in the low byte): the division in
+// fp32, the clamp to +-448 and one rounding to e4m3, NaN keeping the sign of x.
+template <int N>
+__device__ __forceinline__ void e4m3_words(const float *x, float scale, uint32_t *w) {
+  static_assert(N % 4 == 0, "whole e4m3 words");
+#pragma unroll
+  for (int i = 0; i < N / 4; ++i)
+    w[i] = fp8x4_nan_sign(float4_to_fp8x4(x[4 * i] / scale, x[4 * i + 1] / scale,
+                                          x[4 * i + 2] / scale, x[4 * i + 3] / scale),
+                          x + 4 * i);
+}
+
+// The same codes for N = 1, 4, 8 or 16 values stored to dst (N bytes; the 4-, 8- and
+// 16-byte stores need that alignment).
+template <int N>
+__device__ __forceinline__ void encode_e4m3(const float *x, float scale, uint8_t *dst) {
+  if constexpr (N == 1) {
+    const float x4[4] = {x[0], 0.f, 0.f, 0.f};
+    dst[0] = static_cast<uint8_t>(
+        fp8x4_nan_sign(float4_to_fp8x4(x[0] / scale, 0.f, 0.f, 0.f), x4) & 0xffu);
+  } else {
+    static_assert(N == 4 || N == 8 || N == 16, "one 4-, 8- or 16-byte store");
+    uint32_t w[N / 4];
+    e4m3_words<N>(x, scale, w);
+    if constexpr (N == 16) {
+      st16(dst, make_uint4(w[0], w[1], w[2], w[3]));
+    } else if constexpr (N == 8) {
+      *reinterpret_cast<uint2 *>(dst) = make_uint2(w[0], w[1]);
+    } else {
+      *reinterpret_cast<uint32_t *>(dst) = w[0];
+    }
+  }
+}
+
 template <typename T>
 __device__ __forceinline__ uint16_t bits16(T x) {
   uint16_t b;

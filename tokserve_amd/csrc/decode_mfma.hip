@@ -210,31 +210,96 @@ __device__ __forceinline__ uint4 v8_bits(typename Mfma<T>::v8 v) {
   return r;
 }
 
-// The fused append's pool write: sequence b's new key row rotated at its position,
-// and its value row, into pool slot a.slots[b] of KV head kvh (a negative or
-// out-of-pool slot writes nothing). Called by one workgroup per (sequence, KV head).
-template <typename T, int DH, int BS>
-__device__ __forceinline__ void append_new_rows(const DecodeArgs &a, int b, int kvh) {
+// Eight values of a row chunk, held at T's precision, as the pool stores them: T
+// elements (16 bytes) or e4m3 codes of value / scale (8 bytes).
+template <typename T, typename KV>
+__device__ __forceinline__ typename PageIO<T, KV>::raw pool_chunk(const float *x, float scale) {
+  if constexpr (sizeof(KV) == 1) {
+    uint32_t w[2];
+    e4m3_words<8>(x, scale, w);
+    return make_uint2(w[0], w[1]);
+  } else {
+    (void)scale;
+    return pack<T>(x);
+  }
+}
+
+template <typename T, typename KV>
+__device__ __forceinline__ void store_chunk(KV *dst, typename PageIO<T, KV>::raw v) {
+  if constexpr (sizeof(KV) == 1)
+    *reinterpret_cast<uint2 *>(dst) = v;
+  else
+    st16(dst, v);
+}
+
+// The fused append, in two steps run by one wave per (sequence, KV head). First
+// the new rows are staged in LDS (k_s, v_s: Dh entries each, in the pool's form):
+// sequence b's key row rotated at its position and its value row, as T or, over
+// e4m3 pools, as the codes of the rotated row (rounded to T first) and of the value
+// row; lanes t < 3 Dh / 16 take part. Returns whether slot a.slots[b] lies in the
+// pool (a negative slot appends nothing).
+template <typename T, typename KV, int DH, int BS>
+__device__ __forceinline__ bool stage_new_rows(const DecodeArgs &a, int b, int kvh, int t,
+                                               KV *k_s, KV *v_s) {
   constexpr int HALF = DH / 2;
   const int64_t slot = a.slots[b];
-  if (slot < 0 || slot >= a.pool.num_blocks * BS) return;
-  const int t = threadIdx.x;
-  const T *kn = static_cast<const T *>(a.k_new) + b * a.kn_ss + (int64_t)kvh * a.kn_hs;
-  const T *vn = static_cast<const T *>(a.v_new) + b * a.vn_ss + (int64_t)kvh * a.vn_hs;
-  const int64_t blk = slot / BS;
-  const int64_t row = a.pool.layer_base + blk * a.pool.block_stride +
-                      (int64_t)kvh * a.pool.head_stride + (slot - blk * BS) * DH;
+  if (slot < 0 || slot >= a.pool.num_blocks * BS) return false;
   if (t < HALF / 8) {
+    const T *kn = static_cast<const T *>(a.k_new) + b * a.kn_ss + (int64_t)kvh * a.kn_hs;
     const int64_t pos = min(max(a.positions[b], (int64_t)0), a.table_len - 1);
     float cf[8], sf[8], o1[8], o2[8];
     load_table<T, 8>(static_cast<const T *>(a.cos_t) + pos * HALF,
                      static_cast<const T *>(a.sin_t) + pos * HALF, t * 8, cf, sf);
     rotate_values<T, 8>(kn + t * 8, cf, sf, HALF, o1, o2);
-    store_pair<T, 8>(static_cast<T *>(const_cast<void *>(a.kc)) + row + t * 8, o1, o2, HALF);
+    if constexpr (sizeof(KV) == 1) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        o1[e] = round_through<T>(o1[e]);
+        o2[e] = round_through<T>(o2[e]);
+      }
+      store_chunk<T, KV>(k_s + t * 8, pool_chunk<T, KV>(o1, a.k_scale));
+      store_chunk<T, KV>(k_s + t * 8 + HALF, pool_chunk<T, KV>(o2, a.k_scale));
+    } else {
+      store_chunk<T, KV>(k_s + t * 8, pack<T>(o1));
+      store_chunk<T, KV>(k_s + t * 8 + HALF, pack<T>(o2));
+    }
   } else if (t < HALF / 8 + DH / 8) {
+    const T *vn = static_cast<const T *>(a.v_new) + b * a.vn_ss + (int64_t)kvh * a.vn_hs;
     const int c = (t - HALF / 8) * 8;
-    st16(static_cast<T *>(const_cast<void *>(a.vc)) + row + c, ld16(vn + c));
+    if constexpr (sizeof(KV) == 1) {
+      float x[8];
+      unpack<T>(ld16(vn + c), x);
+      store_chunk<T, KV>(v_s + c, pool_chunk<T, KV>(x, a.v_scale));
+    } else {
+      store_chunk<T, KV>(v_s + c, ld16(vn + c));
+    }
   }
+  return true;
+}
+
+// Eight pool elements at p (LDS) in the kernel's page-register form.
+template <typename T, typename KV>
+__device__ __forceinline__ typename PageIO<T, KV>::raw load_chunk(const KV *p) {
+  if constexpr (sizeof(KV) == 1)
+    return *reinterpret_cast<const uint2 *>(p);
+  else
+    return ld16(p);
+}
+
+// Then the staged rows go from LDS to pool slot a.slots[b] (lanes t < Dh / 4; the
+// slot was checked by stage_new_rows).
+template <typename T, typename KV, int DH, int BS>
+__device__ __forceinline__ void write_staged_rows(const DecodeArgs &a, int b, int kvh, int t,
+                                                  const KV *k_s, const KV *v_s) {
+  if (t >= DH / 4) return;
+  const int64_t slot = a.slots[b];
+  const int64_t blk = slot / BS;
+  const int64_t row = a.pool.layer_base + blk * a.pool.block_stride +
+                      (int64_t)kvh * a.pool.head_stride + (slot - blk * BS) * DH;
+  const bool is_k = t < DH / 8;
+  const int c = (is_k ? t : t - DH / 8) * 8;
+  KV *dst = static_cast<KV *>(const_cast<void *>(is_k ? a.kc : a.vc)) + row + c;
+  store_chunk<T, KV>(dst, load_chunk<T, KV>((is_k ? k_s : v_s) + c));
 }
 
 // ROPE: RoPE and the KV append of the sequence's new token fused in (DecodeArgs).
@@ -254,6 +319,11 @@ __global__ __launch_bounds__(64 * kWaves) void decode_mfma_kernel(DecodeArgs a) 
   __shared__ __attribute__((aligned(16))) float m_s[kWaves][G];
   __shared__ __attribute__((aligned(16))) float l_s[kWaves][G];
   __shared__ __attribute__((aligned(16))) float acc_s[kWaves][G][DH];
+  // The fused append's new key and value rows, in the pool's form, and (e4m3 pools)
+  // the workgroup's rotated query rows.
+  __shared__ __attribute__((aligned(16))) KV new_k_s[ROPE ? DH : 1];
+  __shared__ __attribute__((aligned(16))) KV new_v_s[ROPE ? DH : 1];
+  __shared__ __attribute__((aligned(16))) T q_s[ROPE && sizeof(KV) == 1 ? G * DH : 1];
 
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
@@ -277,7 +347,11 @@ __global__ __launch_bounds__(64 * kWaves) void decode_mfma_kernel(DecodeArgs a) 
       for (int i = threadIdx.x; i < G * DH; i += 64 * kWaves)
         out[b * a.o_ss + (int64_t)(kvh * G + i / DH) * a.o_hs + i % DH] = from_float<T>(0.f);
       if constexpr (ROPE) {
-        if (n_pages == 0) append_new_rows<T, DH, BS>(a, b, kvh);
+        if (n_pages == 0 && threadIdx.x < 64 &&
+            stage_new_rows<T, KV, DH, BS>(a, b, kvh, threadIdx.x, new_k_s, new_v_s)) {
+          wave_lds_sync();
+          write_staged_rows<T, KV, DH, BS>(a, b, kvh, threadIdx.x, new_k_s, new_v_s);
+        }
       }
     }
     return;
@@ -295,47 +369,61 @@ __global__ __launch_bounds__(64 * kWaves) void decode_mfma_kernel(DecodeArgs a) 
   constexpr bool kSlab = sizeof(KV) == 1;
   constexpr int kQStep = kSlab ? 8 : 32;
   typename M::v8 qa[NC];
-  {
+  if constexpr (!(ROPE && kSlab)) {
     const T *qp = static_cast<const T *>(a.q) + b * a.q_ss + (int64_t)(kvh * G + r % G) * a.q_hs +
                   grp * (kSlab ? NC * 8 : 8);
 #pragma unroll
     for (int c = 0; c < NC; ++c) qa[c] = as_v8<T>(ld16(qp + c * kQStep));
   }
 
-  // Fused RoPE + append: this lane's query chunks c and c + NC/2 hold dims d and
-  // d + Dh/2 (d = c*32 + grp*8 ..), a rotation pair; the new key row's chunks of the
-  // same dims (for the lanes of the row's token) and the new value row's chunk dc
-  // (for the lanes of its token group) are kept for the last page.
-  raw krot[NC], vnew = IO::zero();
+  // Fused RoPE + append. Pools in the model dtype: this lane's query chunks c and
+  // c + NC/2 hold dims d and d + Dh/2 (d = c*32 + grp*8 ..), a rotation pair. e4m3
+  // pools (slab layout): chunk c holds dims grp*NC*8 + c*8 .., whose partners sit
+  // in another lane group, so the workgroup's G query rows are rotated once into
+  // LDS, a rotation pair per thread, and the lanes read their chunks there. The
+  // wave whose range holds the sequence's last page stages the new rows in LDS; its
+  // lanes of the new token put them in place of what they load of that page, and
+  // after its page loop it writes them to the pool.
   bool patch = false;
   const int new_off = ROPE ? (len - 1) % BS : 0;
   if constexpr (ROPE) {
-    static_assert(!kSlab, "the fused append writes pools in the model dtype");
     constexpr int HALF = DH / 2;
     const int64_t pos = min(max(a.positions[b], (int64_t)0), a.table_len - 1);
     const T *crow = static_cast<const T *>(a.cos_t) + pos * HALF;
     const T *srow = static_cast<const T *>(a.sin_t) + pos * HALF;
-    const T *kn = static_cast<const T *>(a.k_new) + b * a.kn_ss + (int64_t)kvh * a.kn_hs;
-    const T *vn = static_cast<const T *>(a.v_new) + b * a.vn_ss + (int64_t)kvh * a.vn_hs;
-    const int64_t slot = a.slots[b];
-    patch = slot >= 0 && slot < a.pool.num_blocks * BS;
+    if constexpr (kSlab) {
+      const int t = threadIdx.x;
+      if (t < G * HALF / 8) {
+        const int h = t / (HALF / 8), j = (t % (HALF / 8)) * 8;
+        const T *qrow = static_cast<const T *>(a.q) + b * a.q_ss + (int64_t)(kvh * G + h) * a.q_hs;
+        float cf[8], sf[8], o1[8], o2[8];
+        load_table<T, 8>(crow, srow, j, cf, sf);
+        rotate_values<T, 8>(qrow + j, cf, sf, HALF, o1, o2);
+        st16(&q_s[h * DH + j], pack<T>(o1));
+        st16(&q_s[h * DH + j + HALF], pack<T>(o2));
+      }
+      __syncthreads();
 #pragma unroll
-    for (int c = 0; c < NC / 2; ++c) {
-      const int d = c * 32 + grp * 8;
-      float cf[8], sf[8], x1[8], x2[8], o1[8], o2[8];
-      load_table<T, 8>(crow, srow, d, cf, sf);
-      unpack<T>(v8_bits<T>(qa[c]), x1);
-      unpack<T>(v8_bits<T>(qa[c + NC / 2]), x2);
-      rotate_math<T, 8>(x1, x2, cf, sf, o1, o2);
-      qa[c] = as_v8<T>(pack<T>(o1));
-      qa[c + NC / 2] = as_v8<T>(pack<T>(o2));
-      rotate_values<T, 8>(kn + d, cf, sf, HALF, o1, o2);
-      krot[c] = pack<T>(o1);
-      krot[c + NC / 2] = pack<T>(o2);
+      for (int c = 0; c < NC; ++c)
+        qa[c] = as_v8<T>(ld16(&q_s[(r % G) * DH + grp * NC * 8 + c * 8]));
+    } else {
+#pragma unroll
+      for (int c = 0; c < NC / 2; ++c) {
+        const int d = c * 32 + grp * 8;
+        float cf[8], sf[8], x1[8], x2[8], o1[8], o2[8];
+        load_table<T, 8>(crow, srow, d, cf, sf);
+        unpack<T>(v8_bits<T>(qa[c]), x1);
+        unpack<T>(v8_bits<T>(qa[c + NC / 2]), x2);
+        rotate_math<T, 8>(x1, x2, cf, sf, o1, o2);
+        qa[c] = as_v8<T>(pack<T>(o1));
+        qa[c + NC / 2] = as_v8<T>(pack<T>(o2));
+      }
     }
-    vnew = ld16(vn + dc * 8);
-    // The workgroup of the last page writes the new rows to the pool slot.
-    if ((n_pages - 1) / a.pages_per_split == split) append_new_rows<T, DH, BS>(a, b, kvh);
+    // Wave-uniform: this wave holds the sequence's last page.
+    if (w_begin < w_end && w_end == n_pages) {
+      patch = stage_new_rows<T, KV, DH, BS>(a, b, kvh, lane, new_k_s, new_v_s);
+      wave_lds_sync();
+    }
   }
 
   const KV *kc = static_cast<const KV *>(a.kc) + a.pool.layer_base + (int64_t)kvh * a.pool.head_stride;
@@ -396,11 +484,12 @@ __global__ __launch_bounds__(64 * kWaves) void decode_mfma_kernel(DecodeArgs a) 
     if (patch && p == n_pages - 1) {
       if (r == new_off) {
 #pragma unroll
-        for (int c = 0; c < NC; ++c) kr[c] = krot[c];
+        for (int c = 0; c < NC; ++c)
+          kr[c] = load_chunk<T, KV>(new_k_s + (kSlab ? grp * NC * 8 + c * 8 : c * 32 + grp * 8));
       }
 #pragma unroll
       for (int j = 0; j < 4; ++j)
-        if (tg * 4 + j == new_off) vr[j] = vnew;
+        if (tg * 4 + j == new_off) vr[j] = load_chunk<T, KV>(new_v_s + dc * 8);
     }
   };
   auto consume = [&](auto check_end, const raw (&kr)[NC], raw (&vr)[4], int p) {
@@ -512,6 +601,11 @@ __global__ __launch_bounds__(64 * kWaves) void decode_mfma_kernel(DecodeArgs a) 
     }
   }
 
+  // The staged rows to the pool, once this wave has read the page that holds their slot.
+  if constexpr (ROPE) {
+    if (patch) write_staged_rows<T, KV, DH, BS>(a, b, kvh, lane, new_k_s, new_v_s);
+  }
+
   // Per-wave state: l summed over the 16 tokens, acc over the 4 token groups.
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
@@ -603,8 +697,13 @@ bool decode_mfma_supported(int32_t dtype, int32_t head_dim, int32_t group) {
 int32_t launch_decode_mfma(const DecodeArgs &a, int32_t dtype, int32_t num_seqs,
                            int32_t num_kv_heads, int32_t group, int32_t head_dim,
                            hipStream_t stream, bool fp8_pools) {
+  if (a.positions != nullptr && fp8_pools)
+    return dtype == TKS_BFLOAT16
+               ? launch_typed<bf16_t, fp8e4m3_t, true>(a, num_seqs, num_kv_heads, group,
+                                                       head_dim, stream)
+               : launch_typed<_Float16, fp8e4m3_t, true>(a, num_seqs, num_kv_heads, group,
+                                                         head_dim, stream);
   if (a.positions != nullptr) {
-    if (fp8_pools) return TKS_ERR_VALUE;
     return dtype == TKS_BFLOAT16
                ? launch_typed<bf16_t, bf16_t, true>(a, num_seqs, num_kv_heads, group, head_dim,
                                                     stream)

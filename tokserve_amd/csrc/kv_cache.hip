@@ -159,7 +159,7 @@ int32_t launch_gather(const void *key_cache, const void *value_cache, const Pool
 
 template <typename T, int E>
 __device__ __forceinline__ void quantize_chunk(const T *src, uint8_t *dst, float scale) {
-  float x[E], f[E];
+  float x[E];
   if constexpr (E == 16) {
     constexpr int N = Vec<T>::N;
 #pragma unroll
@@ -167,20 +167,7 @@ __device__ __forceinline__ void quantize_chunk(const T *src, uint8_t *dst, float
   } else {
     x[0] = to_float(src[0]);
   }
-#pragma unroll
-  for (int i = 0; i < E; ++i) f[i] = x[i] / scale;
-  if constexpr (E == 16) {
-    uint32_t w[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      w[i] = fp8x4_nan_sign(
-          float4_to_fp8x4(f[4 * i], f[4 * i + 1], f[4 * i + 2], f[4 * i + 3]), x + 4 * i);
-    st16(dst, make_uint4(w[0], w[1], w[2], w[3]));
-  } else {
-    const float x4[4] = {x[0], 0.f, 0.f, 0.f};
-    dst[0] = static_cast<uint8_t>(fp8x4_nan_sign(float4_to_fp8x4(f[0], 0.f, 0.f, 0.f), x4) &
-                                  0xffu);
-  }
+  encode_e4m3<E>(x, scale, dst);
 }
 
 template <typename T, int E>

@@ -566,22 +566,31 @@ int32_t decode_impl(const void *query, int64_t q_seq_stride, int64_t q_head_stri
                                   q_head_stride, key_cache, value_cache, out, out_seq_stride,
                                   out_head_stride);
   if (ra != nullptr) {
-    // Fused when the MFMA kernel runs with its rows in 16-byte chunks and keeps two
-    // waves per SIMD with the extra registers (all but Dh 128 with G 8); otherwise
+    // Fused when the MFMA kernel runs with its new rows in 16-byte chunks; otherwise
     // the RoPE + append launch writes the rotated queries into `out`, which the
     // decode then reads as its query (each workgroup reads its rows before it, or
     // the merge, writes them).
-    const bool fused = mfma && !fp8_pools && !(head_dim == 128 && G == 8) &&
+    const bool fused = mfma &&
                        aligned16(ra->key) && aligned16(ra->value) && aligned16(ra->cos_cache) &&
                        aligned16(ra->sin_cache) && ra->k_ss % 8 == 0 && ra->k_hs % 8 == 0 &&
                        ra->v_ss % 8 == 0 && ra->v_hs % 8 == 0;
     if (!fused) {
-      const int32_t st0 = tks_rope_kv_append(
-          query, out, q_seq_stride, q_head_stride, out_seq_stride, out_head_stride, num_q_heads,
-          ra->key, nullptr, ra->k_ss, ra->k_hs, 0, 0, ra->value, ra->v_ss, ra->v_hs,
-          num_kv_heads, num_seqs, head_dim, ra->positions, ra->cos_cache, ra->sin_cache,
-          ra->cache_len, const_cast<void *>(key_cache), const_cast<void *>(value_cache),
-          num_layers, num_blocks, block_size, layer_index, ra->slot_mapping, dtype, stream);
+      void *kc = const_cast<void *>(key_cache), *vc = const_cast<void *>(value_cache);
+      const int32_t st0 =
+          fp8_pools
+              ? tks_rope_kv_append_fp8(query, out, q_seq_stride, q_head_stride, out_seq_stride,
+                                       out_head_stride, num_q_heads, ra->key, nullptr, ra->k_ss,
+                                       ra->k_hs, 0, 0, ra->value, ra->v_ss, ra->v_hs,
+                                       num_kv_heads, num_seqs, head_dim, ra->positions,
+                                       ra->cos_cache, ra->sin_cache, ra->cache_len, kc, vc,
+                                       num_layers, num_blocks, block_size, layer_index,
+                                       ra->slot_mapping, k_scale, v_scale, dtype, stream)
+              : tks_rope_kv_append(query, out, q_seq_stride, q_head_stride, out_seq_stride,
+                                   out_head_stride, num_q_heads, ra->key, nullptr, ra->k_ss,
+                                   ra->k_hs, 0, 0, ra->value, ra->v_ss, ra->v_hs, num_kv_heads,
+                                   num_seqs, head_dim, ra->positions, ra->cos_cache,
+                                   ra->sin_cache, ra->cache_len, kc, vc, num_layers, num_blocks,
+                                   block_size, layer_index, ra->slot_mapping, dtype, stream);
       if (st0 != TKS_OK) return st0;
       return decode_impl(out, out_seq_stride, out_head_stride, key_cache, value_cache,
                          num_layers, num_blocks, num_kv_heads, block_size, head_dim, layer_index,
@@ -611,6 +620,7 @@ int32_t decode_impl(const void *query, int64_t q_seq_stride, int64_t q_head_stri
       a.vn_ss = ra->v_ss;
       a.vn_hs = ra->v_hs;
       a.slots = ra->slot_mapping;
+      a.k_scale = k_scale;
     }
     st = launch_decode_mfma(a, dtype, num_seqs, num_kv_heads, G, head_dim, s, fp8_pools);
   } else {
@@ -798,7 +808,9 @@ extern "C" int32_t tks_paged_attention_decode(
                      workspace_bytes, false, 1.f, 1.f, dtype, stream);
 }
 
-extern "C" int32_t tks_rope_append_paged_decode(
+namespace {
+
+int32_t rope_append_decode_entry(
     const void *query, int64_t q_seq_stride, int64_t q_head_stride, const void *key,
     int64_t k_seq_stride, int64_t k_head_stride, const void *value, int64_t v_seq_stride,
     int64_t v_head_stride, const int64_t *positions, const void *cos_cache,
@@ -808,7 +820,8 @@ extern "C" int32_t tks_rope_append_paged_decode(
     int32_t block_table_stride, const int32_t *seq_lens, const int32_t *seq_order,
     int32_t num_seqs, int32_t num_q_heads, int32_t max_seq_len, float scale,
     int32_t pages_per_split, void *out, int64_t out_seq_stride, int64_t out_head_stride,
-    void *workspace, int64_t workspace_bytes, int32_t dtype, tks_stream_t stream) {
+    void *workspace, int64_t workspace_bytes, bool fp8_pools, float k_scale, float v_scale,
+    int32_t dtype, tks_stream_t stream) {
   if (!valid_dtype(dtype)) return TKS_ERR_TYPE;
   if (head_dim < 2 || head_dim % 2 != 0 || cache_len <= 0 || num_seqs < 0) return TKS_ERR_VALUE;
   if (num_seqs > 0 && (!key || !value || !positions || !cos_cache || !sin_cache || !slot_mapping))
@@ -820,7 +833,50 @@ extern "C" int32_t tks_rope_append_paged_decode(
                      num_blocks, num_kv_heads, block_size, head_dim, layer_index, block_tables,
                      block_table_stride, seq_lens, seq_order, num_seqs, num_q_heads, max_seq_len,
                      scale, pages_per_split, out, out_seq_stride, out_head_stride, workspace,
-                     workspace_bytes, false, 1.f, 1.f, dtype, stream, &ra);
+                     workspace_bytes, fp8_pools, k_scale, v_scale, dtype, stream, &ra);
+}
+
+}  // namespace
+
+extern "C" int32_t tks_rope_append_paged_decode(
+    const void *query, int64_t q_seq_stride, int64_t q_head_stride, const void *key,
+    int64_t k_seq_stride, int64_t k_head_stride, const void *value, int64_t v_seq_stride,
+    int64_t v_head_stride, const int64_t *positions, const void *cos_cache,
+    const void *sin_cache, int64_t cache_len, const int64_t *slot_mapping, void *key_cache,
+    void *value_cache, int32_t num_layers, int64_t num_blocks, int32_t num_kv_heads,
+    int32_t block_size, int32_t head_dim, int32_t layer_index, const int32_t *block_tables,
+    int32_t block_table_stride, const int32_t *seq_lens, const int32_t *seq_order,
+    int32_t num_seqs, int32_t num_q_heads, int32_t max_seq_len, float scale,
+    int32_t pages_per_split, void *out, int64_t out_seq_stride, int64_t out_head_stride,
+    void *workspace, int64_t workspace_bytes, int32_t dtype, tks_stream_t stream) {
+  return rope_append_decode_entry(
+      query, q_seq_stride, q_head_stride, key, k_seq_stride, k_head_stride, value, v_seq_stride,
+      v_head_stride, positions, cos_cache, sin_cache, cache_len, slot_mapping, key_cache,
+      value_cache, num_layers, num_blocks, num_kv_heads, block_size, head_dim, layer_index,
+      block_tables, block_table_stride, seq_lens, seq_order, num_seqs, num_q_heads, max_seq_len,
+      scale, pages_per_split, out, out_seq_stride, out_head_stride, workspace, workspace_bytes,
+      false, 1.f, 1.f, dtype, stream);
+}
+
+extern "C" int32_t tks_rope_append_paged_decode_fp8(
+    const void *query, int64_t q_seq_stride, int64_t q_head_stride, const void *key,
+    int64_t k_seq_stride, int64_t k_head_stride, const void *value, int64_t v_seq_stride,
+    int64_t v_head_stride, const int64_t *positions, const void *cos_cache,
+    const void *sin_cache, int64_t cache_len, const int64_t *slot_mapping, void *key_cache,
+    void *value_cache, int32_t num_layers, int64_t num_blocks, int32_t num_kv_heads,
+    int32_t block_size, int32_t head_dim, int32_t layer_index, const int32_t *block_tables,
+    int32_t block_table_stride, const int32_t *seq_lens, const int32_t *seq_order,
+    int32_t num_seqs, int32_t num_q_heads, int32_t max_seq_len, float scale,
+    int32_t pages_per_split, void *out, int64_t out_seq_stride, int64_t out_head_stride,
+    void *workspace, int64_t workspace_bytes, float k_scale, float v_scale, int32_t dtype,
+    tks_stream_t stream) {
+  return rope_append_decode_entry(
+      query, q_seq_stride, q_head_stride, key, k_seq_stride, k_head_stride, value, v_seq_stride,
+      v_head_stride, positions, cos_cache, sin_cache, cache_len, slot_mapping, key_cache,
+      value_cache, num_layers, num_blocks, num_kv_heads, block_size, head_dim, layer_index,
+      block_tables, block_table_stride, seq_lens, seq_order, num_seqs, num_q_heads, max_seq_len,
+      scale, pages_per_split, out, out_seq_stride, out_head_stride, workspace, workspace_bytes,
+      true, k_scale, v_scale, dtype, stream);
 }
 
 extern "C" int32_t tks_paged_attention_decode_fp8(

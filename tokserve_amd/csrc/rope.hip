@@ -91,9 +91,10 @@ struct AppendView {
   int64_t layer_base, block_stride, head_stride, num_slots;
   int32_t block_size;
   const int64_t *slots;
+  float k_scale, v_scale;  // e4m3 pools: the codes hold value / scale
 };
 
-template <typename T, int V>
+template <typename T, int V, typename P>
 __global__ __launch_bounds__(kAppendThreads) void rope_append_kernel(
     RopeTensor q, RopeTensor k, AppendView a, const int64_t *__restrict__ positions,
     const T *__restrict__ cos_cache, const T *__restrict__ sin_cache, int64_t cache_len,
@@ -112,8 +113,8 @@ __global__ __launch_bounds__(kAppendThreads) void rope_append_kernel(
     const int64_t block = slot / a.block_size;
     row = a.layer_base + block * a.block_stride + (slot - block * a.block_size) * head_dim;
   }
-  T *kc = static_cast<T *>(a.kc);
-  T *vc = static_cast<T *>(a.vc);
+  P *kc = static_cast<P *>(a.kc);
+  P *vc = static_cast<P *>(a.vc);
   const int rot_items = (q.heads + k.heads) * chunks;
   const int v_chunks = head_dim / V;
   const int items = rot_items + (keep ? k.heads * v_chunks : 0);
@@ -123,12 +124,21 @@ __global__ __launch_bounds__(kAppendThreads) void rope_append_kernel(
       const int h = j / v_chunks;
       const int c = (j - h * v_chunks) * V;
       const T *src = static_cast<const T *>(a.v) + t * a.v_ts + h * a.v_hs + c;
-      T *dst = vc + row + h * a.head_stride + c;
-      if constexpr (V * sizeof(T) == 16) {
+      P *dst = vc + row + h * a.head_stride + c;
+      if constexpr (sizeof(P) != 1 && V * sizeof(T) == 16) {
         st16(dst, ld16(src));
-      } else {
+      } else if constexpr (sizeof(P) != 1) {
 #pragma unroll
         for (int e = 0; e < V; ++e) dst[e] = src[e];
+      } else {
+        float x[V];
+        if constexpr (V * sizeof(T) == 16) {
+          unpack<T>(ld16(src), x);
+        } else {
+#pragma unroll
+          for (int e = 0; e < V; ++e) x[e] = to_float(src[e]);
+        }
+        encode_e4m3<V>(x, a.v_scale, reinterpret_cast<uint8_t *>(dst));
       }
       continue;
     }
@@ -146,7 +156,22 @@ __global__ __launch_bounds__(kAppendThreads) void rope_append_kernel(
       rotate_values<T, V>(src, cf, sf, half, o1, o2);
       if (k.out != nullptr)
         store_pair<T, V>(static_cast<T *>(k.out) + hh * k.osh + t * k.ost + c, o1, o2, half);
-      if (keep) store_pair<T, V>(kc + row + hh * a.head_stride + c, o1, o2, half);
+      if (keep) {
+        if constexpr (sizeof(P) == 1) {
+          // The rotated row at the model dtype's precision, as the two-step path
+          // stores it before the quantizing append reads it.
+#pragma unroll
+          for (int e = 0; e < V; ++e) {
+            o1[e] = round_through<T>(o1[e]);
+            o2[e] = round_through<T>(o2[e]);
+          }
+          P *dst = kc + row + hh * a.head_stride + c;
+          encode_e4m3<V>(o1, a.k_scale, reinterpret_cast<uint8_t *>(dst));
+          encode_e4m3<V>(o2, a.k_scale, reinterpret_cast<uint8_t *>(dst + half));
+        } else {
+          store_pair<T, V>(kc + row + hh * a.head_stride + c, o1, o2, half);
+        }
+      }
     }
   }
 }
@@ -212,17 +237,21 @@ extern "C" int32_t tks_rope(const void *query, void *query_out, int64_t q_sb, in
   }
 }
 
-extern "C" int32_t tks_rope_kv_append(
+namespace {
+
+int32_t rope_kv_append_impl(
     const void *query, void *query_out, int64_t q_ts, int64_t q_hs, int64_t qo_ts,
     int64_t qo_hs, int32_t num_q_heads, const void *key, void *key_out, int64_t k_ts,
     int64_t k_hs, int64_t ko_ts, int64_t ko_hs, const void *value, int64_t v_ts, int64_t v_hs,
     int32_t num_kv_heads, int64_t num_tokens, int32_t head_dim, const int64_t *positions,
     const void *cos_cache, const void *sin_cache, int64_t cache_len, void *key_cache,
     void *value_cache, int32_t num_layers, int64_t num_blocks, int32_t block_size,
-    int32_t layer_index, const int64_t *slot_mapping, int32_t dtype, tks_stream_t stream) {
+    int32_t layer_index, const int64_t *slot_mapping, bool fp8_pools, float k_scale,
+    float v_scale, int32_t dtype, tks_stream_t stream) {
   if (!valid_dtype(dtype)) return TKS_ERR_TYPE;
   if (head_dim < 2 || head_dim % 2 != 0 || num_q_heads < 0 || num_kv_heads <= 0 ||
-      num_tokens < 0 || cache_len <= 0 || num_layers <= 0 || num_blocks <= 0 || block_size <= 0)
+      num_tokens < 0 || cache_len <= 0 || num_layers <= 0 || num_blocks <= 0 || block_size <= 0 ||
+      !valid_scale(k_scale) || !valid_scale(v_scale))
     return TKS_ERR_VALUE;
   if (layer_index < 0 || layer_index >= num_layers) return TKS_ERR_INDEX;
   if (num_tokens == 0) return TKS_OK;
@@ -244,8 +273,14 @@ extern "C" int32_t tks_rope_kv_append(
   a.num_slots = num_blocks * block_size;
   a.block_size = block_size;
   a.slots = slot_mapping;
+  a.k_scale = k_scale;
+  a.v_scale = v_scale;
   hipStream_t s = static_cast<hipStream_t>(stream);
   const dim3 grid(static_cast<unsigned>(num_tokens));
+#define TKS_ROPE_APPEND_POOL(TYPE, VV, POOL)                                                     \
+  rope_append_kernel<TYPE, VV, POOL><<<grid, kAppendThreads, 0, s>>>(                           \
+      q, k, a, positions, static_cast<const TYPE *>(cos_cache),                                 \
+      static_cast<const TYPE *>(sin_cache), cache_len, head_dim)
 #define TKS_ROPE_APPEND(TYPE)                                                                  \
   {                                                                                            \
     constexpr int V = Vec<TYPE>::N;                                                            \
@@ -255,14 +290,16 @@ extern "C" int32_t tks_rope_kv_append(
                      (num_q_heads == 0 || strides_ok(q, V)) && strides_ok(kk, V) &&             \
                      v_ts % V == 0 && v_hs % V == 0 && aligned16(value) &&                      \
                      aligned16(key_cache) && aligned16(value_cache);                            \
-    if (vec)                                                                                   \
-      rope_append_kernel<TYPE, V><<<grid, kAppendThreads, 0, s>>>(                             \
-          q, k, a, positions, static_cast<const TYPE *>(cos_cache),                            \
-          static_cast<const TYPE *>(sin_cache), cache_len, head_dim);                          \
-    else                                                                                       \
-      rope_append_kernel<TYPE, 1><<<grid, kAppendThreads, 0, s>>>(                             \
-          q, k, a, positions, static_cast<const TYPE *>(cos_cache),                            \
-          static_cast<const TYPE *>(sin_cache), cache_len, head_dim);                          \
+    if (fp8_pools) {                                                                           \
+      if (vec)                                                                                 \
+        TKS_ROPE_APPEND_POOL(TYPE, V, fp8e4m3_t);                                              \
+      else                                                                                     \
+        TKS_ROPE_APPEND_POOL(TYPE, 1, fp8e4m3_t);                                              \
+    } else if (vec) {                                                                          \
+      TKS_ROPE_APPEND_POOL(TYPE, V, TYPE);                                                     \
+    } else {                                                                                   \
+      TKS_ROPE_APPEND_POOL(TYPE, 1, TYPE);                                                     \
+    }                                                                                          \
   }
   switch (dtype) {
     case TKS_FLOAT32: TKS_ROPE_APPEND(float); break;
@@ -270,5 +307,39 @@ extern "C" int32_t tks_rope_kv_append(
     default: TKS_ROPE_APPEND(bf16_t); break;
   }
 #undef TKS_ROPE_APPEND
+#undef TKS_ROPE_APPEND_POOL
   return check_launch();
+}
+
+}  // namespace
+
+extern "C" int32_t tks_rope_kv_append(
+    const void *query, void *query_out, int64_t q_ts, int64_t q_hs, int64_t qo_ts,
+    int64_t qo_hs, int32_t num_q_heads, const void *key, void *key_out, int64_t k_ts,
+    int64_t k_hs, int64_t ko_ts, int64_t ko_hs, const void *value, int64_t v_ts, int64_t v_hs,
+    int32_t num_kv_heads, int64_t num_tokens, int32_t head_dim, const int64_t *positions,
+    const void *cos_cache, const void *sin_cache, int64_t cache_len, void *key_cache,
+    void *value_cache, int32_t num_layers, int64_t num_blocks, int32_t block_size,
+    int32_t layer_index, const int64_t *slot_mapping, int32_t dtype, tks_stream_t stream) {
+  return rope_kv_append_impl(query, query_out, q_ts, q_hs, qo_ts, qo_hs, num_q_heads, key,
+                             key_out, k_ts, k_hs, ko_ts, ko_hs, value, v_ts, v_hs, num_kv_heads,
+                             num_tokens, head_dim, positions, cos_cache, sin_cache, cache_len,
+                             key_cache, value_cache, num_layers, num_blocks, block_size,
+                             layer_index, slot_mapping, false, 1.f, 1.f, dtype, stream);
+}
+
+extern "C" int32_t tks_rope_kv_append_fp8(
+    const void *query, void *query_out, int64_t q_ts, int64_t q_hs, int64_t qo_ts,
+    int64_t qo_hs, int32_t num_q_heads, const void *key, void *key_out, int64_t k_ts,
+    int64_t k_hs, int64_t ko_ts, int64_t ko_hs, const void *value, int64_t v_ts, int64_t v_hs,
+    int32_t num_kv_heads, int64_t num_tokens, int32_t head_dim, const int64_t *positions,
+    const void *cos_cache, const void *sin_cache, int64_t cache_len, void *key_cache,
+    void *value_cache, int32_t num_layers, int64_t num_blocks, int32_t block_size,
+    int32_t layer_index, const int64_t *slot_mapping, float k_scale, float v_scale,
+    int32_t dtype, tks_stream_t stream) {
+  return rope_kv_append_impl(query, query_out, q_ts, q_hs, qo_ts, qo_hs, num_q_heads, key,
+                             key_out, k_ts, k_hs, ko_ts, ko_hs, value, v_ts, v_hs, num_kv_heads,
+                             num_tokens, head_dim, positions, cos_cache, sin_cache, cache_len,
+                             key_cache, value_cache, num_layers, num_blocks, block_size,
+                             layer_index, slot_mapping, true, k_scale, v_scale, dtype, stream);
 }

@@ -130,28 +130,22 @@ class GroupedQueryAttention(nn.Module):
         key = qkv[:, hq * dh : (hq + hkv) * dh].view(tokens, hkv, dh)
         value = qkv[:, (hq + hkv) * dh :].view(tokens, hkv, dh)
         split = batch.num_prefill_tokens
-        if split == 0 and not ops.is_fp8_pool(storage.key_storage):
+        if layer_index < 0 or layer_index >= storage.num_layers:
+            raise IndexError("layer_index is out of range")
+        if split == 0:
             # Decode-only iteration: RoPE, the KV append and the attention in one call.
-            if layer_index < 0 or layer_index >= storage.num_layers:
-                raise IndexError("layer_index is out of range")
             attended = ops.rope_append_paged_decode(
                 query, key, value, batch.positions, rotary, storage.key_storage,
                 storage.value_storage, batch.slot_mapping, batch.decode_block_tables,
                 batch.decode_seq_lens, layer_index=layer_index,
-                max_seq_len=batch.decode_max_seq_len, seq_order=batch.decode_seq_order)
+                max_seq_len=batch.decode_max_seq_len, seq_order=batch.decode_seq_order,
+                **storage.scales)
             return self.o_proj(attended.view(tokens, self.hidden_size))
-        if ops.is_fp8_pool(storage.key_storage):
-            # In-place rotation of the packed (1, H, N, Dh) views, then the quantizing append.
-            q4 = query.transpose(0, 1).unsqueeze(0)
-            k4 = key.transpose(0, 1).unsqueeze(0)
-            ops.rope(q4, k4, batch.positions, rotary, query_out=q4, key_out=k4)
-            storage.write_slots(layer_index, batch.slot_mapping, key, value)
-        else:
-            # Q rotated in place; rotated K and V go straight to the pool slots.
-            if layer_index < 0 or layer_index >= storage.num_layers:
-                raise IndexError("layer_index is out of range")
-            ops.rope_kv_append(query, key, value, batch.positions, rotary, storage.key_storage,
-                               storage.value_storage, batch.slot_mapping, layer_index)
+        # Q rotated in place; rotated K and V go straight to the pool slots (quantized
+        # with the pool scales over fp8 pools).
+        ops.rope_kv_append(query, key, value, batch.positions, rotary, storage.key_storage,
+                           storage.value_storage, batch.slot_mapping, layer_index,
+                           **storage.scales)
         attended = torch.empty((tokens, hq, dh), dtype=inputs.dtype, device=inputs.device)
         if split > 0:
             ops.paged_attention_prefill(

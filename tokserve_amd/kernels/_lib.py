@@ -15,7 +15,7 @@ from pathlib import Path
 import torch
 
 LIBRARY_NAME = "libtokserve_hip.so"
-ABI_VERSION = 9
+ABI_VERSION = 10
 
 TKS_OK = 0
 TKS_ERR_VALUE = -1
@@ -65,6 +65,14 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
          _c_void_p, _i32, _c_void_p, _c_void_p, _i32, _i32, _i32, _f32, _i32,
          _c_void_p, _i64, _i64, _c_void_p, _i64, _i32, _c_void_p],
     ),
+    "tks_rope_append_paged_decode_fp8": (
+        _i32,
+        [_c_void_p, _i64, _i64, _c_void_p, _i64, _i64, _c_void_p, _i64, _i64,
+         _c_void_p, _c_void_p, _c_void_p, _i64, _c_void_p,
+         _c_void_p, _c_void_p, _i32, _i64, _i32, _i32, _i32, _i32,
+         _c_void_p, _i32, _c_void_p, _c_void_p, _i32, _i32, _i32, _f32, _i32,
+         _c_void_p, _i64, _i64, _c_void_p, _i64, _f32, _f32, _i32, _c_void_p],
+    ),
     "tks_paged_attention_decode_noalloc_max_workspace_bytes": (_i64, []),
     "tks_paged_attention_decode_noalloc": (
         _i32,
@@ -96,6 +104,14 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
          _c_void_p, _c_void_p, _i64, _i64, _i64, _i64,
          _c_void_p, _i64, _i64, _i32, _i64, _i32, _c_void_p, _c_void_p, _c_void_p, _i64,
          _c_void_p, _c_void_p, _i32, _i64, _i32, _i32, _c_void_p, _i32, _c_void_p],
+    ),
+    "tks_rope_kv_append_fp8": (
+        _i32,
+        [_c_void_p, _c_void_p, _i64, _i64, _i64, _i64, _i32,
+         _c_void_p, _c_void_p, _i64, _i64, _i64, _i64,
+         _c_void_p, _i64, _i64, _i32, _i64, _i32, _c_void_p, _c_void_p, _c_void_p, _i64,
+         _c_void_p, _c_void_p, _i32, _i64, _i32, _i32, _c_void_p, _f32, _f32, _i32,
+         _c_void_p],
     ),
     "tks_vector_add": (_i32, [_c_void_p, _c_void_p, _c_void_p, _i64, _i32, _c_void_p]),
     "tks_silu_mul": (_i32, [_c_void_p, _i64, _i64, _i64, _c_void_p, _i64, _i32, _c_void_p]),

@@ -510,13 +510,15 @@ def rope_kv_append(
     *,
     query_out: torch.Tensor | None = None,
     key_out: torch.Tensor | None = None,
+    k_scale: float = 1.0,
+    v_scale: float = 1.0,
 ) -> torch.Tensor:
     """Packed step: rotate query (N, Hq, Dh) into query_out (in place by default), rotate
     key (N, Hkv, Dh) and append it with value (N, Hkv, Dh) to the pools at slot_mapping.
 
     One launch, bit-identical to rope() followed by kv_append() of the rotated keys.
-    key_out, when given, also receives the rotated keys. Pools in the rows' dtype
-    (fp8 pools take rope() and kv_append() separately).
+    key_out, when given, also receives the rotated keys. Pools in the rows' dtype, or
+    fp8 pools quantized with k_scale / v_scale as kv_append() does.
     """
 
     require_hip("rope_kv_append", query, key, value, positions, key_cache, value_cache,
@@ -529,7 +531,9 @@ def rope_kv_append(
     tokens = query.shape[0]
     if key.shape != (tokens, num_kv_heads, head_dim) or query.shape[2] != head_dim:
         raise ValueError("key and value rows must match the pool's (Hkv, Dh)")
-    if len({query.dtype, key.dtype, value.dtype, key_cache.dtype, table.dtype}) != 1:
+    k_scale, v_scale = _pool_scales(key_cache, k_scale, v_scale)
+    pool_dtype = query.dtype if is_fp8_pool(key_cache) else key_cache.dtype
+    if len({query.dtype, key.dtype, value.dtype, pool_dtype, table.dtype}) != 1:
         raise ValueError("query, key, value, pools and the rotary table must share a dtype")
     if head_dim != table.head_dim:
         raise ValueError("head_dim must match the rotary table")
@@ -549,10 +553,10 @@ def rope_kv_append(
         raise ValueError("key_out must match key and be contiguous in head_dim")
     if query_out is query:
         _ops.rope_kv_append_(query, key, value, pos, table.cos, table.sin, key_cache,
-                             value_cache, slots, layer_index, key_out)
+                             value_cache, slots, layer_index, key_out, k_scale, v_scale)
     else:
         _ops.rope_kv_append(query, key, value, pos, table.cos, table.sin, key_cache, value_cache,
-                            slots, layer_index, query_out, key_out)
+                            slots, layer_index, query_out, key_out, k_scale, v_scale)
     return query_out
 
 
@@ -575,6 +579,8 @@ def rope_append_paged_decode(
     workspace: torch.Tensor | None = None,
     pages_per_split: int = 0,
     seq_order: torch.Tensor | None = None,
+    k_scale: float = 1.0,
+    v_scale: float = 1.0,
 ) -> torch.Tensor:
     """A decode step's RoPE, KV append and attention in one call: query (B, Hq, Dh) is
     rotated at positions (B,) (read only), the rotated key and the value rows (B, Hkv, Dh)
@@ -582,7 +588,8 @@ def rope_append_paged_decode(
     out (B, Hq, Dh) receives the attention over seq_lens[b] keys.
 
     Bit-identical to rope_kv_append() followed by paged_attention_decode() with the
-    same arguments (one launch on the MFMA decode kernel). Pools in the rows' dtype.
+    same arguments (one launch on the MFMA decode kernel). Pools in the rows' dtype, or
+    fp8 pools with their scales.
     """
 
     require_hip("rope_append_paged_decode", query, key, value, positions, key_cache,
@@ -590,14 +597,14 @@ def rope_append_paged_decode(
     num_layers, num_blocks, num_kv_heads, block_size, head_dim = _pool_shape(
         key_cache, value_cache
     )
-    if is_fp8_pool(key_cache):
-        raise ValueError("rope_append_paged_decode needs pools in the rows' dtype")
+    k_scale, v_scale = _pool_scales(key_cache, k_scale, v_scale)
     if query.ndim != 3 or key.ndim != 3 or value.shape != key.shape:
         raise ValueError("query (B, Hq, Dh), key and value (B, Hkv, Dh) expected")
     num_seqs, num_q_heads, _ = query.shape
     if key.shape != (num_seqs, num_kv_heads, head_dim) or query.shape[2] != head_dim:
         raise ValueError("key and value rows must match the pool's (Hkv, Dh)")
-    if len({query.dtype, key.dtype, value.dtype, key_cache.dtype, table.dtype}) != 1:
+    pool_dtype = query.dtype if is_fp8_pool(key_cache) else key_cache.dtype
+    if len({query.dtype, key.dtype, value.dtype, pool_dtype, table.dtype}) != 1:
         raise ValueError("query, key, value, pools and the rotary table must share a dtype")
     if head_dim != table.head_dim:
         raise ValueError("head_dim must match the rotary table")
@@ -628,7 +635,7 @@ def rope_append_paged_decode(
             raise ValueError("seq_order must have shape (B,)")
     _ops.rope_append_paged_decode(query, key, value, pos, table.cos, table.sin, slots, key_cache,
                                   value_cache, tables, lens, order, layer_index, max_seq_len,
-                                  float(scale), pages_per_split, out, workspace)
+                                  float(scale), pages_per_split, out, workspace, k_scale, v_scale)
     return out
 
 

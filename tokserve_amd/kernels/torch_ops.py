@@ -84,19 +84,21 @@ SCHEMAS = {
     "rope_kv_append": (
         "rope_kv_append(Tensor query, Tensor key, Tensor value, Tensor positions, Tensor cos, "
         "Tensor sin, Tensor(a!) key_cache, Tensor(b!) value_cache, Tensor slot_mapping, "
-        "int layer_index, Tensor(c!) query_out, Tensor(d!)? key_out) -> ()"
+        "int layer_index, Tensor(c!) query_out, Tensor(d!)? key_out, float k_scale=1.0, "
+        "float v_scale=1.0) -> ()"
     ),
     "rope_kv_append_": (
         "rope_kv_append_(Tensor(a!) query, Tensor key, Tensor value, Tensor positions, "
         "Tensor cos, Tensor sin, Tensor(b!) key_cache, Tensor(c!) value_cache, "
-        "Tensor slot_mapping, int layer_index, Tensor(d!)? key_out) -> ()"
+        "Tensor slot_mapping, int layer_index, Tensor(d!)? key_out, float k_scale=1.0, "
+        "float v_scale=1.0) -> ()"
     ),
     "rope_append_paged_decode": (
         "rope_append_paged_decode(Tensor query, Tensor key, Tensor value, Tensor positions, "
         "Tensor cos, Tensor sin, Tensor slot_mapping, Tensor(a!) key_cache, "
         "Tensor(b!) value_cache, Tensor block_tables, Tensor seq_lens, Tensor? seq_order, "
         "int layer_index, int max_seq_len, float scale, int pages_per_split, Tensor(c!) out, "
-        "Tensor(d!)? workspace) -> ()"
+        "Tensor(d!)? workspace, float k_scale=1.0, float v_scale=1.0) -> ()"
     ),
     "greedy_argmax": "greedy_argmax(Tensor logits, Tensor(a!) out) -> ()",
     "silu_mul": "silu_mul(Tensor gate_up, Tensor(a!) out) -> ()",
@@ -117,9 +119,10 @@ ENTRY_POINTS = {
     "rms_norm": ("tks_rms_norm",),
     "rope": ("tks_rope",),
     "rope_": ("tks_rope",),
-    "rope_kv_append": ("tks_rope_kv_append",),
-    "rope_kv_append_": ("tks_rope_kv_append",),
+    "rope_kv_append": ("tks_rope_kv_append", "tks_rope_kv_append_fp8"),
+    "rope_kv_append_": ("tks_rope_kv_append", "tks_rope_kv_append_fp8"),
     "rope_append_paged_decode": ("tks_rope_append_paged_decode",
+                                 "tks_rope_append_paged_decode_fp8",
                                  "tks_paged_attention_decode_workspace_bytes"),
     "greedy_argmax": ("tks_argmax",),
     "silu_mul": ("tks_silu_mul",),
@@ -304,9 +307,13 @@ def _rope_inplace(query, key, positions, cos, sin):
 
 
 def _rope_kv_append_launch(query, query_out, key, value, positions, cos, sin, key_cache,
-                           value_cache, slot_mapping, layer_index, key_out):
+                           value_cache, slot_mapping, layer_index, key_out, k_scale, v_scale):
     num_layers, num_blocks, num_kv_heads, block_size, head_dim = _pool_dims(key_cache)
-    status = _lib.load().tks_rope_kv_append(
+    library = _lib.load()
+    fp8 = key_cache.dtype == FP8_POOL_DTYPE
+    scales = (k_scale, v_scale) if fp8 else ()
+    entry = library.tks_rope_kv_append_fp8 if fp8 else library.tks_rope_kv_append
+    status = entry(
         query.data_ptr(), query_out.data_ptr(), query.stride(0), query.stride(1),
         query_out.stride(0), query_out.stride(1), query.shape[1],
         key.data_ptr(), _lib.ptr(key_out), key.stride(0), key.stride(1),
@@ -314,31 +321,37 @@ def _rope_kv_append_launch(query, query_out, key, value, positions, cos, sin, ke
         value.data_ptr(), value.stride(0), value.stride(1), num_kv_heads, query.shape[0],
         head_dim, positions.data_ptr(), cos.data_ptr(), sin.data_ptr(), cos.shape[0],
         key_cache.data_ptr(), value_cache.data_ptr(), num_layers, num_blocks, block_size,
-        layer_index, slot_mapping.data_ptr(), _code(query), _stream(query))
+        layer_index, slot_mapping.data_ptr(), *scales, _code(query), _stream(query))
     _lib.check(status, "rope_kv_append")
 
 
 def _rope_kv_append(query, key, value, positions, cos, sin, key_cache, value_cache,
-                    slot_mapping, layer_index, query_out, key_out):
+                    slot_mapping, layer_index, query_out, key_out, k_scale=1.0, v_scale=1.0):
     _rope_kv_append_launch(query, query_out, key, value, positions, cos, sin, key_cache,
-                           value_cache, slot_mapping, layer_index, key_out)
+                           value_cache, slot_mapping, layer_index, key_out, k_scale, v_scale)
 
 
 def _rope_kv_append_inplace(query, key, value, positions, cos, sin, key_cache, value_cache,
-                            slot_mapping, layer_index, key_out):
+                            slot_mapping, layer_index, key_out, k_scale=1.0, v_scale=1.0):
     _rope_kv_append_launch(query, query, key, value, positions, cos, sin, key_cache,
-                           value_cache, slot_mapping, layer_index, key_out)
+                           value_cache, slot_mapping, layer_index, key_out, k_scale, v_scale)
 
 
 def _rope_append_paged_decode(query, key, value, positions, cos, sin, slot_mapping, key_cache,
                               value_cache, block_tables, seq_lens, seq_order, layer_index,
-                              max_seq_len, scale, pages_per_split, out, workspace_tensor):
+                              max_seq_len, scale, pages_per_split, out, workspace_tensor,
+                              k_scale=1.0, v_scale=1.0):
     num_layers, num_blocks, num_kv_heads, block_size, head_dim = _pool_dims(key_cache)
     if workspace_tensor is None:
         nbytes = decode_workspace_bytes(query.shape[0], query.shape[1], num_kv_heads, head_dim,
                                         block_size, max_seq_len, pages_per_split)
         workspace_tensor = workspace(query.device, nbytes, "decode")
-    status = _lib.load().tks_rope_append_paged_decode(
+    library = _lib.load()
+    fp8 = key_cache.dtype == FP8_POOL_DTYPE
+    scales = (k_scale, v_scale) if fp8 else ()
+    entry = (library.tks_rope_append_paged_decode_fp8 if fp8
+             else library.tks_rope_append_paged_decode)
+    status = entry(
         query.data_ptr(), query.stride(0), query.stride(1),
         key.data_ptr(), key.stride(0), key.stride(1),
         value.data_ptr(), value.stride(0), value.stride(1),
@@ -349,7 +362,7 @@ def _rope_append_paged_decode(query, key, value, positions, cos, sin, slot_mappi
         query.shape[0], query.shape[1], max_seq_len, scale, pages_per_split,
         out.data_ptr(), out.stride(0), out.stride(1),
         _lib.ptr(workspace_tensor), 0 if workspace_tensor is None else workspace_tensor.numel(),
-        _code(query), _stream(query))
+        *scales, _code(query), _stream(query))
     _lib.check(status, "rope_append_paged_decode")
 
 
