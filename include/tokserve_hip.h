@@ -157,11 +157,12 @@ int32_t tks_paged_attention_decode(const void *query, int64_t q_seq_stride, int6
  *     (a negative slot appends nothing);
  *   - out receives the attention of the rotated query over keys 0..seq_lens[b]-1,
  *     as tks_paged_attention_decode computes it (same workspace rule).
- * Results are bit-identical to the two calls. For bf16/fp16 pools on the MFMA
- * decode kernel the query is rotated in registers and the new rows are written and
- * used by the workgroup that reads the sequence's last page: one launch (plus the
- * split merge). Other shapes run the two calls, with the rotated queries staged
- * in `out`.
+ * Results are bit-identical to the two calls. On the MFMA decode kernel (bf16/fp16
+ * rows in 16-byte chunks) this is one launch (plus the split merge): each
+ * workgroup rotates its query rows as it loads them, and the wave that reads the
+ * sequence's last page uses the new rows in place of what it loads of their slot,
+ * then writes them to the pool. Other shapes run the two calls, with the rotated
+ * queries staged in `out`.
  */
 int32_t tks_rope_append_paged_decode(
     const void *query, int64_t q_seq_stride, int64_t q_head_stride, const void *key,

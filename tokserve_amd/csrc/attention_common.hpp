@@ -160,8 +160,8 @@ struct DecodeArgs {
   // RoPE + KV append fused into the decode (launch_decode_mfma with rope = true):
   // sequence b's query is rotated in registers at positions[b] (q itself is not
   // written); its new key row (rotated) and value row go to pool slot slots[b]
-  // (negative: none), written by the workgroup that reads the sequence's last page
-  // (over e4m3 pools quantized with k_scale and v_scale).
+  // (negative: none), written by the wave that reads the sequence's last page (over
+  // e4m3 pools quantized with k_scale and v_scale).
   const int64_t *positions = nullptr;
   const void *cos_t = nullptr, *sin_t = nullptr;  // [table_len, Dh / 2] in the model dtype
   int64_t table_len = 0;

@@ -303,10 +303,10 @@ __device__ __forceinline__ void write_staged_rows(const DecodeArgs &a, int b, in
 }
 
 // ROPE: RoPE and the KV append of the sequence's new token fused in (DecodeArgs).
-// Every workgroup rotates its query rows in registers; the new key row is rotated
-// and the value row copied to the pool by the workgroup that reads the sequence's
-// last page, which also substitutes both rows for what it loads of that page, so
-// no workgroup reads pool memory written in the same launch.
+// Every workgroup rotates its query rows as it loads them; the wave that reads the
+// sequence's last page stages the rotated key row and the value row in LDS, uses
+// them in place of what it loads of their slot and writes them to the pool after
+// its page loop, so no workgroup reads pool memory written in the same launch.
 template <typename T, typename KV, int DH, int G, bool ROPE>
 __global__ __launch_bounds__(64 * kWaves) void decode_mfma_kernel(DecodeArgs a) {
   using S = DecodeShape<DH, G>;
