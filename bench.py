@@ -660,6 +660,38 @@ def measure_decode_serving_shape(device, seed: int, steps: int, warmup: int) -> 
     ms_eager = _time_ms(step, steps, warmup)
     ms = _graph_ms(step, warmup)
     nbytes = algorithmic_bytes(batch)
+
+    # The engine's decode layer: RoPE of the new query and key, the append of the new
+    # K/V rows at position len - 1, and the attention, as one fused call and as the
+    # RoPE + append launch followed by the decode.
+    n, hq, hkv, dh = len(contexts), 32, 4, 64
+    gen = torch.Generator(device=device).manual_seed(seed + 7)
+    qkv = torch.randn(n, (hq + 2 * hkv) * dh, generator=gen, device=device).to(torch.bfloat16)
+    query = qkv[:, : hq * dh].view(n, hq, dh)
+    key = qkv[:, hq * dh : (hq + hkv) * dh].view(n, hkv, dh)
+    value = qkv[:, (hq + hkv) * dh :].view(n, hkv, dh)
+    pos = batch.seq_lens.to(torch.int64) - 1
+    tables = batch.block_tables.to(torch.int64)
+    slots = tables[torch.arange(n, device=device), pos // 16] * 16 + pos % 16
+    table = ops.RotaryTable(dh, theta=10_000.0, max_position=2048, dtype=torch.bfloat16,
+                            device=device)
+    rotated = torch.empty_like(query)
+
+    def fused() -> None:
+        ops.rope_append_paged_decode(
+            query, key, value, pos, table, batch.key_cache, batch.value_cache, slots,
+            batch.block_tables, batch.seq_lens, layer_index=0, max_seq_len=batch.max_seq_len,
+            out=out, seq_order=order)
+
+    def two_launches() -> None:
+        ops.rope_kv_append(query, key, value, pos, table, batch.key_cache, batch.value_cache,
+                           slots, 0, query_out=rotated)
+        ops.paged_attention_decode(
+            rotated, batch.key_cache, batch.value_cache, batch.block_tables, batch.seq_lens,
+            layer_index=0, max_seq_len=batch.max_seq_len, out=out, seq_order=order)
+
+    ms_fused = _graph_ms(fused, warmup)
+    ms_two = _graph_ms(two_launches, warmup)
     return {
         "workload": "decode at the e2e serving shape: 128 seqs, ctx = prompt U[64,1024] + 64, "
                     "Hq 32 / Hkv 4, Dh 64, block 16, bf16",
@@ -669,6 +701,11 @@ def measure_decode_serving_shape(device, seed: int, steps: int, warmup: int) -> 
         "ms_per_step_eager": round(ms_eager, 5),
         "algorithmic_bytes": nbytes,
         "gbps": round(nbytes / (ms * 1e-3) / 1e9, 1),
+        "rope_append_decode": {
+            "note": "a decode layer's RoPE + KV append + attention, HIP graph of 20 launches",
+            "fused_ms": round(ms_fused, 5),
+            "rope_kv_append_then_decode_ms": round(ms_two, 5),
+        },
     }
 
 
