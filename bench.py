@@ -758,10 +758,11 @@ def measure_decode_small_batches(device, seed: int, steps: int, warmup: int) -> 
 
 def measure_small_fp32_step(device, steps: int, warmup: int) -> dict:
     """The CPU-runnable fp32 decode step (8 sequences, contexts U[16, 512] + 1, 8/2 heads,
-    Dh 64, block 16, 512-block pool): RMSNorm (hidden 512, eps 1e-5), RoPE (theta 1e4) of
-    the new Q/K at each sequence's next position with the KV append through slot_mapping
-    in the same launch (as the model layer runs them), split-K decode attention.
-    Launch-bound: reported in microseconds, eager and as a HIP graph."""
+    Dh 64, block 16, 512-block pool): RMSNorm (hidden 512, eps 1e-5), then RoPE (theta 1e4)
+    of the new Q/K at each sequence's last position, the KV append through slot_mapping and
+    split-K decode attention in one call (as the model layer runs them; also timed as the
+    RoPE + append launch followed by the decode). Launch-bound: reported in microseconds,
+    eager and as a HIP graph."""
 
     import torch
 
@@ -785,22 +786,35 @@ def measure_small_fp32_step(device, steps: int, warmup: int) -> dict:
 
     def step() -> None:
         ops.rms_norm(hidden, weight, 1e-5, out=normed)
+        ops.rope_append_paged_decode(
+            batch.query, new_k, new_v, positions, table, batch.key_cache, batch.value_cache,
+            slots, batch.block_tables, batch.seq_lens, layer_index=0,
+            max_seq_len=batch.max_seq_len, out=out)
+
+    def step_two_launches() -> None:
+        ops.rms_norm(hidden, weight, 1e-5, out=normed)
         ops.rope_kv_append(batch.query, new_k, new_v, positions, table, batch.key_cache,
                            batch.value_cache, slots, 0, query_out=q_rot)
         ops.paged_attention_decode(
             q_rot, batch.key_cache, batch.value_cache, batch.block_tables,
             batch.seq_lens, layer_index=0, max_seq_len=batch.max_seq_len, out=out)
 
+    def captured(fn):
+        fn()
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            fn()
+        return graph
+
     eager_us = _time_ms(step, steps, warmup) * 1e3
-    step()
-    torch.cuda.synchronize()
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph):
-        step()
+    graph = captured(step)
     graph_us = _time_ms(graph.replay, steps, warmup) * 1e3
     flush = _llc_flush_buffer(device)
     graph_us_cold = _time_ms_cold(graph.replay, steps, flush) * 1e3
     del flush
+    graph_two = captured(step_two_launches)
+    graph_two_us = _time_ms(graph_two.replay, steps, warmup) * 1e3
     kv_bytes = sum(batch.contexts) * 2 * 64 * 2 * 4
     return {
         "workload": "decode_fp32_small: 8 seqs, ctx U[16,512]+1, Hq 8 / Hkv 2, Dh 64, block 16, "
@@ -808,6 +822,7 @@ def measure_small_fp32_step(device, steps: int, warmup: int) -> dict:
         "step_us_eager": round(eager_us, 2),
         "step_us_graph": round(graph_us, 2),
         "step_us_graph_llc_flushed": round(graph_us_cold, 2),
+        "step_us_graph_rope_append_then_decode": round(graph_two_us, 2),
         "kv_bytes": kv_bytes,
     }
 

@@ -3,8 +3,9 @@ against the two calls it replaces, tks_rope_kv_append then tks_paged_attention_d
 on the same inputs: the pools after the call and the outputs are bit-identical, the
 query is left as it was. Covered: the fused MFMA launch (bf16 / fp16, Dh 64 and 128,
 several GQA groups, with and without key splits, partly filled and exactly full last
-pages, a new token that opens a page), the two-call path it takes elsewhere (fp32 on the
-generic kernel, new rows not in 16-byte chunks), a negative slot (nothing appended) and an empty
+pages, a new token that opens a page), the two-launch path the entry takes elsewhere
+(fp32, Dh 32 and block size 8 on the generic kernel, new rows not in 16-byte chunks), a
+negative slot (nothing appended) and an empty
 sequence (its row is appended, its output is zero). Over fp8 (e4m3) pools the same
 against tks_rope_kv_append_fp8 then tks_paged_attention_decode_fp8, and the fp8
 RoPE + append launch against tks_rope then the quantizing tks_kv_append_fp8.
@@ -25,17 +26,46 @@ CASES = [
     (torch.float16, 16, 8, 128, [5, 48, 49, 700]),
     (torch.bfloat16, 16, 16, 128, [300, 17, 1]),
     (torch.bfloat16, 32, 4, 128, [90, 900]),       # G 8 at Dh 128
-    (torch.float32, 8, 2, 64, [16, 17, 513, 100]),  # fp32: generic kernel, two calls
+    (torch.float32, 8, 2, 64, [16, 17, 513, 100]),  # fp32: generic kernel, two launches
+    (torch.float32, 16, 4, 128, [1, 64, 65, 300]),  # fp32, Dh 128: likewise
+    (torch.bfloat16, 8, 2, 32, [17, 40, 3, 64]),    # Dh 32: likewise
 ]
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("kv_dtype", [None, torch.float8_e4m3fn])
+def test_fused_decode_step_block_size_8_takes_two_launches(device, dtype, kv_dtype) -> None:
+    hq, hkv, dh, contexts = 8, 2, 64, [7, 8, 9, 300, 1]
+    batch, query, key, value, positions, slots, table = _inputs(
+        device, dtype, hq, hkv, dh, contexts, seed=51, kv_dtype=kv_dtype, block_size=8)
+    kw = dict(k_scale=0.5, v_scale=2.0) if kv_dtype is not None else {}
+    kc_ref, vc_ref = batch.key_cache.clone(), batch.value_cache.clone()
+    q_ref = query.clone()
+    ops.rope_kv_append(q_ref, key, value, positions, table, kc_ref, vc_ref, slots, 0, **kw)
+    for pages_per_split in (0, 3):
+        kc, vc = batch.key_cache.clone(), batch.value_cache.clone()
+        expected = ops.paged_attention_decode(
+            q_ref, kc_ref, vc_ref, batch.block_tables, batch.seq_lens, layer_index=0,
+            max_seq_len=batch.max_seq_len, pages_per_split=pages_per_split, **kw)
+        actual = ops.rope_append_paged_decode(
+            query, key, value, positions, table, kc, vc, slots, batch.block_tables,
+            batch.seq_lens, layer_index=0, max_seq_len=batch.max_seq_len,
+            pages_per_split=pages_per_split, **kw)
+        torch.cuda.synchronize()
+        bits = torch.int32 if dtype == torch.float32 else torch.int16
+        assert torch.equal(actual.cpu().view(bits), expected.cpu().view(bits))
+        assert torch.equal(kc.view(torch.uint8), kc_ref.view(torch.uint8))
+        assert torch.equal(vc.view(torch.uint8), vc_ref.view(torch.uint8))
 
 
 FP8 = torch.float8_e4m3fn
 
 
-def _inputs(device, dtype, hq, hkv, dh, contexts, seed, kv_dtype=None, scales=(1.0, 1.0)):
+def _inputs(device, dtype, hq, hkv, dh, contexts, seed, kv_dtype=None, scales=(1.0, 1.0),
+            block_size=16):
     batch = workloads.paged_batch(contexts, [1] * len(contexts), num_q_heads=hq,
-                                  num_kv_heads=hkv, head_dim=dh, block_size=16, dtype=dtype,
-                                  device=device, seed=seed, kv_dtype=kv_dtype,
+                                  num_kv_heads=hkv, head_dim=dh, block_size=block_size,
+                                  dtype=dtype, device=device, seed=seed, kv_dtype=kv_dtype,
                                   k_scale=scales[0], v_scale=scales[1])
     b = len(contexts)
     g = torch.Generator().manual_seed(seed + 3)
@@ -47,7 +77,8 @@ def _inputs(device, dtype, hq, hkv, dh, contexts, seed, kv_dtype=None, scales=(1
     positions = (lens - 1).to(device)
     tables = batch.block_tables.to(torch.int64).cpu()
     pos = lens - 1
-    slots = (tables[torch.arange(b), pos // 16] * 16 + pos % 16).to(device)
+    slots = (tables[torch.arange(b), pos // block_size] * block_size + pos % block_size)
+    slots = slots.to(device)
     table = ops.RotaryTable(dh, theta=10_000.0, max_position=8192, dtype=dtype, device=device)
     return batch, query, key, value, positions, slots, table
 
@@ -97,7 +128,7 @@ def test_fused_decode_step_negative_slot_appends_nothing(device) -> None:
     assert torch.equal(batch.key_cache, kc_ref) and torch.equal(batch.value_cache, vc_ref)
 
 
-@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
 def test_fused_decode_step_empty_sequence_still_appends(device, dtype) -> None:
     contexts = [0, 40, 17, 0]
     hq, hkv, dh = 16, 4, 128
@@ -123,7 +154,8 @@ def test_fused_decode_step_empty_sequence_still_appends(device, dtype) -> None:
         query, key, value, positions, table, batch.key_cache, batch.value_cache, slots,
         batch.block_tables, batch.seq_lens, layer_index=0, max_seq_len=batch.max_seq_len)
     torch.cuda.synchronize()
-    assert torch.equal(actual.cpu().view(torch.int16), expected.cpu().view(torch.int16))
+    bits = torch.int32 if dtype == torch.float32 else torch.int16
+    assert torch.equal(actual.cpu().view(bits), expected.cpu().view(bits))
     assert not actual[0].any() and not actual[3].any()
     assert torch.equal(batch.key_cache, kc_ref) and torch.equal(batch.value_cache, vc_ref)
 
@@ -134,7 +166,7 @@ FP8_CASES = [
     (torch.bfloat16, 32, 8, 128, [1, 16, 17, 31, 32, 33, 200, 1025, 4096, 4097], (1.0, 1.0)),
     (torch.float16, 16, 8, 128, [5, 48, 49, 700], (2.0, 0.75)),
     (torch.bfloat16, 32, 4, 128, [90, 900, 33], (0.125, 4.0)),   # G 8 at Dh 128
-    (torch.float32, 8, 2, 64, [16, 17, 513, 100], (0.5, 2.0)),   # fp32: two calls
+    (torch.float32, 8, 2, 64, [16, 17, 513, 100], (0.5, 2.0)),   # fp32: two launches
 ]
 
 

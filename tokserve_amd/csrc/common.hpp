@@ -215,14 +215,19 @@ __device__ __forceinline__ void e4m3_words(const float *x, float scale, uint32_t
                           x + 4 * i);
 }
 
+// The code of one such value.
+__device__ __forceinline__ uint8_t e4m3_code(float x, float scale) {
+  const float x4[4] = {x, 0.f, 0.f, 0.f};
+  return static_cast<uint8_t>(fp8x4_nan_sign(float4_to_fp8x4(x / scale, 0.f, 0.f, 0.f), x4) &
+                              0xffu);
+}
+
 // The same codes for N = 1, 4, 8 or 16 values stored to dst (N bytes; the 4-, 8- and
 // 16-byte stores need that alignment).
 template <int N>
 __device__ __forceinline__ void encode_e4m3(const float *x, float scale, uint8_t *dst) {
   if constexpr (N == 1) {
-    const float x4[4] = {x[0], 0.f, 0.f, 0.f};
-    dst[0] = static_cast<uint8_t>(
-        fp8x4_nan_sign(float4_to_fp8x4(x[0] / scale, 0.f, 0.f, 0.f), x4) & 0xffu);
+    dst[0] = e4m3_code(x[0], scale);
   } else {
     static_assert(N == 4 || N == 8 || N == 16, "one 4-, 8- or 16-byte store");
     uint32_t w[N / 4];
