@@ -3,11 +3,12 @@ iteration and one decode iteration of the batched executor, and of the reference
 per-sequence forward, recorded with a dispatch mode (the analogue of the reference's
 call-count check that its custom kernels ran, tests/gpu/test_tiled_attention_end_to_end.py:237-290).
 
-Per layer a packed iteration makes two RMSNorm launches (the first layer's input norm
-without a residual), one SiLU*mul, and either one RoPE + KV append and one prefill
-attention launch (an iteration with prefill tokens) or one fused RoPE + KV append +
-decode attention call (a decode-only iteration); the final norm and one greedy argmax
-close it. No softmax, matmul-based attention or gather of the pools runs in torch.
+Over pools in the model dtype and over fp8 pools alike, per layer a packed iteration makes
+two RMSNorm launches (the first layer's input norm without a residual), one SiLU*mul, and
+either one RoPE + KV append and one prefill attention launch (an iteration with prefill
+tokens) or one fused RoPE + KV append + decode attention call (a decode-only iteration);
+the final norm and one greedy argmax close it. No softmax, matmul-based attention or
+gather of the pools runs in torch.
 """
 
 from collections import Counter
@@ -57,13 +58,16 @@ def _model(device, dtype) -> LlamaModel:
     return model.to(dtype).eval()
 
 
-@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
-def test_packed_iterations_launch_only_library_kernels(device, dtype) -> None:
+@pytest.mark.parametrize("dtype, kv_dtype", [(torch.bfloat16, None), (torch.float32, None),
+                                             (torch.bfloat16, torch.float8_e4m3fn)])
+def test_packed_iterations_launch_only_library_kernels(device, dtype, kv_dtype) -> None:
     model = _model(device, dtype)
     config = model.config
+    scales = dict(k_scale=0.5, v_scale=0.25) if kv_dtype is not None else {}
     manager = PagedKVCacheManager(num_layers=LAYERS, num_blocks=64,
                                   num_key_value_heads=config.num_key_value_heads, block_size=16,
-                                  head_dim=config.head_dim, device=device, dtype=dtype)
+                                  head_dim=config.head_dim, device=device, dtype=dtype,
+                                  kv_dtype=kv_dtype, **scales)
     scheduler = RequestScheduler(max_running_requests=8, cache_manager=manager)
     executor = BatchExecutor(model, manager, use_graphs=False)
     for index, length in enumerate((37, 5, 64)):
@@ -81,10 +85,12 @@ def test_packed_iterations_launch_only_library_kernels(device, dtype) -> None:
 
     pre, dec = _ours(prefill.count), _ours(decode.count)
     assert pre["rope_kv_append_"] + pre["rope_kv_append"] == LAYERS, pre
+    assert pre["rope"] + pre["rope_"] + pre["kv_append"] == 0, pre
     assert pre["paged_attention_prefill"] == LAYERS, pre
     assert pre["paged_attention_decode"] + pre["rope_append_paged_decode"] == 0, pre
     assert dec["rope_append_paged_decode"] == LAYERS, dec
     assert dec["rope_kv_append_"] + dec["rope_kv_append"] == 0, dec
+    assert dec["rope"] + dec["rope_"] + dec["kv_append"] == 0, dec
     assert dec["paged_attention_prefill"] + dec["paged_attention_decode"] == 0, dec
     for calls in (prefill, decode):
         ours = _ours(calls.count)
