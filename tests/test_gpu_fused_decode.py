@@ -264,6 +264,28 @@ def test_fused_decode_step_unaligned_new_rows_take_two_launches(device, kv_dtype
     assert torch.equal(batch.value_cache.view(torch.uint8), vc_ref.view(torch.uint8))
 
 
+@pytest.mark.parametrize("kv_dtype", [None, FP8])
+def test_fused_decode_step_lengths_past_the_host_bound(device, kv_dtype) -> None:
+    """A length above max_seq_len is clamped to the bound, as the decode alone clamps it:
+    the new rows still go to their slot, and the attention covers the clamped keys."""
+    hq, hkv, dh, contexts = 32, 8, 128, [100, 40, 64, 65]
+    batch, query, key, value, positions, slots, table = _inputs(
+        device, torch.bfloat16, hq, hkv, dh, contexts, seed=61, kv_dtype=kv_dtype)
+    kw = dict(k_scale=0.5, v_scale=2.0) if kv_dtype is not None else {}
+    kc_ref, vc_ref = batch.key_cache.clone(), batch.value_cache.clone()
+    q_ref = query.clone()
+    ops.rope_kv_append(q_ref, key, value, positions, table, kc_ref, vc_ref, slots, 0, **kw)
+    expected = ops.paged_attention_decode(q_ref, kc_ref, vc_ref, batch.block_tables,
+                                          batch.seq_lens, layer_index=0, max_seq_len=64, **kw)
+    actual = ops.rope_append_paged_decode(
+        query, key, value, positions, table, batch.key_cache, batch.value_cache, slots,
+        batch.block_tables, batch.seq_lens, layer_index=0, max_seq_len=64, **kw)
+    torch.cuda.synchronize()
+    assert torch.equal(actual.cpu().view(torch.int16), expected.cpu().view(torch.int16))
+    assert torch.equal(batch.key_cache.view(torch.uint8), kc_ref.view(torch.uint8))
+    assert torch.equal(batch.value_cache.view(torch.uint8), vc_ref.view(torch.uint8))
+
+
 def test_fused_decode_step_argument_errors(device) -> None:
     dtype, hq, hkv, dh, contexts = CASES[0]
     batch, query, key, value, positions, slots, table = _inputs(device, dtype, hq, hkv, dh,

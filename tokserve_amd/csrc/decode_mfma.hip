@@ -384,7 +384,8 @@ __global__ __launch_bounds__(64 * kWaves) void decode_mfma_kernel(DecodeArgs a) 
   // wave whose range holds the sequence's last page stages the new rows in LDS; its
   // lanes of the new token put them in place of what they load of that page, and
   // after its page loop it writes them to the pool.
-  bool patch = false;
+  bool staged = false;  // this wave staged the new rows (it writes them to the pool)
+  bool patch = false;   // ... and puts them in place of its loads (length not clamped)
   const int new_off = ROPE ? (len - 1) % BS : 0;
   if constexpr (ROPE) {
     constexpr int HALF = DH / 2;
@@ -421,7 +422,8 @@ __global__ __launch_bounds__(64 * kWaves) void decode_mfma_kernel(DecodeArgs a) 
     }
     // Wave-uniform: this wave holds the sequence's last page.
     if (w_begin < w_end && w_end == n_pages) {
-      patch = stage_new_rows<T, KV, DH, BS>(a, b, kvh, lane, new_k_s, new_v_s);
+      staged = stage_new_rows<T, KV, DH, BS>(a, b, kvh, lane, new_k_s, new_v_s);
+      patch = staged && a.seq_lens[b] == len;
       wave_lds_sync();
     }
   }
@@ -603,7 +605,7 @@ __global__ __launch_bounds__(64 * kWaves) void decode_mfma_kernel(DecodeArgs a) 
 
   // The staged rows to the pool, once this wave has read the page that holds their slot.
   if constexpr (ROPE) {
-    if (patch) write_staged_rows<T, KV, DH, BS>(a, b, kvh, lane, new_k_s, new_v_s);
+    if (staged) write_staged_rows<T, KV, DH, BS>(a, b, kvh, lane, new_k_s, new_v_s);
   }
 
   // Per-wave state: l summed over the 16 tokens, acc over the 4 token groups.
