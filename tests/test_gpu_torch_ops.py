@@ -1,7 +1,8 @@
 """The kernels as PyTorch operators (torch.ops.tokserve_amd.*) under torch.compile.
 
 A packed decode step of the Llama-3-8B layer shape (RMSNorm -> QKV GEMM -> RoPE with
-the K/V append into the pools -> split-K decode attention) compiles with
+the K/V append into the pools -> split-K decode attention, as two operators or as the
+fused one) compiles with
 fullgraph=True (no graph break: every kernel call is an operator that tracing sees,
 with a fake kernel for shapes and its writes declared in its schema) and gives
 results bit-identical to eager execution: outputs and the written pools. The
@@ -34,7 +35,7 @@ def _step_inputs(device, seed):
     return batch, hidden, weight, qkv_weight, positions.to(device), slots.to(device)
 
 
-def _make_step(table, max_seq_len, pages_per_split):
+def _make_step(table, max_seq_len, pages_per_split, fused):
     def step(hidden, weight, qkv_weight, positions, slots, key_cache, value_cache, tables, lens):
         normed = ops.rms_norm(hidden, weight, 1e-5)
         qkv = normed @ qkv_weight.t()
@@ -42,6 +43,10 @@ def _make_step(table, max_seq_len, pages_per_split):
         query = qkv[:, : 32 * 128].view(tokens, 32, 128)
         key = qkv[:, 32 * 128 : 40 * 128].view(tokens, 8, 128)
         value = qkv[:, 40 * 128 :].view(tokens, 8, 128)
+        if fused:
+            return ops.rope_append_paged_decode(
+                query, key, value, positions, table, key_cache, value_cache, slots, tables,
+                lens, layer_index=0, max_seq_len=max_seq_len, pages_per_split=pages_per_split)
         ops.rope_kv_append(query, key, value, positions, table, key_cache, value_cache, slots, 0)
         return ops.paged_attention_decode(query, key_cache, value_cache, tables, lens,
                                           layer_index=0, max_seq_len=max_seq_len,
@@ -50,12 +55,14 @@ def _make_step(table, max_seq_len, pages_per_split):
     return step
 
 
+@pytest.mark.parametrize("fused", [False, True])
 @pytest.mark.parametrize("pages_per_split", [0, 8])
-def test_compiled_packed_decode_step_is_bit_identical_to_eager(device, pages_per_split) -> None:
+def test_compiled_packed_decode_step_is_bit_identical_to_eager(device, pages_per_split,
+                                                               fused) -> None:
     batch, hidden, weight, qkv_weight, positions, slots = _step_inputs(device, seed=5)
     table = ops.RotaryTable(128, theta=500_000.0, max_position=4096, dtype=torch.bfloat16,
                             device=device)
-    step = _make_step(table, batch.max_seq_len, pages_per_split)
+    step = _make_step(table, batch.max_seq_len, pages_per_split, fused)
     compiled = torch.compile(step, fullgraph=True, backend="aot_eager", dynamic=False)
     pools = []
     outs = []
