@@ -22,6 +22,14 @@ def test_cpu_tensors_are_rejected() -> None:
         ops.rms_norm(torch.ones(2, 7), torch.ones(7), 1e-6)
     with pytest.raises(ValueError, match="requires HIP device tensors"):
         ops.greedy_argmax(torch.ones(2, 7))
+    table = ops.RotaryTable(8, theta=10_000.0, max_position=16, dtype=torch.float32,
+                            device=torch.device("cpu"))
+    with pytest.raises(ValueError, match="requires HIP device tensors"):
+        ops.rope_append_paged_decode(
+            torch.zeros(1, 4, 8), torch.zeros(1, 2, 8), torch.zeros(1, 2, 8),
+            torch.zeros(1, dtype=torch.int64), table, kc, kc.clone(),
+            torch.zeros(1, dtype=torch.int64), torch.zeros(1, 1, dtype=torch.int32),
+            torch.ones(1, dtype=torch.int32), layer_index=0, max_seq_len=1)
 
 
 def test_rotary_table_matches_reference_formula() -> None:
@@ -113,3 +121,9 @@ def test_operators_trace_with_fake_tensors() -> None:
         torch.ops.tokserve_amd.paged_attention_decode(q, pool, pool, tables, lens, None, 0, 64,
                                                       0.125, 0, 1.0, 1.0, out, None)
         assert out.shape == q.shape
+        kv = torch.empty(4, 2, 64, dtype=torch.bfloat16, device="cuda")
+        pos = torch.zeros(4, dtype=torch.int64, device="cuda")
+        cos = torch.empty(16, 32, dtype=torch.bfloat16, device="cuda")
+        torch.ops.tokserve_amd.rope_append_paged_decode(q, kv, kv, pos, cos, cos, pos, pool,
+                                                        pool, tables, lens, None, 0, 64, 0.125,
+                                                        0, out, None)
