@@ -19,6 +19,8 @@ from tokserve_amd.kernels import ops
 
 pytestmark = pytest.mark.gpu
 
+FP8 = torch.float8_e4m3fn
+
 CASES = [
     # dtype, Hq, Hkv, Dh, contexts
     (torch.bfloat16, 32, 4, 64, [64 + 37 * i for i in range(24)]),
@@ -30,6 +32,30 @@ CASES = [
     (torch.float32, 16, 4, 128, [1, 64, 65, 300]),  # fp32, Dh 128: likewise
     (torch.bfloat16, 8, 2, 32, [17, 40, 3, 64]),    # Dh 32: likewise
 ]
+
+
+@pytest.mark.parametrize("dh", [64, 128])
+@pytest.mark.parametrize("group", [1, 2, 4, 8, 16])
+@pytest.mark.parametrize("dtype, kv_dtype", [(torch.bfloat16, None), (torch.float16, FP8)])
+def test_fused_decode_step_every_mfma_group(device, dh, group, dtype, kv_dtype) -> None:
+    hkv = 2
+    contexts = [1, 15, 16, 17, 130, 700]
+    batch, query, key, value, positions, slots, table = _inputs(
+        device, dtype, hkv * group, hkv, dh, contexts, seed=70 + group + dh, kv_dtype=kv_dtype)
+    kw = dict(k_scale=0.75, v_scale=1.25) if kv_dtype is not None else {}
+    kc_ref, vc_ref = batch.key_cache.clone(), batch.value_cache.clone()
+    q_ref = query.clone()
+    ops.rope_kv_append(q_ref, key, value, positions, table, kc_ref, vc_ref, slots, 0, **kw)
+    expected = ops.paged_attention_decode(q_ref, kc_ref, vc_ref, batch.block_tables,
+                                          batch.seq_lens, layer_index=0,
+                                          max_seq_len=batch.max_seq_len, **kw)
+    actual = ops.rope_append_paged_decode(
+        query, key, value, positions, table, batch.key_cache, batch.value_cache, slots,
+        batch.block_tables, batch.seq_lens, layer_index=0, max_seq_len=batch.max_seq_len, **kw)
+    torch.cuda.synchronize()
+    assert torch.equal(actual.cpu().view(torch.int16), expected.cpu().view(torch.int16))
+    assert torch.equal(batch.key_cache.view(torch.uint8), kc_ref.view(torch.uint8))
+    assert torch.equal(batch.value_cache.view(torch.uint8), vc_ref.view(torch.uint8))
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
@@ -56,9 +82,6 @@ def test_fused_decode_step_block_size_8_takes_two_launches(device, dtype, kv_dty
         assert torch.equal(actual.cpu().view(bits), expected.cpu().view(bits))
         assert torch.equal(kc.view(torch.uint8), kc_ref.view(torch.uint8))
         assert torch.equal(vc.view(torch.uint8), vc_ref.view(torch.uint8))
-
-
-FP8 = torch.float8_e4m3fn
 
 
 def _inputs(device, dtype, hq, hkv, dh, contexts, seed, kv_dtype=None, scales=(1.0, 1.0),
