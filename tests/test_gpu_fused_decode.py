@@ -309,6 +309,51 @@ def test_fused_decode_step_lengths_past_the_host_bound(device, kv_dtype) -> None
     assert torch.equal(batch.value_cache.view(torch.uint8), vc_ref.view(torch.uint8))
 
 
+@pytest.mark.parametrize("fp8", [False, True])
+def test_fused_decode_step_at_the_full_llama3_8b_decode_size(device, fp8) -> None:
+    """The 256-sequence Llama-3-8B decode batch (contexts log-uniform in [128, 8192]): the
+    fused step equals the two launches bit for bit at full size."""
+    batch = (workloads.decode_llama3_8b_fp8 if fp8 else workloads.decode_llama3_8b)(device)
+    n, hq, hkv, dh = batch.num_seqs, 32, 8, 128
+    g = torch.Generator(device=device).manual_seed(3)
+    qkv = torch.randn(n, (hq + 2 * hkv) * dh, generator=g, device=device).to(torch.bfloat16)
+    query = qkv[:, : hq * dh].view(n, hq, dh)
+    key = qkv[:, hq * dh : (hq + hkv) * dh].view(n, hkv, dh)
+    value = qkv[:, (hq + hkv) * dh :].view(n, hkv, dh)
+    positions = batch.seq_lens.to(torch.int64) - 1
+    tables = batch.block_tables.to(torch.int64)
+    slots = tables[torch.arange(n, device=device), positions // 16] * 16 + positions % 16
+    table = ops.RotaryTable(dh, theta=500_000.0, max_position=8192, dtype=torch.bfloat16,
+                            device=device)
+    order = ops.longest_first(batch.contexts, device)
+    kc_ref, vc_ref = batch.key_cache.clone(), batch.value_cache.clone()
+    q_ref = query.clone()
+    ops.rope_kv_append(q_ref, key, value, positions, table, kc_ref, vc_ref, slots, 0)
+    expected = ops.paged_attention_decode(q_ref, kc_ref, vc_ref, batch.block_tables,
+                                          batch.seq_lens, layer_index=0,
+                                          max_seq_len=batch.max_seq_len, seq_order=order)
+    del kc_ref, vc_ref
+    actual = ops.rope_append_paged_decode(
+        query, key, value, positions, table, batch.key_cache, batch.value_cache, slots,
+        batch.block_tables, batch.seq_lens, layer_index=0, max_seq_len=batch.max_seq_len,
+        seq_order=order)
+    torch.cuda.synchronize()
+    assert torch.equal(actual.view(torch.int16), expected.view(torch.int16))
+    # The appended rows: each sequence's slot holds the rotated key and the value.
+    rows = slots // 16, slots % 16
+    q4 = query.clone().transpose(0, 1).unsqueeze(0)
+    k4 = key.clone().transpose(0, 1).unsqueeze(0)
+    ops.rope(q4, k4, positions, table, query_out=q4, key_out=k4)
+    k_rot = k4[0].transpose(0, 1)
+    stored_k = batch.key_cache[0, rows[0], :, rows[1], :]
+    stored_v = batch.value_cache[0, rows[0], :, rows[1], :]
+    if fp8:
+        k_rot = k_rot.float().clamp(-448, 448).to(torch.float8_e4m3fn)
+        value = value.float().clamp(-448, 448).to(torch.float8_e4m3fn)
+    assert torch.equal(stored_k.view(torch.uint8), k_rot.view(torch.uint8))
+    assert torch.equal(stored_v.view(torch.uint8), value.view(torch.uint8))
+
+
 def test_fused_decode_step_argument_errors(device) -> None:
     dtype, hq, hkv, dh, contexts = CASES[0]
     batch, query, key, value, positions, slots, table = _inputs(device, dtype, hq, hkv, dh,
