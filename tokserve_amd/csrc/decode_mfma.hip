@@ -384,6 +384,7 @@ __global__ __launch_bounds__(64 * kWaves) void decode_mfma_kernel(DecodeArgs a) 
   // wave whose range holds the sequence's last page stages the new rows in LDS; its
   // lanes of the new token put them in place of what they load of that page, and
   // after its page loop it writes them to the pool.
+  const int32_t *bt_row = a.bt + (int64_t)b * a.bt_stride;
   bool staged = false;  // this wave staged the new rows (it writes them to the pool)
   bool patch = false;   // ... and puts them in place of its loads (length not clamped)
   const int new_off = ROPE ? (len - 1) % BS : 0;
@@ -392,6 +393,18 @@ __global__ __launch_bounds__(64 * kWaves) void decode_mfma_kernel(DecodeArgs a) 
     const int64_t pos = min(max(a.positions[b], (int64_t)0), a.table_len - 1);
     const T *crow = static_cast<const T *>(a.cos_t) + pos * HALF;
     const T *srow = static_cast<const T *>(a.sin_t) + pos * HALF;
+    // Wave-uniform: this wave holds the sequence's last page. It stages the new rows
+    // before the e4m3 path's query barrier (their loads then overlap the barrier's
+    // wait), after the register rotation otherwise (measured the faster order each).
+    const bool last_wave = w_begin < w_end && w_end == n_pages;
+    auto stage = [&]() {
+      if (last_wave) {
+        staged = stage_new_rows<T, KV, DH, BS>(a, b, kvh, lane, new_k_s, new_v_s);
+        patch = staged && a.seq_lens[b] == len;
+        wave_lds_sync();
+      }
+    };
+    if constexpr (kSlab) stage();
     if constexpr (kSlab) {
       const int t = threadIdx.x;
       if (t < G * HALF / 8) {
@@ -419,12 +432,7 @@ __global__ __launch_bounds__(64 * kWaves) void decode_mfma_kernel(DecodeArgs a) 
         qa[c] = as_v8<T>(pack<T>(o1));
         qa[c + NC / 2] = as_v8<T>(pack<T>(o2));
       }
-    }
-    // Wave-uniform: this wave holds the sequence's last page.
-    if (w_begin < w_end && w_end == n_pages) {
-      staged = stage_new_rows<T, KV, DH, BS>(a, b, kvh, lane, new_k_s, new_v_s);
-      patch = staged && a.seq_lens[b] == len;
-      wave_lds_sync();
+      stage();
     }
   }
 
@@ -432,7 +440,6 @@ __global__ __launch_bounds__(64 * kWaves) void decode_mfma_kernel(DecodeArgs a) 
   const KV *vc = static_cast<const KV *>(a.vc) + a.pool.layer_base + (int64_t)kvh * a.pool.head_stride;
   const int k_off = r * DH + grp * (kSlab ? NC * 8 : 8);
   const int v_off = tg * 4 * DH + dc * 8;
-  const int32_t *bt_row = a.bt + (int64_t)b * a.bt_stride;
 
   float acc[HPL][8];
 #pragma unroll
