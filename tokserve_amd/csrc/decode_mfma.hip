@@ -203,13 +203,6 @@ struct BoolConst {
   static constexpr bool value = B;
 };
 
-template <typename T>
-__device__ __forceinline__ uint4 v8_bits(typename Mfma<T>::v8 v) {
-  uint4 r;
-  __builtin_memcpy(&r, &v, 16);
-  return r;
-}
-
 // Eight values of a row chunk, held at T's precision, as the pool stores them: T
 // elements (16 bytes) or e4m3 codes of value / scale (8 bytes).
 template <typename T, typename KV>
@@ -319,11 +312,11 @@ __global__ __launch_bounds__(64 * kWaves) void decode_mfma_kernel(DecodeArgs a) 
   __shared__ __attribute__((aligned(16))) float m_s[kWaves][G];
   __shared__ __attribute__((aligned(16))) float l_s[kWaves][G];
   __shared__ __attribute__((aligned(16))) float acc_s[kWaves][G][DH];
-  // The fused append's new key and value rows, in the pool's form, and (e4m3 pools)
-  // the workgroup's rotated query rows.
+  // The fused append's new key and value rows, in the pool's form, and the
+  // workgroup's rotated query rows.
   __shared__ __attribute__((aligned(16))) KV new_k_s[ROPE ? DH : 1];
   __shared__ __attribute__((aligned(16))) KV new_v_s[ROPE ? DH : 1];
-  __shared__ __attribute__((aligned(16))) T q_s[ROPE && sizeof(KV) == 1 ? G * DH : 1];
+  __shared__ __attribute__((aligned(16))) T q_s[ROPE ? G * DH : 1];
 
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
@@ -369,71 +362,47 @@ __global__ __launch_bounds__(64 * kWaves) void decode_mfma_kernel(DecodeArgs a) 
   constexpr bool kSlab = sizeof(KV) == 1;
   constexpr int kQStep = kSlab ? 8 : 32;
   typename M::v8 qa[NC];
-  if constexpr (!(ROPE && kSlab)) {
+  if constexpr (!ROPE) {
     const T *qp = static_cast<const T *>(a.q) + b * a.q_ss + (int64_t)(kvh * G + r % G) * a.q_hs +
                   grp * (kSlab ? NC * 8 : 8);
 #pragma unroll
     for (int c = 0; c < NC; ++c) qa[c] = as_v8<T>(ld16(qp + c * kQStep));
   }
 
-  // Fused RoPE + append. Pools in the model dtype: this lane's query chunks c and
-  // c + NC/2 hold dims d and d + Dh/2 (d = c*32 + grp*8 ..), a rotation pair. e4m3
-  // pools (slab layout): chunk c holds dims grp*NC*8 + c*8 .., whose partners sit
-  // in another lane group, so the workgroup's G query rows are rotated once into
-  // LDS, a rotation pair per thread, and the lanes read their chunks there. The
-  // wave whose range holds the sequence's last page stages the new rows in LDS; its
-  // lanes of the new token put them in place of what they load of that page, and
-  // after its page loop it writes them to the pool.
+  // Fused RoPE + append. The workgroup's G query rows are rotated once into LDS, one
+  // rotation pair (dims d, d + Dh/2) per thread, and every lane reads its chunks there
+  // (over e4m3 pools a pair's halves sit in different lane groups; over pools in the
+  // model dtype this also beat rotating each lane's pair in registers, 2-3 %). The wave
+  // whose range holds the sequence's last page stages the new rows in LDS first, so
+  // its loads overlap the barrier's wait; its lanes of the new token put them in place
+  // of what they load of that page, and after its page loop it writes them to the pool.
   const int32_t *bt_row = a.bt + (int64_t)b * a.bt_stride;
   bool staged = false;  // this wave staged the new rows (it writes them to the pool)
   bool patch = false;   // ... and puts them in place of its loads (length not clamped)
   const int new_off = ROPE ? (len - 1) % BS : 0;
   if constexpr (ROPE) {
     constexpr int HALF = DH / 2;
-    const int64_t pos = min(max(a.positions[b], (int64_t)0), a.table_len - 1);
-    const T *crow = static_cast<const T *>(a.cos_t) + pos * HALF;
-    const T *srow = static_cast<const T *>(a.sin_t) + pos * HALF;
-    // Wave-uniform: this wave holds the sequence's last page. It stages the new rows
-    // before the e4m3 path's query barrier (their loads then overlap the barrier's
-    // wait), after the register rotation otherwise (measured the faster order each).
-    const bool last_wave = w_begin < w_end && w_end == n_pages;
-    auto stage = [&]() {
-      if (last_wave) {
-        staged = stage_new_rows<T, KV, DH, BS>(a, b, kvh, lane, new_k_s, new_v_s);
-        patch = staged && a.seq_lens[b] == len;
-        wave_lds_sync();
-      }
-    };
-    if constexpr (kSlab) stage();
-    if constexpr (kSlab) {
-      const int t = threadIdx.x;
-      if (t < G * HALF / 8) {
-        const int h = t / (HALF / 8), j = (t % (HALF / 8)) * 8;
-        const T *qrow = static_cast<const T *>(a.q) + b * a.q_ss + (int64_t)(kvh * G + h) * a.q_hs;
-        float cf[8], sf[8], o1[8], o2[8];
-        load_table<T, 8>(crow, srow, j, cf, sf);
-        rotate_values<T, 8>(qrow + j, cf, sf, HALF, o1, o2);
-        st16(&q_s[h * DH + j], pack<T>(o1));
-        st16(&q_s[h * DH + j + HALF], pack<T>(o2));
-      }
-      __syncthreads();
-#pragma unroll
-      for (int c = 0; c < NC; ++c)
-        qa[c] = as_v8<T>(ld16(&q_s[(r % G) * DH + grp * NC * 8 + c * 8]));
-    } else {
-#pragma unroll
-      for (int c = 0; c < NC / 2; ++c) {
-        const int d = c * 32 + grp * 8;
-        float cf[8], sf[8], x1[8], x2[8], o1[8], o2[8];
-        load_table<T, 8>(crow, srow, d, cf, sf);
-        unpack<T>(v8_bits<T>(qa[c]), x1);
-        unpack<T>(v8_bits<T>(qa[c + NC / 2]), x2);
-        rotate_math<T, 8>(x1, x2, cf, sf, o1, o2);
-        qa[c] = as_v8<T>(pack<T>(o1));
-        qa[c + NC / 2] = as_v8<T>(pack<T>(o2));
-      }
-      stage();
+    if (w_begin < w_end && w_end == n_pages) {  // wave-uniform
+      staged = stage_new_rows<T, KV, DH, BS>(a, b, kvh, lane, new_k_s, new_v_s);
+      patch = staged && a.seq_lens[b] == len;
+      wave_lds_sync();
     }
+    const int t = threadIdx.x;
+    if (t < G * HALF / 8) {
+      const int64_t pos = min(max(a.positions[b], (int64_t)0), a.table_len - 1);
+      const int h = t / (HALF / 8), j = (t % (HALF / 8)) * 8;
+      const T *qrow = static_cast<const T *>(a.q) + b * a.q_ss + (int64_t)(kvh * G + h) * a.q_hs;
+      float cf[8], sf[8], o1[8], o2[8];
+      load_table<T, 8>(static_cast<const T *>(a.cos_t) + pos * HALF,
+                       static_cast<const T *>(a.sin_t) + pos * HALF, j, cf, sf);
+      rotate_values<T, 8>(qrow + j, cf, sf, HALF, o1, o2);
+      st16(&q_s[h * DH + j], pack<T>(o1));
+      st16(&q_s[h * DH + j + HALF], pack<T>(o2));
+    }
+    __syncthreads();
+#pragma unroll
+    for (int c = 0; c < NC; ++c)
+      qa[c] = as_v8<T>(ld16(&q_s[(r % G) * DH + (kSlab ? grp * NC * 8 + c * 8 : c * 32 + grp * 8)]));
   }
 
   const KV *kc = static_cast<const KV *>(a.kc) + a.pool.layer_base + (int64_t)kvh * a.pool.head_stride;
