@@ -50,10 +50,35 @@ def measured_traffic() -> float | None:
     return None
 
 
-def cpu_baseline(batch, target_seconds: float) -> dict:
+BF16_ATOL = 2e-2  # bf16 outputs within 2e-2 absolute of the reference's path
+
+
+def _abs_err(actual, expected) -> float:
+    return float((actual.float().cpu() - expected.float()).abs().max()) if expected.numel() else 0.0
+
+
+def _attention_parity(pairs: list[tuple], what: str) -> dict:
+    """pairs of (GPU output, torch-backend oracle output, fp32-arithmetic oracle output):
+    the largest absolute error against either of the reference's arithmetics, against
+    the bf16 bound."""
+
+    vs_torch = max(_abs_err(gpu, ref) for gpu, ref, _ in pairs)
+    vs_fp32 = max(_abs_err(gpu, ref) for gpu, _, ref in pairs)
+    worst = max(vs_torch, vs_fp32)
+    return {"checked": what, "max_abs_err": round(worst, 6),
+            "max_abs_err_vs_torch_backend": round(vs_torch, 6),
+            "max_abs_err_vs_fp32_arithmetic": round(vs_fp32, 6), "atol": BF16_ATOL,
+            "ok": bool(worst <= BF16_ATOL)}
+
+
+def cpu_baseline(batch, out, target_seconds: float) -> tuple[dict, dict]:
     """Time the oracle's per-request decode (gather + repeat_kv + causal_attention, bf16)
     on the host over the sequences of the same workload, in batch order, repeating whole
-    passes until target_seconds of CPU work (at least one full pass)."""
+    passes until target_seconds of CPU work (at least one full pass).
+
+    The first pass's outputs, and one more pass in the reference kernel's arithmetic
+    (fp32 scores, softmax and accumulator, one rounding on the store), check `out`, the
+    GPU's output for the same batch: (baseline, parity)."""
 
     import torch
 
@@ -75,13 +100,19 @@ def cpu_baseline(batch, target_seconds: float) -> dict:
     per_pass = sum(c * hkv * dh * 2 * elem for c in batch.contexts) + 2 * batch.query.numel() * elem
     elapsed = 0.0
     passes = 0
+    outputs = []
     while passes == 0 or elapsed < target_seconds:
         start = time.perf_counter()
-        for q, kc, vc, table, lens in requests:
-            paged.decode_batch(q, kc, vc, table, lens, 0)
+        outputs = [paged.decode_batch(q, kc, vc, table, lens, 0)
+                   for q, kc, vc, table, lens in requests]
         elapsed += time.perf_counter() - start
         passes += 1
-    return {
+    fp32 = [paged.decode_batch(q, kc, vc, table, lens, 0, torch.float32)
+            for q, kc, vc, table, lens in requests]
+    parity = _attention_parity([(out, torch.cat(outputs), torch.cat(fp32))],
+                               f"all {batch.num_seqs} sequences x 32 heads x 128 of the timed "
+                               "launch's output, against the oracle")
+    baseline = {
         "value": round(per_pass * passes / elapsed / 1e9, 4),
         "unit": "GB/s",
         "cores": cores,
@@ -90,6 +121,7 @@ def cpu_baseline(batch, target_seconds: float) -> dict:
                   f"workload, per-request torch-backend decode (bf16) on {cores} host "
                   f"threads, {elapsed:.1f} s",
     }
+    return baseline, parity
 
 
 def _cpu_threads() -> int:
@@ -115,10 +147,25 @@ def _cpu_median(fn, target_seconds: float) -> tuple[float, int]:
     return times[len(times) // 2], len(times)
 
 
-def cpu_small_fp32_step(target_seconds: float) -> dict:
+FP32_TOL = dict(rtol=1e-5, atol=1e-6)  # fp32 outputs within 1e-5 relative
+
+
+def _close(actual, expected, rtol: float, atol: float) -> dict:
+    """Largest absolute error and whether every element is within atol + rtol * |expected|."""
+
+    actual, expected = actual.float().cpu(), expected.float()
+    err = (actual - expected).abs()
+    return {"max_abs_err": round(float(err.max()), 9),
+            "ok": bool((err <= atol + rtol * expected.abs()).all())}
+
+
+def cpu_small_fp32_step(target_seconds: float, gpu: dict | None = None) -> tuple[dict, dict]:
     """The fp32 decode step of measure_small_fp32_step through the oracle (the reference's
     torch backend, request by request): RMSNorm, RoPE of each new Q/K at its position, the
-    slot write, then the paged decode of every sequence."""
+    slot write, then the paged decode of every sequence.
+
+    gpu: the GPU's first step (normed rows, attention output, both pools): the oracle's
+    step must give the same pools bit for bit and outputs within 1e-5 relative."""
 
     import torch
 
@@ -134,8 +181,8 @@ def cpu_small_fp32_step(target_seconds: float) -> dict:
     new_v = torch.randn(8, 2, 64, generator=g)
     key_cache, value_cache = batch.key_cache.clone(), batch.value_cache.clone()
 
-    def step() -> None:
-        torch_path.rms_norm(hidden, weight, 1e-5)
+    def step():
+        normed = torch_path.rms_norm(hidden, weight, 1e-5)
         rotated = []
         for b, ctx in enumerate(batch.contexts):
             q, k = torch_path.apply_rope(batch.query[b][None, :, None, :],
@@ -145,18 +192,38 @@ def cpu_small_fp32_step(target_seconds: float) -> dict:
             key_cache[0, block, :, offset, :] = k[0, :, 0, :]
             value_cache[0, block, :, offset, :] = new_v[b]
             rotated.append(q[0, :, 0, :])
-        paged.decode_batch(torch.stack(rotated), key_cache, value_cache, batch.block_tables,
-                           batch.seq_lens, 0)
+        out = paged.decode_batch(torch.stack(rotated), key_cache, value_cache,
+                                 batch.block_tables, batch.seq_lens, 0)
+        return normed, out
 
     seconds, runs = _cpu_median(step, target_seconds)
-    return {"value": round(seconds * 1e6, 1), "unit": "us per step", "cores": cores,
-            "kind": "port",
-            "sample": f"the whole step, median of {runs} runs on {cores} host threads"}
+    baseline = {"value": round(seconds * 1e6, 1), "unit": "us per step", "cores": cores,
+                "kind": "port",
+                "sample": f"the whole step, median of {runs} runs on {cores} host threads"}
+    if gpu is None:
+        return baseline, None
+    normed, out = step()
+    norm = _close(gpu["normed"], normed, **FP32_TOL)
+    attention = _close(gpu["out"], out, **FP32_TOL)
+    pools = bool(torch.equal(gpu["key_cache"].cpu(), key_cache)
+                 and torch.equal(gpu["value_cache"].cpu(), value_cache))
+    parity = {"checked": "the step's RMSNorm rows, attention output and both pools after "
+                         "the RoPE + append, against the oracle",
+              "max_abs_err": max(norm["max_abs_err"], attention["max_abs_err"]),
+              "rtol": FP32_TOL["rtol"], "atol": FP32_TOL["atol"],
+              "pools_bit_exact": pools, "ok": norm["ok"] and attention["ok"] and pools}
+    return baseline, parity
 
 
-def cpu_norm_rope(target_seconds: float) -> dict:
+def cpu_norm_rope(target_seconds: float, gpu: dict | None = None) -> tuple[dict, dict]:
     """The packed RMSNorm and RoPE of measure_norm_rope through the oracle (the reference's
-    torch ops, bf16 in, fp32 weight): GB/s of the same algorithmic bytes."""
+    torch ops, bf16 in, fp32 weight): GB/s of the same algorithmic bytes.
+
+    gpu: the GPU's outputs for the same stream (normed rows, rotated Q and K): RoPE must
+    match the oracle bit for bit, and RMSNorm (fp32 out) lie within the bf16 bound (the
+    oracle rounds the normalised row to bf16 before the fp32 weight)."""
+
+    import torch
 
     from oracle import torch_path
     from tokserve_amd import workloads
@@ -173,58 +240,71 @@ def cpu_norm_rope(target_seconds: float) -> dict:
         target_seconds / 2)
     norm_bytes = n * 4096 * (2 + 4) + 4096 * 4
     rope_bytes = n * (40 * 128 * 2 * 2 + 8)
-    return {"rmsnorm_gbps": round(norm_bytes / norm_s / 1e9, 2),
-            "rope_gbps": round(rope_bytes / rope_s / 1e9, 2), "unit": "GB/s", "cores": cores,
-            "kind": "port",
-            "sample": f"the whole {n}-token stream, medians of {norm_runs} / {rope_runs} runs "
-                      f"on {cores} host threads"}
+    baseline = {"rmsnorm_gbps": round(norm_bytes / norm_s / 1e9, 2),
+                "rope_gbps": round(rope_bytes / rope_s / 1e9, 2), "unit": "GB/s",
+                "cores": cores, "kind": "port",
+                "sample": f"the whole {n}-token stream, medians of {norm_runs} / {rope_runs} "
+                          f"runs on {cores} host threads"}
+    if gpu is None:
+        return baseline, None
+    norm = _close(gpu["normed"], torch_path.rms_norm(data.hidden, data.weight, data.epsilon),
+                  rtol=0.0, atol=BF16_ATOL)
+    rq, rk = torch_path.apply_rope(query, key, data.positions, theta=data.theta)
+    rope = bool(torch.equal(gpu["query"].cpu(), rq) and torch.equal(gpu["key"].cpu(), rk))
+    parity = {"checked": f"all {n} RMSNorm rows and all rotated Q/K rows, against the oracle",
+              "max_abs_err": norm["max_abs_err"], "atol": BF16_ATOL,
+              "rope_bit_exact": rope, "ok": norm["ok"] and rope}
+    return baseline, parity
 
 
-def cpu_mixed(target_seconds: float) -> dict:
-    """The mixed step's attention through the oracle (the reference's torch backend, bf16,
-    request by request) on a sample of its requests: 2 of the 16 prefill chunks and 16 of
-    the 240 decodes, drawn from the workload's own generator; the full step's time is
-    projected from the sample's TFLOP/s and GB/s."""
+def cpu_mixed(pre, dec, rows, pools_before, out_p, out_d,
+              target_seconds: float) -> tuple[dict, dict]:
+    """The whole mixed step through the oracle (the reference's torch backend, bf16,
+    request by request): the append of the step's new rows into the pools as they were
+    before the GPU's step (the C oracle's scatter, not timed), then all 16 chunks'
+    prefill and all 240 decodes, timed until target_seconds (at least 2 runs).
+
+    The GPU's pools after its append must equal the oracle's bit for bit, and its
+    prefill and decode outputs (out_p, out_d) must lie within the bf16 bound of the
+    oracle's, in both of the reference's arithmetics: (baseline, parity)."""
 
     import torch
 
-    from oracle import paged
-    from tokserve_amd import workloads
+    from oracle import kvslots, paged
 
     cores = _cpu_threads()
-    gen = torch.Generator().manual_seed(0)
-    priors = workloads.uniform_ints(16, 0, 2048, gen)
-    decode_ctx = workloads.uniform_ints(240, 256, 4096, gen)
-    chunks, decodes = 2, 16
-    contexts = [p + 512 for p in priors[:chunks]] + decode_ctx[:decodes]
-    batch = workloads.paged_batch(contexts, [512] * chunks + [1] * decodes, num_q_heads=32,
-                                  num_kv_heads=8, head_dim=128, block_size=16,
-                                  dtype=torch.bfloat16, device="cpu", seed=7)
-    n_pre = 512 * chunks
-    pre_s, pre_runs = _cpu_median(
-        lambda: paged.prefill_batch(batch.query[:n_pre], batch.key_cache, batch.value_cache,
-                                    batch.block_tables[:chunks], batch.seq_lens[:chunks],
-                                    batch.cu_seqlens_q[: chunks + 1], 0), target_seconds / 2)
-    dec_s, dec_runs = _cpu_median(
-        lambda: paged.decode_batch(batch.query[n_pre:], batch.key_cache, batch.value_cache,
-                                   batch.block_tables[chunks:], batch.seq_lens[chunks:], 0),
-        target_seconds / 2)
+    k_ref, v_ref = pools_before
+    kvslots.kv_append(rows.key.cpu(), rows.value.cpu(), k_ref, v_ref, rows.slots.cpu(), 0)
+    pools_equal = bool(torch.equal(pre.key_cache.cpu(), k_ref)
+                       and torch.equal(pre.value_cache.cpu(), v_ref))
+    qp, btp, lp, cup = (pre.query.cpu(), pre.block_tables.cpu(), pre.seq_lens.cpu(),
+                        pre.cu_seqlens_q.cpu())
+    qd, btd, ld = dec.query.cpu(), dec.block_tables.cpu(), dec.seq_lens.cpu()
 
-    def flops(prior_list):
-        return sum(4 * 32 * 128 * (512 * p + 512 * 513 // 2) for p in prior_list)
+    def step(compute=None):
+        return (paged.prefill_batch(qp, k_ref, v_ref, btp, lp, cup, 0, compute),
+                paged.decode_batch(qd, k_ref, v_ref, btd, ld, 0, compute))
 
-    def kv_bytes(ctx_list):
-        return sum(c * 8 * 128 * 2 * 2 for c in ctx_list)
-
-    tflops = flops(priors[:chunks]) / pre_s / 1e12
-    gbps = kv_bytes(decode_ctx[:decodes]) / dec_s / 1e9
-    step_ms = (flops(priors) / (tflops * 1e12) + kv_bytes(decode_ctx) / (gbps * 1e9)) * 1e3
-    return {"value": round(step_ms, 1), "unit": "ms per step (projected)",
-            "prefill_tflops": round(tflops, 4), "decode_gbps": round(gbps, 3), "cores": cores,
-            "kind": "port",
-            "sample": f"{chunks} of the 16 prefill chunks (median of {pre_runs} runs) and "
-                      f"{decodes} of the 240 decodes (median of {dec_runs}) on {cores} host "
-                      "threads; the full step projected from their rates"}
+    times: list[float] = []
+    first = None
+    while len(times) < 2 or sum(times) < target_seconds:
+        t0 = time.perf_counter()
+        outputs = step()
+        times.append(time.perf_counter() - t0)
+        first = first or outputs
+    fp32 = step(torch.float32)
+    parity = _attention_parity([(out_p, first[0], fp32[0]), (out_d, first[1], fp32[1])],
+                               "all 16 chunks (8,192 query rows) and all 240 decodes of the "
+                               "step's output, against the oracle")
+    parity["append_pools_bit_exact"] = pools_equal
+    parity["ok"] = parity["ok"] and pools_equal
+    times.sort()
+    baseline = {"value": round(times[len(times) // 2] * 1e3, 1), "unit": "ms per step",
+                "cores": cores, "kind": "port",
+                "sample": f"the whole step's attention (16 prefill chunks + 240 decodes, "
+                          f"request by request), median of {len(times)} runs on {cores} host "
+                          "threads; the append is not timed"}
+    return baseline, parity
 
 
 def main() -> int:
@@ -273,6 +353,19 @@ def main() -> int:
             batch.seq_lens, layer_index=0, max_seq_len=batch.max_seq_len, out=out,
             workspace=workspace, pages_per_split=args.pages_per_split, seq_order=order,
         )
+
+    # Parity before timing (the reference's benchmark establishes parity before it times
+    # anything): the CPU baseline leg runs the oracle over the same batch, and its
+    # outputs check this launch's output; a mismatch ends the run without a figure.
+    step()
+    torch.cuda.synchronize()
+    baseline = parity = None
+    if not args.no_cpu_baseline:
+        baseline, parity = cpu_baseline(batch, out.clone(), args.cpu_seconds)
+        if not parity["ok"]:
+            print(json.dumps({"parity_failed": "decode_llama3_8b", "parity": parity}),
+                  file=sys.stderr, flush=True)
+            return 1
 
     # At least `--warmup` launches and at least 150 ms of back-to-back work: clocks
     # leave their idle state only after ~50 ms of sustained load.
@@ -337,14 +430,18 @@ def main() -> int:
             "traffic": traffic,
         },
     }
+    def cpu_or(seconds: float) -> float | None:
+        return None if args.no_cpu_baseline else seconds
+
     if not args.no_secondary:
         secondaries = {
-            "mixed_step": lambda: measure_mixed(device, 20, 5),
+            "mixed_step": lambda: measure_mixed(device, 20, 5, cpu_seconds=cpu_or(3.0)),
             "mixed_step_fp8_kv": lambda: measure_mixed(device, 20, 5,
                                                        kv_dtype=torch.float8_e4m3fn),
             "prefill_long": lambda: measure_prefill_long(device),
-            "norm_rope": lambda: measure_norm_rope(device, 20, 5),
-            "small_fp32_step": lambda: measure_small_fp32_step(device, 50, 10),
+            "norm_rope": lambda: measure_norm_rope(device, 20, 5, cpu_seconds=cpu_or(4.0)),
+            "small_fp32_step": lambda: measure_small_fp32_step(device, 50, 10,
+                                                               cpu_seconds=cpu_or(2.0)),
             "decode_fp8_kv": lambda: measure_decode_fp8(device, args.seed, 50, 10),
             "decode_small_batches": lambda: measure_decode_small_batches(device, args.seed, 50,
                                                                          10),
@@ -357,13 +454,6 @@ def main() -> int:
             print(f"unknown secondary measurement(s): {sorted(unknown)}", file=sys.stderr)
             return 2
         result["secondary"] = {name: secondaries[name]() for name in chosen}
-        if not args.no_cpu_baseline:
-            cpu = {"small_fp32_step": lambda: cpu_small_fp32_step(2.0),
-                   "norm_rope": lambda: cpu_norm_rope(4.0),
-                   "mixed_step": lambda: cpu_mixed(6.0)}
-            for name in chosen:
-                if name in cpu:
-                    result["secondary"][name]["cpu_baseline"] = cpu[name]()
     if not args.no_e2e:
         e2e = measure_e2e(device, args.seed,
                           None if args.no_cpu_baseline else args.cpu_seconds)
@@ -374,12 +464,16 @@ def main() -> int:
                 device, args.seed, None, kv_dtype=torch.float8_e4m3fn)
             result["secondary"]["e2e_tinyllama_fp32"] = measure_e2e(
                 device, args.seed, None, dtype=torch.float32)
-    if not args.no_cpu_baseline:
-        result["cpu_baseline"] = cpu_baseline(batch, args.cpu_seconds)
+    if baseline is not None:
+        result["cpu_baseline"] = baseline
+    result["parity"] = parity
+    checks = [parity] + [entry["parity"] for entry in result.get("secondary", {}).values()
+                         if isinstance(entry, dict) and entry.get("parity")]
+    result["parity_all_ok"] = None if parity is None else all(c["ok"] for c in checks)
     print(json.dumps(result), flush=True)
     if args.copy_calibration:
         copy_calibration(device)
-    return 0
+    return 0 if result["parity_all_ok"] in (None, True) else 1
 
 
 def _settle(fn, warmup: int, seconds: float = 0.15) -> None:
@@ -440,10 +534,13 @@ def _llc_flush_buffer(device):
     return torch.zeros(512 << 20, dtype=torch.uint8, device=device)
 
 
-def measure_mixed(device, steps: int, warmup: int, kv_dtype=None) -> dict:
+def measure_mixed(device, steps: int, warmup: int, kv_dtype=None,
+                  cpu_seconds: float | None = None) -> dict:
     """Mixed chunked-prefill + decode step (Llama-3-8B layer shape, bf16): 16 chunks of
     512 tokens on prior contexts U[0, 2048] and 240 decodes on contexts U[256, 4096].
-    kv_dtype torch.float8_e4m3fn: the same step over fp8 pools (scale 1)."""
+    kv_dtype torch.float8_e4m3fn: the same step over fp8 pools (scale 1). cpu_seconds:
+    before timing, the first step's pools and outputs are checked by the CPU baseline
+    leg (cpu_mixed), which runs that long."""
 
     import torch
 
@@ -457,18 +554,11 @@ def measure_mixed(device, steps: int, warmup: int, kv_dtype=None) -> dict:
     order = ops.longest_first(dec.contexts, device)
     # The step's new K/V rows (every prefill token and every decode token, 8,432 rows),
     # scattered through slot_mapping into their sequences' paged blocks before attention.
-    tables = torch.cat((pre.block_tables, dec.block_tables)).cpu()
-    positions = [p for ctx, ql in zip(pre.contexts + dec.contexts, pre.query_lens + dec.query_lens)
-                 for p in range(ctx - ql, ctx)]
-    rows = [b for b, ql in enumerate(pre.query_lens + dec.query_lens) for _ in range(ql)]
-    slots = torch.tensor([int(tables[b, p // 16]) * 16 + p % 16 for b, p in zip(rows, positions)],
-                         dtype=torch.int64, device=device)
-    rng = torch.Generator(device=device).manual_seed(3)
-    new_k = torch.randn((len(rows), 8, 128), generator=rng, device=device).to(torch.bfloat16)
-    new_v = torch.randn((len(rows), 8, 128), generator=rng, device=device).to(torch.bfloat16)
+    rows = workloads.step_new_rows([pre, dec])
 
     def append() -> None:
-        ops.kv_append(new_k, new_v, pre.key_cache, pre.value_cache, slots, 0, **scales)
+        ops.kv_append(rows.key, rows.value, pre.key_cache, pre.value_cache, rows.slots, 0,
+                      **scales)
 
     def prefill() -> None:
         ops.paged_attention_prefill(
@@ -486,6 +576,13 @@ def measure_mixed(device, steps: int, warmup: int, kv_dtype=None) -> dict:
         prefill()
         decode()
 
+    checked = None
+    if cpu_seconds is not None:
+        before = (pre.key_cache.cpu(), pre.value_cache.cpu())
+        step()
+        torch.cuda.synchronize()
+        checked = cpu_mixed(pre, dec, rows, before, out_p.clone(), out_d.clone(), cpu_seconds)
+        del before
     ms_app = _time_ms(append, steps, warmup)
     ms_pre = _time_ms(prefill, steps, warmup)
     ms_dec = _time_ms(decode, steps, warmup)
@@ -498,8 +595,9 @@ def measure_mixed(device, steps: int, warmup: int, kv_dtype=None) -> dict:
         flops += 4 * hq * dh * visible
     dec_bytes = (sum(dec.contexts) * 8 * dh * 2 * dec.key_cache.element_size()
                  + 2 * dec.query.numel() * 2)
-    app_bytes = len(rows) * (2 * 8 * 128 * 2 + 2 * 8 * 128 * pre.key_cache.element_size() + 8)
-    return {
+    n_rows = rows.slots.shape[0]
+    app_bytes = n_rows * (2 * 8 * 128 * 2 + 2 * 8 * 128 * pre.key_cache.element_size() + 8)
+    result = {
         "workload": "mixed_llama3_8b: 16 x 512-token prefill chunks (prior U[0,2048]) + 240 "
                     "decodes (ctx U[256,4096]), Hq 32 / Hkv 8, Dh 128, block 16, bf16"
                     + ("" if kv_dtype is None else "; fp8 e4m3 K/V pools")
@@ -513,6 +611,9 @@ def measure_mixed(device, steps: int, warmup: int, kv_dtype=None) -> dict:
         "decode_ms": round(ms_dec, 5),
         "decode_gbps": round(dec_bytes / (ms_dec * 1e-3) / 1e9, 1),
     }
+    if checked is not None:
+        result["cpu_baseline"], result["parity"] = checked
+    return result
 
 
 def _clock_power() -> dict | None:
@@ -756,13 +857,15 @@ def measure_decode_small_batches(device, seed: int, steps: int, warmup: int) -> 
     }
 
 
-def measure_small_fp32_step(device, steps: int, warmup: int) -> dict:
+def measure_small_fp32_step(device, steps: int, warmup: int,
+                            cpu_seconds: float | None = None) -> dict:
     """The CPU-runnable fp32 decode step (8 sequences, contexts U[16, 512] + 1, 8/2 heads,
     Dh 64, block 16, 512-block pool): RMSNorm (hidden 512, eps 1e-5), then RoPE (theta 1e4)
     of the new Q/K at each sequence's last position, the KV append through slot_mapping and
     split-K decode attention in one call (as the model layer runs them; also timed as the
     RoPE + append launch followed by the decode). Launch-bound: reported in microseconds,
-    eager and as a HIP graph."""
+    eager and as a HIP graph. cpu_seconds: before timing, the first step's outputs and
+    pools are checked by the CPU baseline leg (cpu_small_fp32_step), which runs that long."""
 
     import torch
 
@@ -807,6 +910,13 @@ def measure_small_fp32_step(device, steps: int, warmup: int) -> dict:
             fn()
         return graph
 
+    checked = None
+    if cpu_seconds is not None:
+        step()
+        torch.cuda.synchronize()
+        checked = cpu_small_fp32_step(cpu_seconds, {
+            "normed": normed.clone(), "out": out.clone(), "key_cache": batch.key_cache.clone(),
+            "value_cache": batch.value_cache.clone()})
     eager_us = _time_ms(step, steps, warmup) * 1e3
     graph = captured(step)
     graph_us = _time_ms(graph.replay, steps, warmup) * 1e3
@@ -816,7 +926,7 @@ def measure_small_fp32_step(device, steps: int, warmup: int) -> dict:
     graph_two = captured(step_two_launches)
     graph_two_us = _time_ms(graph_two.replay, steps, warmup) * 1e3
     kv_bytes = sum(batch.contexts) * 2 * 64 * 2 * 4
-    return {
+    result = {
         "workload": "decode_fp32_small: 8 seqs, ctx U[16,512]+1, Hq 8 / Hkv 2, Dh 64, block 16, "
                     "fp32; RMSNorm 512 + RoPE with KV append + decode attention",
         "step_us_eager": round(eager_us, 2),
@@ -825,9 +935,12 @@ def measure_small_fp32_step(device, steps: int, warmup: int) -> dict:
         "step_us_graph_rope_append_then_decode": round(graph_two_us, 2),
         "kv_bytes": kv_bytes,
     }
+    if checked is not None:
+        result["cpu_baseline"], result["parity"] = checked
+    return result
 
 
-def measure_norm_rope(device, steps: int, warmup: int) -> dict:
+def measure_norm_rope(device, steps: int, warmup: int, cpu_seconds: float | None = None) -> dict:
     """RMSNorm (hidden 4096, fp32 weight -> fp32 out, the Triton wrapper's contract) and
     RoPE (32 + 8 heads x 128, theta 5e5, in place) on a packed ragged bf16 stream.
 
@@ -837,7 +950,9 @@ def measure_norm_rope(device, steps: int, warmup: int) -> dict:
     the old per-launch flush measurement (a 512 MB read before each launch, each launch
     bracketed by its own HIP events). Ceiling: torch's own elementwise kernels moving the
     same bytes in the same directions (a bf16 -> fp32 conversion of the rows; copies of
-    Q and K), timed the same two ways."""
+    Q and K), timed the same two ways. cpu_seconds: before timing, one launch of each
+    (RoPE out of place) is checked by the CPU baseline leg (cpu_norm_rope), which runs
+    that long."""
 
     import torch
 
@@ -874,6 +989,15 @@ def measure_norm_rope(device, steps: int, warmup: int) -> dict:
         fns = [make(i) for i in range(sets)]
         return lambda: [fn() for fn in fns]
 
+    checked = None
+    if cpu_seconds is not None:
+        q4 = data.query.permute(1, 0, 2).unsqueeze(0)
+        k4 = data.key.permute(1, 0, 2).unsqueeze(0)
+        normed = ops.rms_norm(data.hidden, data.weight, data.epsilon)
+        rq, rk = ops.rope(q4, k4, data.positions, table)
+        torch.cuda.synchronize()
+        checked = cpu_norm_rope(cpu_seconds, {"normed": normed, "query": rq, "key": rk})
+        del normed, rq, rk
     norm_bytes = n * 4096 * (2 + 4) + 4096 * 4
     rope_bytes = n * (40 * 128 * 2 * 2 + 8)
     result = {
@@ -898,6 +1022,8 @@ def measure_norm_rope(device, steps: int, warmup: int) -> dict:
                       ("rope", "torch_copy_same_bytes_as_rope")):
         result[name]["cold_frac_of_same_bytes_torch"] = round(
             result[ref]["cold_ms"] / result[name]["cold_ms"], 3)
+    if checked is not None:
+        result["cpu_baseline"], result["parity"] = checked
     return result
 
 
@@ -951,10 +1077,14 @@ def measure_e2e(device, seed: int, cpu_seconds: float | None, kv_dtype=None,
     from tokserve_amd.engine.model import LlamaModel
 
     config = tinyllama_1_1b(max_position_embeddings=2048)
-    torch.manual_seed(seed)
-    with torch.device(device):
-        model = LlamaModel(config)
     dtype = torch.bfloat16 if dtype is None else dtype
+    torch.manual_seed(seed)
+    if dtype == torch.float32:
+        # Drawn on the host, as the fp32 greedy-token fixture's weights were.
+        model = LlamaModel(config).to(device)
+    else:
+        with torch.device(device):
+            model = LlamaModel(config)
     model = model.to(dtype).eval()
     specs = workloads.tinyllama_requests(seed=seed)
     # The server's warm-up: each engine first serves another request set of the same
@@ -1019,9 +1149,55 @@ def measure_e2e(device, seed: int, cpu_seconds: float | None, kv_dtype=None,
         "decode_tokens_per_s": round(
             sum(len(r.decode_ids) for r in history[1:]) / max(sum(decode_steps), 1e-9), 1),
     }
+    if dtype == torch.float32 and seed == 0:
+        result["parity"] = fixture_token_parity(engine, history, "timed-")
     if cpu_seconds is not None:
         result["cpu_baseline"] = e2e_cpu_baseline(model, specs, cpu_seconds)
     return result
+
+
+FP32_TOKENS = ROOT / "tests" / "golden" / "e2e_tinyllama_fp32_tokens.pt"
+
+
+def fixture_token_parity(engine, history, prefix: str) -> dict | None:
+    """The fp32 run's greedy tokens and iteration records against the committed fixture
+    of the reference's torch backend on the same workload (made on the host by
+    tests/golden/make_e2e_fp32_tokens.py): tokens match up to each request's first
+    differing token (after it, the two continuations attend to different tokens)."""
+
+    import torch
+
+    if not FP32_TOKENS.is_file():
+        return None
+    fixture = torch.load(FP32_TOKENS, weights_only=True)
+    matched = total = identical = 0
+    first = None
+    for i, rid in enumerate(fixture["request_ids"]):
+        expected = fixture["tokens"][i].tolist()
+        got = engine.scheduler.get_request(prefix + rid).result.generated_token_ids[0].tolist()
+        total += len(expected)
+        same = next((j for j, (a, b) in enumerate(zip(got, expected)) if a != b),
+                    min(len(got), len(expected)))
+        matched += same
+        if got == expected:
+            identical += 1
+        elif first is None:
+            first = {"request": rid, "token": same,
+                     "fixture_top2_margin": float(fixture["margins"][i][same])
+                     if same < len(expected) else None}
+
+    def strip(ids):
+        return [x[len(prefix):] for x in ids]
+
+    records = [{"admitted": strip(r.admitted_ids), "prefill": strip(r.prefill_ids),
+                "decode": strip(r.decode_ids), "completed": strip(r.completed_ids),
+                "active": strip(r.active_ids)} for r in history]
+    same_records = records == fixture["records"]
+    return {"checked": f"{total} greedy tokens of {len(fixture['request_ids'])} requests and "
+                       f"{len(fixture['records'])} iteration records against the fixture",
+            "tokens_matched": matched, "tokens": total, "requests_identical": identical,
+            "first_divergence": first, "records_identical": same_records,
+            "ok": matched == total and same_records}
 
 
 def e2e_cpu_baseline(model, specs, target_seconds: float) -> dict:

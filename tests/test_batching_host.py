@@ -102,7 +102,42 @@ def _oracle_events(specs, max_running, num_blocks, block_size, eos=None):
     for rid, prompt, n in specs:
         reference.submit(oracle_engine.Request(rid, list(prompt), n, eos_token_id=eos))
     records = reference.run()
-    return reference.events, records
+    return _one_forward_per_iteration(reference.events), records
+
+
+def _one_forward_per_iteration(events: list[tuple]) -> list[tuple]:
+    """The reference's hook sequence (each prefill's started / finished around its own
+    forward) as an engine that serves an iteration's prefills with one forward emits it:
+    within each iteration, every prefill_started moves, in order, to where the first one
+    was; everything else keeps its place."""
+
+    out: list[tuple] = []
+    group: list[tuple] = []
+    for event in events + [("record_iteration",)]:
+        group.append(event)
+        if event[0] != "record_iteration":
+            continue
+        starts = [e for e in group if e[0] == "prefill_started"]
+        rest = [e for e in group if e[0] != "prefill_started"]
+        if starts:
+            first = next(i for i, e in enumerate(group) if e[0] == "prefill_started")
+            rest[first:first] = starts
+        out.extend(rest)
+        group = []
+    return out[:-1]
+
+
+def test_one_forward_order_moves_only_the_starts() -> None:
+    events = [("request_admitted", "a"), ("request_admitted", "b"),
+              ("prefill_started", "a"), ("prefill_finished", "a"), ("token_produced", "a"),
+              ("prefill_started", "b"), ("prefill_finished", "b"), ("token_produced", "b"),
+              ("record_iteration", 2, 0), ("token_produced", "a"), ("record_iteration", 0, 1)]
+    assert _one_forward_per_iteration(events) == [
+        ("request_admitted", "a"), ("request_admitted", "b"),
+        ("prefill_started", "a"), ("prefill_started", "b"),
+        ("prefill_finished", "a"), ("token_produced", "a"),
+        ("prefill_finished", "b"), ("token_produced", "b"),
+        ("record_iteration", 2, 0), ("token_produced", "a"), ("record_iteration", 0, 1)]
 
 
 @pytest.mark.parametrize(("specs", "max_running", "num_blocks", "block_size"), [
@@ -113,7 +148,8 @@ def test_metrics_hooks_follow_the_reference_order(specs, max_running, num_blocks
                                                   block_size) -> None:
     """The ragged scenario (tests/integration/test_continuous_batch_ragged.py:57-169) and a
     mix with a zero-token request: the same hook calls, in the same order, as the
-    reference's per-request loop (restated in oracle/engine.py)."""
+    reference's per-request loop (restated in oracle/engine.py), except that an
+    iteration's prefill_started calls all come before its one packed forward."""
 
     recorder = Recorder()
     engine, scheduler, _ = _engine(max_running, num_blocks, block_size, metrics=recorder)
@@ -242,12 +278,37 @@ def test_module_level_execution_reuses_one_executor_per_manager() -> None:
     execution.BatchExecutor = StubExecutor
     try:
         execute_prefill(model, manager, requests)
-        first = execution._executors[manager]
+        first = manager._batch_executor
         execute_decode(model, manager, requests, metrics=Recorder())
-        assert execution._executors[manager] is first
+        assert manager._batch_executor is first
     finally:
         execution.BatchExecutor = original
     assert requests[0].num_generated_tokens == 2
+
+
+def test_module_level_execution_lets_the_manager_go() -> None:
+    """The executor execute_prefill / execute_decode keep for a manager (with its pools and
+    decode graphs) is collected with the manager once the caller drops it."""
+
+    import gc
+    import weakref
+
+    model, manager = _model(), _manager(16, 2)
+    requests = _running([("a", [1, 2], 3)])
+    original = execution.BatchExecutor
+    execution.BatchExecutor = StubExecutor
+    try:
+        execute_prefill(model, manager, requests)
+        execute_decode(model, manager, requests)
+    finally:
+        execution.BatchExecutor = original
+    assert requests[0].num_generated_tokens == 2
+    alive = weakref.ref(manager)
+    executor = weakref.ref(manager._batch_executor)
+    assert executor().manager is manager
+    del manager, requests
+    gc.collect()
+    assert alive() is None and executor() is None
 
 
 def test_reference_keyword_interfaces_and_module_paths() -> None:
@@ -279,6 +340,32 @@ def test_reference_keyword_interfaces_and_module_paths() -> None:
         rope.apply_rope(torch.ones(1, 2, 3, 8), torch.ones(1, 1, 3, 8), positions[:3],
                         theta=10_000.0)
     assert build_iteration_plan([]).is_empty
+
+
+def test_reference_cache_keyword_and_paged_generate_module() -> None:
+    """tokserve/engine/model.py:50,124 and attention.py:181 take cache= beside paged_cache=;
+    generate_with_paged_cache lives at tokserve/generation/paged_generate.py:18. cache=None
+    is accepted (the call goes on, here to the device check), a contiguous cache raises
+    ValueError, with the reference's message when a paged cache comes too."""
+
+    import inspect
+
+    from tokserve_amd.generation import paged_generate
+
+    assert list(inspect.signature(paged_generate.generate_with_paged_cache).parameters) == [
+        "model", "input_ids", "config", "manager", "sequence_id"]
+    model = LlamaModel(LlamaConfig(**CONFIG))
+    ids = torch.ones(1, 3, dtype=torch.int64)
+    block, attention = model.layers[0], model.layers[0].self_attention
+    hidden, positions = torch.ones(1, 3, CONFIG["hidden_size"]), torch.arange(3)
+    for call in (lambda **kw: model(ids, **kw), lambda **kw: block(hidden, positions, **kw),
+                 lambda **kw: attention(hidden, positions, **kw)):
+        with pytest.raises(ValueError, match="requires HIP device tensors|CUDA"):
+            call(cache=None)
+        with pytest.raises(ValueError, match="contiguous KV caches are not supported"):
+            call(cache=object())
+        with pytest.raises(ValueError, match="choose either contiguous or paged cache"):
+            call(cache=object(), paged_cache=object())
 
 
 class _Ready:

@@ -18,7 +18,8 @@ from tokserve_amd.engine.config import LlamaConfig
 from tokserve_amd.engine.model import LlamaModel
 from tokserve_amd.engine.paged.inference import decode_paged, prefill_paged
 from tokserve_amd.engine.paged.manager import PagedKVCacheManager
-from tokserve_amd.generation.generate import generate, generate_with_paged_cache
+from tokserve_amd.generation.generate import generate
+from tokserve_amd.generation.paged_generate import generate_with_paged_cache
 from tokserve_amd.generation.types import GenerationConfig
 from tokserve_amd.scheduler.request import ScheduledRequest
 from tokserve_amd.scheduler.scheduler import RequestScheduler
@@ -75,6 +76,20 @@ def test_full_recompute_and_paged_generation_agree(device) -> None:
     paged = generate_with_paged_cache(model, prompt, config, manager, sequence_id="p")
     assert full.token_ids.tolist() == paged.token_ids.tolist()
     assert manager.allocator.allocated_count == 0
+    # The reference's call forms: the module path tokserve.generation.paged_generate and
+    # an explicit cache=None on the model and a block (tokserve/engine/model.py:50,124).
+    from tokserve_amd.generation import paged_generate
+
+    again = paged_generate.generate_with_paged_cache(model, prompt, config, manager,
+                                                     sequence_id="p")
+    assert again.token_ids.tolist() == paged.token_ids.tolist()
+    assert torch.equal(model(prompt, cache=None), model(prompt))
+    hidden = model.embed_tokens(prompt)
+    positions = torch.arange(5, device=device)
+    assert torch.equal(model.layers[0](hidden, positions, cache=None),
+                       model.layers[0](hidden, positions))
+    with pytest.raises(ValueError, match="contiguous KV caches are not supported"):
+        model(prompt, cache=object())
 
 
 def _run_both(model, device, specs, *, max_running, num_blocks, block_size, kv_dtype=None,
@@ -165,29 +180,67 @@ def test_tinyllama_width_fp32_greedy_tokens_identical(device) -> None:
     assert [r.completed_ids for r in engine.history] == [r.completed_ids for r in expected]
 
 
-def test_e2e_config_fp32_greedy_tokens_identical(device) -> None:
-    """The end-to-end serving configuration's model in fp32: TinyLlama-1.1B shape (22
-    layers, hidden 2048, 32/4 heads of 64, MLP 5632, vocabulary 32000), random init under
-    a seed, the first three requests of the e2e workload (prompts of 113, 962 and 544
-    tokens) with 4 greedy tokens each, block size 16. The batched engine on the GPU and
-    the oracle engine on the host give identical tokens and iteration records."""
+def _fixture_script():
+    """tests/golden/make_e2e_fp32_tokens.py as a module (its model builder and digest)."""
+
+    import importlib.util
+
+    path = Path(__file__).parent / "golden" / "make_e2e_fp32_tokens.py"
+    spec = importlib.util.spec_from_file_location("make_e2e_fp32_tokens", path)
+    module = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(module)
+    return module
+
+
+def test_e2e_config_fp32_all_greedy_tokens_match_fixture(device) -> None:
+    """The end-to-end serving configuration in fp32 at full scale: TinyLlama-1.1B shape
+    (22 layers, hidden 2048, 32/4 heads of 64, MLP 5632, vocabulary 32000), random init on
+    the host under torch.manual_seed(0), all 128 requests of the e2e workload (prompts
+    U[64, 1024]), 128 greedy tokens each, block size 16, max 128 running, served by the
+    batched engine with decode HIP graphs and overlapped decode. Every one of the 16,384
+    tokens, every iteration record and every released block list equals the fixture the
+    reference's torch backend produced on the host (tests/golden/make_e2e_fp32_tokens.py,
+    oracle/engine.py); the weights are checked against the fixture's digest first."""
 
     from tokserve_amd import workloads
-    from tokserve_amd.engine.config import tinyllama_1_1b
 
-    torch.manual_seed(0)
-    with torch.device(device):
-        model = LlamaModel(tinyllama_1_1b(max_position_embeddings=2048))
-    model = model.eval()
-    specs = [(s.request_id, list(s.prompt), 4) for s in workloads.tinyllama_requests(seed=0)[:3]]
-    blocks = sum((len(prompt) + n + 15) // 16 for _, prompt, n in specs)
-    engine, _, _, _, reference, expected = _run_both(model, device, specs, max_running=128,
-                                                     num_blocks=blocks, block_size=16)
-    for rid, _, _ in specs:
-        assert engine.scheduler.get_request(rid).result.generated_token_ids[0].tolist() == \
-            reference.finished[rid].generated, rid
-    assert [r.decode_ids for r in engine.history] == [r.decode_ids for r in expected]
-    assert [r.completed_ids for r in engine.history] == [r.completed_ids for r in expected]
+    script = _fixture_script()
+    fixture = torch.load(script.OUT, weights_only=True)
+    host_model = script.build_model()
+    assert script.weights_sha256(host_model) == fixture["weights_sha256"]
+    model = host_model.to(device).eval()
+    specs = workloads.tinyllama_requests(seed=0, max_new_tokens=fixture["max_new_tokens"])
+    assert [s.request_id for s in specs] == fixture["request_ids"]
+    manager = _manager(model, device, num_blocks=fixture["num_blocks"], block_size=16)
+    scheduler = RequestScheduler(max_running_requests=fixture["max_running"],
+                                 cache_manager=manager)
+    engine = ContinuousBatchEngine(model, scheduler, manager, overlap_decode=True)
+    assert engine.executor.graphs is not None
+    released = {}
+    original = manager.release_sequence
+
+    def record(sequence_id):
+        released[sequence_id] = list(manager.get_sequence(sequence_id).block_ids)
+        original(sequence_id)
+
+    manager.release_sequence = record
+    for spec in specs:
+        scheduler.submit(ScheduledRequest(spec.request_id,
+                                          torch.tensor([spec.prompt], device=device),
+                                          GenerationConfig(max_new_tokens=spec.max_new_tokens)))
+    engine.run_until_idle()
+    for i, rid in enumerate(fixture["request_ids"]):
+        got = scheduler.get_request(rid).result.generated_token_ids[0].tolist()
+        expected = fixture["tokens"][i].tolist()
+        if got != expected:
+            j = next(j for j, (a, b) in enumerate(zip(got, expected)) if a != b)
+            pytest.fail(f"{rid}: token {j} is {got[j]}, the fixture's {expected[j]} "
+                        f"(fixture top-2 margin {float(fixture['margins'][i][j]):.3g})")
+    records = [{"admitted": list(r.admitted_ids), "prefill": list(r.prefill_ids),
+                "decode": list(r.decode_ids), "completed": list(r.completed_ids),
+                "active": list(r.active_ids)} for r in engine.history]
+    assert records == fixture["records"]
+    assert released == fixture["released_blocks"]
 
 
 def test_e2e_config_bf16_records_blocks_logits_and_graphs(device) -> None:

@@ -127,3 +127,88 @@ def test_operators_trace_with_fake_tensors() -> None:
         torch.ops.tokserve_amd.rope_append_paged_decode(q, kv, kv, pos, cos, cos, pos, pool,
                                                         pool, tables, lens, None, 0, 64, 0.125,
                                                         0, out, None)
+
+
+@pytest.fixture
+def meta_as_device(monkeypatch):
+    """Tensors on the meta device stand in for HIP tensors (CPU tensors stay host
+    tensors), and the library's operators only record that they were reached."""
+
+    reached: list[str] = []
+
+    def require(operation, *tensors):
+        for tensor in tensors:
+            if tensor.device.type != "meta":
+                raise ValueError(f"{operation} requires HIP device tensors")
+        return tensors[0].device
+
+    class Library:
+        def __getattr__(self, name):
+            return lambda *args, **kwargs: reached.append(name)
+
+    monkeypatch.setattr(ops, "require_hip", require)
+    monkeypatch.setattr(ops, "_ops", Library())
+    return reached
+
+
+def _decode_args(device):
+    kc = torch.zeros(1, 4, 2, 16, 8, device=device)
+    return (torch.zeros(3, 4, 8, device=device), kc, torch.zeros_like(kc),
+            torch.zeros(3, 1, dtype=torch.int32, device=device),
+            torch.ones(3, dtype=torch.int32, device=device))
+
+
+def test_decode_sequence_order_and_workspace_must_be_device_tensors(meta_as_device) -> None:
+    """A host seq_order or workspace beside device tensors would hand a host address to the
+    kernel: every decode entry point rejects it, and a seq_order of the wrong length,
+    before anything is launched."""
+
+    meta = torch.device("meta")
+    args = _decode_args(meta)
+    good_order = torch.arange(3, dtype=torch.int32, device=meta)
+    ops.paged_attention_decode(*args, layer_index=0, max_seq_len=1, seq_order=good_order,
+                               workspace=torch.zeros(64, dtype=torch.uint8, device=meta))
+    ops.paged_attention_decode_noalloc(*args, layer_index=0, max_seq_len=1,
+                                       out=torch.zeros_like(args[0]), seq_order=good_order)
+    assert meta_as_device == ["paged_attention_decode", "paged_attention_decode_noalloc"]
+    meta_as_device.clear()
+    host_order = torch.arange(3, dtype=torch.int32)
+    for order, message in ((host_order, "requires HIP device tensors"),
+                           (torch.arange(4, dtype=torch.int32, device=meta),
+                            r"seq_order must have shape \(B,\)")):
+        with pytest.raises(ValueError, match=message):
+            ops.paged_attention_decode(*args, layer_index=0, max_seq_len=1, seq_order=order)
+        with pytest.raises(ValueError, match=message):
+            ops.paged_attention_decode_noalloc(*args, layer_index=0, max_seq_len=1,
+                                               out=torch.zeros_like(args[0]), seq_order=order)
+    for workspace, message in ((torch.zeros(64, dtype=torch.uint8), "requires HIP device"),
+                               (torch.zeros(16, device=meta), "contiguous uint8")):
+        with pytest.raises(ValueError, match=message):
+            ops.paged_attention_decode(*args, layer_index=0, max_seq_len=1, workspace=workspace)
+    assert meta_as_device == []
+
+
+def test_fused_decode_sequence_order_and_workspace_must_be_device_tensors(
+        meta_as_device) -> None:
+    meta = torch.device("meta")
+    query, kc, vc, tables, lens = _decode_args(meta)
+    table = ops.RotaryTable(8, theta=10_000.0, max_position=16, dtype=torch.float32,
+                            device=meta)
+    rows = (torch.zeros(3, 2, 8, device=meta), torch.zeros(3, 2, 8, device=meta),
+            torch.zeros(3, dtype=torch.int64, device=meta))
+
+    def call(**kwargs):
+        ops.rope_append_paged_decode(query, *rows[:2], rows[2], table, kc, vc,
+                                     torch.zeros(3, dtype=torch.int64, device=meta), tables,
+                                     lens, layer_index=0, max_seq_len=1, **kwargs)
+
+    call(seq_order=torch.arange(3, dtype=torch.int32, device=meta))
+    assert meta_as_device == ["rope_append_paged_decode"]
+    meta_as_device.clear()
+    with pytest.raises(ValueError, match="requires HIP device tensors"):
+        call(seq_order=torch.arange(3, dtype=torch.int32))
+    with pytest.raises(ValueError, match="requires HIP device tensors"):
+        call(workspace=torch.zeros(64, dtype=torch.uint8))
+    with pytest.raises(ValueError, match="contiguous uint8"):
+        call(workspace=torch.zeros(64, dtype=torch.int32, device=meta))
+    assert meta_as_device == []

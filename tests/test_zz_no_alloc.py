@@ -88,3 +88,45 @@ def test_no_alloc_decode_rejects_batches_beyond_the_static_buffer(device) -> Non
         0.1, 1, None, 0, 0, 2, None)
     assert status == _lib.TKS_ERR_WORKSPACE
     assert ctypes.c_int32(status).value == -4
+
+
+def test_no_alloc_decode_allocates_nothing_and_replays_in_a_graph(device) -> None:
+    """What the entry point is for: a multi-split batch (pages_per_split 2, so the split
+    partials go to the static buffer) leaves torch's allocated device memory unchanged
+    when called eagerly, and the call captured in a HIP graph gives the workspace entry's
+    output on every replay, with eager work and synchronisations between the replays."""
+
+    library = _lib.load()
+    batch = workloads.paged_batch([2049, 700, 160, 5], [1] * 4, num_q_heads=32,
+                                  num_kv_heads=8, head_dim=128, block_size=16,
+                                  dtype=torch.bfloat16, device=device, seed=63)
+    other = workloads.paged_batch([900, 31], [1] * 2, num_q_heads=32, num_kv_heads=8,
+                                  head_dim=128, block_size=16, dtype=torch.bfloat16,
+                                  device=device, seed=64)
+    expected = _with_workspace(library, batch, 2)
+    expected_other = _with_workspace(library, other, 2)
+    out = torch.empty_like(batch.query)
+    code = _lib.dtype_code(batch.query.dtype)
+    torch.cuda.synchronize()
+    before = torch.cuda.memory_allocated(device)
+    status = library.tks_paged_attention_decode_noalloc(*_args(batch, out, 2), code,
+                                                        _lib.stream_of(batch.query))
+    torch.cuda.synchronize()
+    assert status == _lib.TKS_OK
+    assert torch.cuda.memory_allocated(device) == before
+    assert torch.equal(out, expected)
+
+    captured = torch.zeros_like(batch.query)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        status = library.tks_paged_attention_decode_noalloc(
+            *_args(batch, captured, 2), code, _lib.stream_of(batch.query))
+    assert status == _lib.TKS_OK
+    for _ in range(3):
+        captured.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(captured, expected)
+        # An eager call on another batch between replays reuses the static buffer.
+        assert torch.equal(_no_alloc(library, other, 2), expected_other)
+        torch.cuda.synchronize()

@@ -20,10 +20,13 @@ An iteration runs in three phases:
              reservation back: the pool and every sequence are as before the
              call, and no request has changed;
   3. apply   tokens are appended and the metrics hooks fire, per request in
-             the reference's order: for each prefill, prefill_started,
-             prefill_finished and token_produced; then token_produced for
-             each decode. (The hooks of a prefill all fire after the packed
-             forward that served the whole iteration.)
+             the reference's order: for each prefill, prefill_finished and
+             token_produced; then token_produced for each decode.
+The prefill hooks bracket the forward that serves the prefill, as the
+reference's do (execution.py:39-50): prefill_started fires for every prefill
+of the iteration, in plan order, just before the packed forward, and
+prefill_finished once it has run, so a collector's prefill duration is the
+forward's (one forward serves them all, so their starts come together).
 Requests with max_new_tokens == 0 complete at prefill without a forward or
 hooks, as in the reference.
 
@@ -39,7 +42,6 @@ iteration i.
 
 from __future__ import annotations
 
-import weakref
 from collections.abc import Sequence
 from dataclasses import dataclass
 
@@ -105,6 +107,9 @@ class BatchExecutor:
         if checked.prefill or checked.decode:
             with self.manager.reservation() as reservation:
                 pre_work, dec_work = self._reserve(reservation, checked)
+                if metrics is not None:
+                    for request in checked.prefill:
+                        metrics.prefill_started(request.request_id)
                 tokens = self._forward(pre_work, dec_work, [*checked.prefill, *checked.decode])
                 reservation.commit()
         return self._apply(prefill, checked, tokens, metrics)
@@ -250,7 +255,6 @@ class BatchExecutor:
                 completed.append(request.request_id)
                 continue
             if metrics is not None:
-                metrics.prefill_started(request.request_id)
                 metrics.prefill_finished(request.request_id)
             request.mark_prefill_complete()
             _take(request, next(served), metrics, completed)
@@ -277,17 +281,16 @@ def _check_group(requests: Sequence[ScheduledRequest], kind: str) -> None:
             raise ValueError(f"{kind} requests must be running")
 
 
-# One executor per (cache manager, model), kept while the manager lives, so that
-# callers looping over execute_decode reuse its staging buffers and decode graphs.
-_executors: weakref.WeakKeyDictionary[PagedKVCacheManager, BatchExecutor] = (
-    weakref.WeakKeyDictionary())
-
-
 def _executor_for(model: LlamaModel, manager: PagedKVCacheManager) -> BatchExecutor:
-    executor = _executors.get(manager)
+    """The executor of (model, manager), so that callers looping over execute_decode
+    reuse its staging buffers and decode graphs. It is kept on the manager itself: the
+    two refer to each other, and the cycle (with the pools and graphs it holds) is
+    collected once the caller lets go of the manager."""
+
+    executor = getattr(manager, "_batch_executor", None)
     if executor is None or executor.model is not model:
         executor = BatchExecutor(model, manager)
-        _executors[manager] = executor
+        manager._batch_executor = executor
     return executor
 
 

@@ -34,7 +34,21 @@ if TYPE_CHECKING:
     from tokserve_amd.engine.paged.sequence_cache import SequencePagedKVCache
     from tokserve_amd.engine.paged.storage import PagedKVStorage
 
-__all__ = ["GroupedQueryAttention"]
+__all__ = ["GroupedQueryAttention", "reject_contiguous_cache"]
+
+
+def reject_contiguous_cache(cache: object, paged_cache: object) -> None:
+    """The `cache=` keyword of the reference's forwards (model.py:50,124,
+    attention.py:181) takes its contiguous per-sequence KV cache (engine/cache.py),
+    which this library does not provide: None is accepted, as the reference's default,
+    and any other value raises ValueError (with the reference's message when a paged
+    cache is given too)."""
+
+    if cache is None:
+        return
+    if paged_cache is not None:
+        raise ValueError("choose either contiguous or paged cache")
+    raise ValueError("contiguous KV caches are not supported; pass paged_cache instead")
 
 
 class GroupedQueryAttention(nn.Module):
@@ -62,13 +76,16 @@ class GroupedQueryAttention(nn.Module):
         inputs: torch.Tensor,
         positions: torch.Tensor,
         *,
+        cache: None = None,
         paged_cache: SequencePagedKVCache | None = None,
         layer_index: int | None = None,
     ) -> torch.Tensor:
-        """(1, T, D) -> (1, T, D) attention output for one sequence."""
+        """(1, T, D) -> (1, T, D) attention output for one sequence. `cache` must be
+        None (see reject_contiguous_cache)."""
 
         if inputs.ndim != 3:
             raise ValueError("inputs must have shape (B, T, D)")
+        reject_contiguous_cache(cache, paged_cache)
         if inputs.shape[0] < 1 or inputs.shape[1] < 1:
             raise ValueError("batch and sequence dimensions must be positive")
         if inputs.shape[-1] != self.hidden_size:

@@ -24,7 +24,7 @@ from typing import TYPE_CHECKING
 import torch
 from torch import nn
 
-from tokserve_amd.engine.attention import GroupedQueryAttention
+from tokserve_amd.engine.attention import GroupedQueryAttention, reject_contiguous_cache
 from tokserve_amd.engine.config import LlamaConfig
 from tokserve_amd.engine.kernel_backend import KernelBackend, check_backend
 from tokserve_amd.engine.layers import RMSNorm, SwiGLU
@@ -55,11 +55,16 @@ class LlamaDecoderBlock(nn.Module):
         inputs: torch.Tensor,
         positions: torch.Tensor,
         *,
+        cache: None = None,
         paged_cache: SequencePagedKVCache | None = None,
         layer_index: int | None = None,
     ) -> torch.Tensor:
+        """One block on (B, T, D) inputs; `cache` must be None (the reference's contiguous
+        cache is not provided, see reject_contiguous_cache)."""
+
         if inputs.ndim != 3:
             raise ValueError("inputs must have shape (B, T, D)")
+        reject_contiguous_cache(cache, paged_cache)
         if inputs.shape[-1] != self.hidden_size:
             raise ValueError("inputs must use the configured hidden_size")
         attended = self.self_attention(self.input_norm(inputs), positions,
@@ -100,13 +105,16 @@ class LlamaModel(nn.Module):
 
     @torch.inference_mode()
     def forward(
-        self, token_ids: torch.Tensor, *, paged_cache: SequencePagedKVCache | None = None
+        self, token_ids: torch.Tensor, *, cache: None = None,
+        paged_cache: SequencePagedKVCache | None = None,
     ) -> torch.Tensor:
         """token_ids (1, T) -> logits (1, T, V); with a paged cache the T tokens are
-        appended after its current_length positions (model.py:119-206)."""
+        appended after its current_length positions (model.py:119-206). `cache` must be
+        None (the reference's contiguous cache is not provided)."""
 
         if token_ids.ndim != 2:
             raise ValueError("token_ids must have shape (B, T)")
+        reject_contiguous_cache(cache, paged_cache)
         if token_ids.dtype not in (torch.int32, torch.int64):
             raise TypeError("token_ids must contain integers")
         batch, length = token_ids.shape

@@ -1,7 +1,7 @@
-"""Next-token selection (tokserve/generation/{greedy,sampling,temperature,top_k,top_p}.py).
+"""Next-token selection (tokserve/generation/{sampling,temperature,top_k,top_p}.py).
 
-Greedy selection, the hot path's, is the tks_argmax kernel: the first index of
-each row's maximum, NaN counting as the maximum, as torch.argmax. Sampling
+Greedy selection, the hot path's, is generation.greedy.select_greedy (the
+tks_argmax kernel). Sampling
 (temperature, top-k, top-p, multinomial with the request's own generator) uses
 torch's device ops in the reference's order; it is outside the measured path.
 """
@@ -10,23 +10,11 @@ from __future__ import annotations
 
 import torch
 
+from tokserve_amd.generation.greedy import select_greedy
 from tokserve_amd.generation.types import GenerationConfig
-from tokserve_amd.kernels import ops
 
 __all__ = ["select_greedy", "scale_temperature", "filter_top_k", "filter_top_p",
            "sample_from_logits", "select_next_token"]
-
-
-def select_greedy(logits: torch.Tensor) -> torch.Tensor:
-    """(B, V) logits -> (B, 1) int64 indices of the first row maximum."""
-
-    if logits.ndim != 2:
-        raise ValueError("logits must have shape (B, V)")
-    if logits.shape[0] < 1:
-        raise ValueError("logits must contain at least one batch row")
-    if logits.shape[1] < 1:
-        raise ValueError("vocabulary size must be positive")
-    return ops.greedy_argmax(logits)
 
 
 def scale_temperature(logits: torch.Tensor, temperature: float) -> torch.Tensor:

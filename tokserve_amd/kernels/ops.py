@@ -193,6 +193,30 @@ def longest_first(seq_lens: list[int], device: torch.device | str) -> torch.Tens
     return torch.tensor(order, dtype=torch.int32).to(device)
 
 
+def _seq_order(operation: str, query: torch.Tensor,
+               seq_order: torch.Tensor | None) -> torch.Tensor | None:
+    """A decode launch's sequence order: int32 (B,) on the query's device, or None."""
+
+    if seq_order is None:
+        return None
+    require_hip(operation, query, seq_order)
+    order = _int_tensor(seq_order, torch.int32, "seq_order")
+    if order.shape != (query.shape[0],):
+        raise ValueError("seq_order must have shape (B,)")
+    return order
+
+
+def _check_workspace(operation: str, query: torch.Tensor, workspace: torch.Tensor | None) -> None:
+    """A caller's split workspace: contiguous uint8 on the query's device (its size is
+    checked against the launch's partials by the library)."""
+
+    if workspace is None:
+        return
+    require_hip(operation, query, workspace)
+    if workspace.dtype != torch.uint8 or not workspace.is_contiguous():
+        raise ValueError("workspace must be a contiguous uint8 tensor")
+
+
 def paged_attention_decode(
     query: torch.Tensor,
     key_cache: torch.Tensor,
@@ -245,12 +269,8 @@ def paged_attention_decode(
         out = torch.empty(query.shape, dtype=query.dtype, device=query.device)
     if scale is None:
         scale = 1.0 / sqrt(head_dim)
-    order = None
-    if seq_order is not None:
-        require_hip("paged_attention_decode", query, seq_order)
-        order = _int_tensor(seq_order, torch.int32, "seq_order")
-        if order.shape != (num_seqs,):
-            raise ValueError("seq_order must have shape (B,)")
+    order = _seq_order("paged_attention_decode", query, seq_order)
+    _check_workspace("paged_attention_decode", query, workspace)
     _ops.paged_attention_decode(query, key_cache, value_cache, tables, lens, order, layer_index,
                                 max_seq_len, float(scale), pages_per_split, k_scale, v_scale, out,
                                 workspace)
@@ -291,7 +311,7 @@ def paged_attention_decode_noalloc(
     lens = _int_tensor(seq_lens, torch.int32, "seq_lens")
     if tables.ndim != 2 or tables.shape[0] != query.shape[0] or lens.shape != (query.shape[0],):
         raise ValueError("block_tables (B, max_blocks) and seq_lens (B,) must match query")
-    order = None if seq_order is None else _int_tensor(seq_order, torch.int32, "seq_order")
+    order = _seq_order("paged_attention_decode", query, seq_order)
     _ops.paged_attention_decode_noalloc(
         query, key_cache, value_cache, tables, lens, order, layer_index, max_seq_len,
         float(1.0 / sqrt(head_dim) if scale is None else scale), pages_per_split, out)
@@ -628,11 +648,8 @@ def rope_append_paged_decode(
         raise ValueError("out must match query and be contiguous in head_dim")
     if scale is None:
         scale = 1.0 / sqrt(head_dim)
-    order = None
-    if seq_order is not None:
-        order = _int_tensor(seq_order, torch.int32, "seq_order")
-        if order.shape != (num_seqs,):
-            raise ValueError("seq_order must have shape (B,)")
+    order = _seq_order("rope_append_paged_decode", query, seq_order)
+    _check_workspace("rope_append_paged_decode", query, workspace)
     _ops.rope_append_paged_decode(query, key, value, pos, table.cos, table.sin, slots, key_cache,
                                   value_cache, tables, lens, order, layer_index, max_seq_len,
                                   float(scale), pages_per_split, out, workspace, k_scale, v_scale)

@@ -11,7 +11,8 @@ Shapes (all block_size 16 unless noted):
                       count, tables from one random permutation.
   mixed_llama3_8b     16 prefill chunks of 512 tokens on prior contexts U[0, 2048]
                       plus 240 decodes on contexts U[256, 4096], Hq 32 / Hkv 8,
-                      Dh 128, bf16.
+                      Dh 128, bf16; step_new_rows gives the 8,432 K/V rows the
+                      step appends before attention.
 Random numbers come from a seeded CPU torch.Generator (small shapes) or a
 seeded device generator (pool contents of the large shapes), so a workload is
 a pure function of its seed.
@@ -227,6 +228,38 @@ def mixed_llama3_8b(
         cu_seqlens_q=cu_dec, contexts=contexts[chunks:], query_lens=qlens[chunks:],
     )
     return prefill, decode
+
+
+@dataclass
+class NewRows:
+    """The K/V rows one step appends: row i goes to pool slot slots[i]."""
+
+    key: torch.Tensor         # (N, Hkv, Dh)
+    value: torch.Tensor       # (N, Hkv, Dh)
+    slots: torch.Tensor       # (N,) int64: block_id * block_size + offset
+
+
+def step_new_rows(parts: list[PagedBatch], *, seed: int = 3) -> NewRows:
+    """The new K/V rows of a step over `parts` (e.g. the prefill and decode halves of
+    mixed_llama3_8b): every query token of every sequence, in packed order, at its
+    position (the last query_lens[b] of the contexts[b] positions), slot from the
+    sequence's block table. Values N(0, 1) from a device generator seeded `seed`,
+    rounded to the pool's model dtype (the query dtype)."""
+
+    first = parts[0]
+    device = first.query.device
+    _, _, hkv, bs, dh = first.key_cache.shape
+    slots: list[int] = []
+    for part in parts:
+        tables = part.block_tables.cpu()
+        for b, (ctx, ql) in enumerate(zip(part.contexts, part.query_lens)):
+            row = tables[b].tolist()
+            slots.extend(row[p // bs] * bs + p % bs for p in range(ctx - ql, ctx))
+    n = len(slots)
+    gen = torch.Generator(device=device).manual_seed(seed)
+    key = torch.randn((n, hkv, dh), generator=gen, device=device).to(first.query.dtype)
+    value = torch.randn((n, hkv, dh), generator=gen, device=device).to(first.query.dtype)
+    return NewRows(key, value, torch.tensor(slots, dtype=torch.int64, device=device))
 
 
 @dataclass
