@@ -552,6 +552,7 @@ def measure_mixed(device, steps: int, warmup: int, kv_dtype=None,
     out_p = torch.empty_like(pre.query)
     out_d = torch.empty_like(dec.query)
     order = ops.longest_first(dec.contexts, device)
+    pre_order = ops.longest_first(pre.contexts, device)
     # The step's new K/V rows (every prefill token and every decode token, 8,432 rows),
     # scattered through slot_mapping into their sequences' paged blocks before attention.
     rows = workloads.step_new_rows([pre, dec])
@@ -564,7 +565,7 @@ def measure_mixed(device, steps: int, warmup: int, kv_dtype=None,
         ops.paged_attention_prefill(
             pre.query, pre.key_cache, pre.value_cache, pre.block_tables, pre.seq_lens,
             pre.cu_seqlens_q, layer_index=0, max_query_len=pre.max_query_len,
-            max_seq_len=pre.max_seq_len, out=out_p, **scales)
+            max_seq_len=pre.max_seq_len, out=out_p, seq_order=pre_order, **scales)
 
     def decode() -> None:
         ops.paged_attention_decode(

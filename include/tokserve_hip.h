@@ -222,6 +222,11 @@ int32_t tks_paged_attention_decode_noalloc(
  * Token n, head hq: query[n*q_token_stride + hq*q_head_stride + d], same for out.
  * num_tokens (host) == cu_seqlens_q[num_seqs]; max_query_len and max_seq_len
  * (host) bound the per-sequence query and key lengths.
+ * seq_order (device int32 [num_seqs], may be NULL): the order in which
+ * sequences (with all their query tiles) are handed to workgroups, a
+ * permutation of 0..num_seqs-1, as for decode. Passing the sequences with the
+ * most keys first shortens the tail of long chunks started last; results do
+ * not depend on it.
  */
 int32_t tks_paged_attention_prefill(const void *query, int64_t q_token_stride,
                                     int64_t q_head_stride, const void *key_cache,
@@ -230,7 +235,7 @@ int32_t tks_paged_attention_prefill(const void *query, int64_t q_token_stride,
                                     int32_t head_dim, int32_t layer_index,
                                     const int32_t *block_tables, int32_t block_table_stride,
                                     const int32_t *seq_lens, const int32_t *cu_seqlens_q,
-                                    int32_t num_seqs, int64_t num_tokens, int32_t num_q_heads,
+                                    const int32_t *seq_order, int32_t num_seqs, int64_t num_tokens, int32_t num_q_heads,
                                     int32_t max_query_len,
                                     int32_t max_seq_len, float scale, void *out,
                                     int64_t out_token_stride, int64_t out_head_stride,
@@ -299,8 +304,8 @@ int32_t tks_paged_attention_prefill_fp8(
     const void *value_cache, int32_t num_layers, int64_t num_blocks, int32_t num_kv_heads,
     int32_t block_size, int32_t head_dim, int32_t layer_index, const int32_t *block_tables,
     int32_t block_table_stride, const int32_t *seq_lens, const int32_t *cu_seqlens_q,
-    int32_t num_seqs, int64_t num_tokens, int32_t num_q_heads, int32_t max_query_len,
-    int32_t max_seq_len, float scale, void *out, int64_t out_token_stride,
+    const int32_t *seq_order, int32_t num_seqs, int64_t num_tokens, int32_t num_q_heads,
+    int32_t max_query_len, int32_t max_seq_len, float scale, void *out, int64_t out_token_stride,
     int64_t out_head_stride, void *workspace, int64_t workspace_bytes, float k_scale,
     float v_scale, int32_t dtype, tks_stream_t stream);
 

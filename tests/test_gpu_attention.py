@@ -7,14 +7,14 @@ one rounding on the store) and its torch backend's (a rounding to the dtype afte
 every op). The oracle is the reference's torch backend (gather + repeat_kv +
 causal_attention, oracle/paged.py) run in either arithmetic.
 
-Against the torch backend, 2e-2 absolute is asserted as it stands on the
-benchmark-shaped batches (the whole 256-sequence Llama-3-8B decode batch, the
-whole mixed step, long contexts), whose outputs average many keys and stay
-small. The short synthetic cases (a handful of keys, |o| up to ~4) add one step of the stored dtype at the
-element's magnitude (bf16 2^-7 relative, fp16 2^-10): one bf16 step at |o| in
+Against the torch backend, 2e-2 absolute is asserted as it stands on the benchmark-
+shaped batches (the whole 256-sequence Llama-3-8B decode batch, the whole mixed
+step, long contexts), whose outputs average many keys and stay small. The short
+synthetic cases (a handful of keys, |o| up to ~4) add one step of the stored dtype
+at the element's magnitude (bf16 2^-7 relative, fp16 2^-10): one bf16 step at |o| in
 [2, 4) is 0.0156, and the torch backend's own roundings put it up to 0.0234 away
-from the fp32 arithmetic on these cases (measured on the CPU), so two correct
-bf16 results can differ by more than 2e-2 there.
+from the fp32 arithmetic on these cases (measured on the CPU), so two correct bf16
+results can differ by more than 2e-2 there.
 """
 
 import pytest
@@ -277,13 +277,40 @@ def test_mixed_step_full_size_matches_oracle(device) -> None:
     k_ref, v_ref = pre.key_cache.cpu(), pre.value_cache.cpu()
     kvslots.kv_append(rows.key.cpu(), rows.value.cpu(), k_ref, v_ref, rows.slots.cpu(), 0)
     ops.kv_append(rows.key, rows.value, pre.key_cache, pre.value_cache, rows.slots, 0)
-    out_p = _prefill(pre)
+    out_p = ops.paged_attention_prefill(
+        pre.query, pre.key_cache, pre.value_cache, pre.block_tables, pre.seq_lens,
+        pre.cu_seqlens_q, layer_index=0, max_query_len=pre.max_query_len,
+        max_seq_len=pre.max_seq_len, seq_order=ops.longest_first(pre.contexts, device))
     out_d = _decode(dec, seq_order=ops.longest_first(dec.contexts, device))
     torch.cuda.synchronize()
     assert torch.equal(pre.key_cache.cpu(), k_ref)
     assert torch.equal(pre.value_cache.cpu(), v_ref)
     _assert_parity(out_p, _prefill_oracle, pre, strict=True)
     _assert_parity(out_d, _decode_oracle, dec, strict=True)
+
+
+@pytest.mark.parametrize(("hq", "hkv", "dh"), [(32, 8, 128), (32, 4, 64)])
+def test_prefill_sequence_order_does_not_change_results(device, hq, hkv, dh) -> None:
+    """The prefill's sequence order (most keys first, or reversed) only changes which
+    workgroups start first: outputs are bit-identical to the natural order."""
+
+    contexts, qlens = [300, 2000, 40, 700, 1, 513], [100, 512, 40, 64, 1, 513]
+    batch = workloads.paged_batch(contexts, qlens, num_q_heads=hq, num_kv_heads=hkv,
+                                  head_dim=dh, block_size=16, dtype=torch.bfloat16,
+                                  device=device, seed=23)
+    natural = _prefill(batch)
+    results = []
+    for order in (ops.longest_first(contexts, device),
+                  torch.arange(5, -1, -1, dtype=torch.int32, device=device)):
+        results.append(ops.paged_attention_prefill(
+            batch.query, batch.key_cache, batch.value_cache, batch.block_tables,
+            batch.seq_lens, batch.cu_seqlens_q, layer_index=0,
+            max_query_len=batch.max_query_len, max_seq_len=batch.max_seq_len,
+            seq_order=order))
+    torch.cuda.synchronize()
+    for planned in results:
+        assert torch.equal(planned, natural)
+    _assert_parity(natural, _prefill_oracle, batch)
 
 
 def test_mixed_step_other_seed_subset_matches_oracle(device) -> None:

@@ -118,7 +118,8 @@ class DecodeGraphs:
         empty32 = torch.empty(0, dtype=torch.int32, device=self.device)
         return PackedBatch(
             num_prefill_tokens=0, prefill_cu_seqlens_q=empty32, prefill_seq_lens=empty32,
-            prefill_block_tables=empty32.view(0, 1), prefill_max_query_len=0,
+            prefill_block_tables=empty32.view(0, 1), prefill_seq_order=empty32,
+            prefill_max_query_len=0,
             prefill_max_seq_len=0, decode_max_seq_len=w * self.block_size, **views)
 
     def _upload(self, host: np.ndarray, static: torch.Tensor, b: int,

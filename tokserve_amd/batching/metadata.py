@@ -10,7 +10,8 @@ names of the hot path):
   positions      (N,) int64   absolute position of each row
   slot_mapping   (N,) int64   pool slot block_ids[p // BS] * BS + p % BS of each row
   prefill_*      cu_seqlens_q (Bp+1,) int32, seq_lens (Bp,) int32 (keys after
-                 the append), block_tables (Bp, W) int32
+                 the append), block_tables (Bp, W) int32, seq_order (Bp,) int32
+                 (most keys first, the order chunks reach the GPU)
   decode_*       seq_lens (Bd,) int32, block_tables (Bd, W) int32, seq_order
                  (Bd,) int32 (longest first, the order sequences reach the GPU)
   logits_rows    (B,) int64   row of each sequence's last token
@@ -52,6 +53,7 @@ class PackedBatch:
     prefill_block_tables: torch.Tensor
     prefill_max_query_len: int
     prefill_max_seq_len: int
+    prefill_seq_order: torch.Tensor
     decode_seq_lens: torch.Tensor
     decode_block_tables: torch.Tensor
     decode_seq_order: torch.Tensor
@@ -111,12 +113,14 @@ class PackedBatchBuilder:
         cu = offsets[: n_pre + 1].astype(np.int32)
         dec_lens = ends[n_pre:].astype(np.int32)
         order = np.argsort(-dec_lens, kind="stable").astype(np.int32)
+        pre_order = np.argsort(-ends[:n_pre], kind="stable").astype(np.int32)
 
         sections = [
             ("token_ids", token_ids), ("positions", positions.astype(np.int64)),
             ("slot_mapping", slot_mapping), ("logits_rows", logits_rows.astype(np.int64)),
             ("prefill_cu_seqlens_q", cu), ("prefill_seq_lens", ends[:n_pre].astype(np.int32)),
-            ("prefill_block_tables", tables[:n_pre]), ("decode_seq_lens", dec_lens),
+            ("prefill_block_tables", tables[:n_pre]), ("prefill_seq_order", pre_order),
+            ("decode_seq_lens", dec_lens),
             ("decode_block_tables", tables[n_pre:]), ("decode_seq_order", order),
         ]
         layout = []

@@ -188,6 +188,8 @@ struct PrefillArgs {
   int32_t num_pairs;  // sequences * KV heads
   int32_t tiles;      // query tiles per (sequence, KV head): ceil(max_query_len / tile)
   float v_scale = 1.f;  // V decode factor (pages decoded from fp8 pools; 1 otherwise)
+  const int32_t *seq_order = nullptr;  // rank -> sequence (null: identity)
+  int32_t num_seqs = 0;
 };
 
 // 16-key pages of one sequence the MFMA prefill kernel holds in LDS: it serves

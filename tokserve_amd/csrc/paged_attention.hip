@@ -654,10 +654,10 @@ int32_t prefill_impl(const void *query, int64_t q_token_stride, int64_t q_head_s
                      int64_t num_blocks, int32_t num_kv_heads, int32_t block_size,
                      int32_t head_dim, int32_t layer_index, const int32_t *block_tables,
                      int32_t block_table_stride, const int32_t *seq_lens,
-                     const int32_t *cu_seqlens_q, int32_t num_seqs, int64_t num_tokens,
-                     int32_t num_q_heads, int32_t max_query_len, int32_t max_seq_len,
-                     float scale, void *out, int64_t out_token_stride, int64_t out_head_stride,
-                     bool fp8_pools, void *workspace, int64_t workspace_bytes, float k_scale,
+                     const int32_t *cu_seqlens_q, const int32_t *seq_order, int32_t num_seqs,
+                     int64_t num_tokens, int32_t num_q_heads, int32_t max_query_len,
+                     int32_t max_seq_len, float scale, void *out, int64_t out_token_stride,
+                     int64_t out_head_stride, bool fp8_pools, void *workspace, int64_t workspace_bytes, float k_scale,
                      float v_scale, int32_t dtype, tks_stream_t stream) {
   if (!valid_dtype(dtype)) return TKS_ERR_TYPE;
   if (!pool_ok(num_layers, num_blocks, num_kv_heads, block_size, head_dim) || num_seqs < 0 ||
@@ -692,6 +692,8 @@ int32_t prefill_impl(const void *query, int64_t q_token_stride, int64_t q_head_s
     PrefillArgs p{query,    q_token_stride, q_head_stride, key_cache,    value_cache,
                   pool,     block_tables,   block_table_stride, seq_lens, cu_seqlens_q,
                   scale_log2, key_cap,      out,           out_token_stride, out_head_stride};
+    p.seq_order = seq_order;
+    p.num_seqs = num_seqs;
     return launch_prefill_mfma(p, dtype, num_seqs, num_kv_heads, G, head_dim, max_query_len, s);
   }
   if (mfma_shape) {
@@ -720,6 +722,8 @@ int32_t prefill_impl(const void *query, int64_t q_token_stride, int64_t q_head_s
                   scratch,  sp.table,       block_table_stride, seq_lens, cu_seqlens_q,
                   scale_log2, key_cap,      out,           out_token_stride, out_head_stride};
     p.v_scale = v_scale;
+    p.seq_order = seq_order;
+    p.num_seqs = num_seqs;
     return launch_prefill_mfma(p, dtype, num_seqs, num_kv_heads, G, head_dim, max_query_len, s);
   }
   const int kv_elem = fp8_pools ? 1 : elem_bytes(dtype);
@@ -900,12 +904,12 @@ extern "C" int32_t tks_paged_attention_prefill(
     const void *value_cache, int32_t num_layers, int64_t num_blocks, int32_t num_kv_heads,
     int32_t block_size, int32_t head_dim, int32_t layer_index, const int32_t *block_tables,
     int32_t block_table_stride, const int32_t *seq_lens, const int32_t *cu_seqlens_q,
-    int32_t num_seqs, int64_t num_tokens, int32_t num_q_heads, int32_t max_query_len,
-    int32_t max_seq_len, float scale, void *out, int64_t out_token_stride,
+    const int32_t *seq_order, int32_t num_seqs, int64_t num_tokens, int32_t num_q_heads,
+    int32_t max_query_len, int32_t max_seq_len, float scale, void *out, int64_t out_token_stride,
     int64_t out_head_stride, int32_t dtype, tks_stream_t stream) {
   return prefill_impl(query, q_token_stride, q_head_stride, key_cache, value_cache, num_layers,
                       num_blocks, num_kv_heads, block_size, head_dim, layer_index, block_tables,
-                      block_table_stride, seq_lens, cu_seqlens_q, num_seqs, num_tokens,
+                      block_table_stride, seq_lens, cu_seqlens_q, seq_order, num_seqs, num_tokens,
                       num_q_heads, max_query_len, max_seq_len, scale, out, out_token_stride,
                       out_head_stride, false, nullptr, 0, 1.f, 1.f, dtype, stream);
 }
@@ -932,13 +936,13 @@ extern "C" int32_t tks_paged_attention_prefill_fp8(
     const void *value_cache, int32_t num_layers, int64_t num_blocks, int32_t num_kv_heads,
     int32_t block_size, int32_t head_dim, int32_t layer_index, const int32_t *block_tables,
     int32_t block_table_stride, const int32_t *seq_lens, const int32_t *cu_seqlens_q,
-    int32_t num_seqs, int64_t num_tokens, int32_t num_q_heads, int32_t max_query_len,
-    int32_t max_seq_len, float scale, void *out, int64_t out_token_stride,
+    const int32_t *seq_order, int32_t num_seqs, int64_t num_tokens, int32_t num_q_heads,
+    int32_t max_query_len, int32_t max_seq_len, float scale, void *out, int64_t out_token_stride,
     int64_t out_head_stride, void *workspace, int64_t workspace_bytes, float k_scale,
     float v_scale, int32_t dtype, tks_stream_t stream) {
   return prefill_impl(query, q_token_stride, q_head_stride, key_cache, value_cache, num_layers,
                       num_blocks, num_kv_heads, block_size, head_dim, layer_index, block_tables,
-                      block_table_stride, seq_lens, cu_seqlens_q, num_seqs, num_tokens,
+                      block_table_stride, seq_lens, cu_seqlens_q, seq_order, num_seqs, num_tokens,
                       num_q_heads, max_query_len, max_seq_len, scale, out, out_token_stride,
                       out_head_stride, true, workspace, workspace_bytes, k_scale, v_scale, dtype,
                       stream);

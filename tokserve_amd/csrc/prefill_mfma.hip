@@ -309,7 +309,8 @@ __global__ __launch_bounds__(64 * kPWaves) __attribute__((amdgpu_waves_per_eu(
   if (pair >= a.num_pairs) return;
   const int tile = a.tiles - 1 - slot % a.tiles;
   const int kvh = pair % a.num_kv_heads;
-  const int b = pair / a.num_kv_heads;
+  const int rank = pair / a.num_kv_heads;
+  const int b = a.seq_order ? min(max(a.seq_order[rank], 0), a.num_seqs - 1) : rank;
   const int q0 = a.cu_q[b];
   const int q_len = a.cu_q[b + 1] - q0;
   const int t0 = tile * QT;

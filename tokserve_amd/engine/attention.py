@@ -169,7 +169,8 @@ class GroupedQueryAttention(nn.Module):
                 query[:split], storage.key_storage, storage.value_storage,
                 batch.prefill_block_tables, batch.prefill_seq_lens, batch.prefill_cu_seqlens_q,
                 layer_index=layer_index, max_query_len=batch.prefill_max_query_len,
-                max_seq_len=batch.prefill_max_seq_len, out=attended[:split], **storage.scales,
+                max_seq_len=batch.prefill_max_seq_len, out=attended[:split],
+                seq_order=batch.prefill_seq_order, **storage.scales,
             )
         if split < tokens:
             ops.paged_attention_decode(

@@ -15,7 +15,7 @@ from pathlib import Path
 import torch
 
 LIBRARY_NAME = "libtokserve_hip.so"
-ABI_VERSION = 10
+ABI_VERSION = 11
 
 TKS_OK = 0
 TKS_ERR_VALUE = -1
@@ -83,7 +83,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "tks_paged_attention_prefill": (
         _i32,
         [_c_void_p, _i64, _i64, _c_void_p, _c_void_p, _i32, _i64, _i32, _i32, _i32, _i32,
-         _c_void_p, _i32, _c_void_p, _c_void_p, _i32, _i64, _i32, _i32, _i32, _f32,
+         _c_void_p, _i32, _c_void_p, _c_void_p, _c_void_p, _i32, _i64, _i32, _i32, _i32, _f32,
          _c_void_p, _i64, _i64, _i32, _c_void_p],
     ),
     "tks_rms_norm": (
@@ -139,7 +139,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "tks_paged_attention_prefill_fp8": (
         _i32,
         [_c_void_p, _i64, _i64, _c_void_p, _c_void_p, _i32, _i64, _i32, _i32, _i32, _i32,
-         _c_void_p, _i32, _c_void_p, _c_void_p, _i32, _i64, _i32, _i32, _i32, _f32,
+         _c_void_p, _i32, _c_void_p, _c_void_p, _c_void_p, _i32, _i64, _i32, _i32, _i32, _f32,
          _c_void_p, _i64, _i64, _c_void_p, _i64, _f32, _f32, _i32, _c_void_p],
     ),
 }

@@ -183,7 +183,7 @@ def decode_workspace_bytes(
 
 
 def longest_first(seq_lens: list[int], device: torch.device | str) -> torch.Tensor:
-    """Host-side decode plan: sequence indices by decreasing length (int32, on device).
+    """Host-side launch plan: sequence indices by decreasing length (int32, on device).
 
     Built from the lengths the scheduler already holds on the host; ties keep
     batch order so the plan is deterministic.
@@ -193,15 +193,16 @@ def longest_first(seq_lens: list[int], device: torch.device | str) -> torch.Tens
     return torch.tensor(order, dtype=torch.int32).to(device)
 
 
-def _seq_order(operation: str, query: torch.Tensor,
+def _seq_order(operation: str, like: torch.Tensor,
                seq_order: torch.Tensor | None) -> torch.Tensor | None:
-    """A decode launch's sequence order: int32 (B,) on the query's device, or None."""
+    """A launch's sequence order: int32 (B,) on the device of `like` (B = like.shape[0],
+    the decode query or the seq_lens), or None."""
 
     if seq_order is None:
         return None
-    require_hip(operation, query, seq_order)
+    require_hip(operation, like, seq_order)
     order = _int_tensor(seq_order, torch.int32, "seq_order")
-    if order.shape != (query.shape[0],):
+    if order.shape != (like.shape[0],):
         raise ValueError("seq_order must have shape (B,)")
     return order
 
@@ -331,6 +332,7 @@ def paged_attention_prefill(
     max_seq_len: int,
     scale: float | None = None,
     out: torch.Tensor | None = None,
+    seq_order: torch.Tensor | None = None,
     k_scale: float = 1.0,
     v_scale: float = 1.0,
 ) -> torch.Tensor:
@@ -338,7 +340,9 @@ def paged_attention_prefill(
 
     Sequence b owns query rows cu_seqlens_q[b] .. cu_seqlens_q[b+1]-1; its
     seq_lens[b] keys already include those rows, so query i sits at absolute
-    position seq_lens[b] - q_len_b + i. fp8 pools are decoded with
+    position seq_lens[b] - q_len_b + i. `seq_order` (int32 permutation of 0..B-1,
+    e.g. longest_first of seq_lens) is the order in which sequences reach
+    workgroups; results do not depend on it. fp8 pools are decoded with
     (k_scale, v_scale).
     """
 
@@ -369,8 +373,10 @@ def paged_attention_prefill(
         out = torch.empty(query.shape, dtype=query.dtype, device=query.device)
     if scale is None:
         scale = 1.0 / sqrt(head_dim)
-    _ops.paged_attention_prefill(query, key_cache, value_cache, tables, lens, cu, layer_index,
-                                 max_query_len, max_seq_len, float(scale), k_scale, v_scale, out)
+    order = _seq_order("paged_attention_prefill", lens, seq_order)
+    _ops.paged_attention_prefill(query, key_cache, value_cache, tables, lens, cu, order,
+                                 layer_index, max_query_len, max_seq_len, float(scale), k_scale,
+                                 v_scale, out)
     return out
 
 

@@ -66,7 +66,8 @@ SCHEMAS = {
     ),
     "paged_attention_prefill": (
         "paged_attention_prefill(Tensor query, Tensor key_cache, Tensor value_cache, "
-        "Tensor block_tables, Tensor seq_lens, Tensor cu_seqlens_q, int layer_index, "
+        "Tensor block_tables, Tensor seq_lens, Tensor cu_seqlens_q, Tensor? seq_order, "
+        "int layer_index, "
         "int max_query_len, int max_seq_len, float scale, float k_scale, float v_scale, "
         "Tensor(a!) out) -> ()"
     ),
@@ -249,14 +250,15 @@ def _paged_attention_decode_noalloc(query, key_cache, value_cache, block_tables,
 
 
 def _paged_attention_prefill(query, key_cache, value_cache, block_tables, seq_lens,
-                             cu_seqlens_q, layer_index, max_query_len, max_seq_len, scale,
-                             k_scale, v_scale, out):
+                             cu_seqlens_q, seq_order, layer_index, max_query_len, max_seq_len,
+                             scale, k_scale, v_scale, out):
     dims = _pool_dims(key_cache)
     num_seqs = seq_lens.shape[0]
     common = (query.data_ptr(), query.stride(0), query.stride(1),
               key_cache.data_ptr(), value_cache.data_ptr(), *dims, layer_index,
               block_tables.data_ptr(), block_tables.shape[1], seq_lens.data_ptr(),
-              cu_seqlens_q.data_ptr(), num_seqs, query.shape[0], query.shape[1],
+              cu_seqlens_q.data_ptr(), _lib.ptr(seq_order), num_seqs, query.shape[0],
+              query.shape[1],
               max_query_len, max_seq_len, scale, out.data_ptr(), out.stride(0), out.stride(1))
     library = _lib.load()
     if key_cache.dtype == FP8_POOL_DTYPE:
