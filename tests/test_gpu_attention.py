@@ -7,9 +7,9 @@ one rounding on the store) and its torch backend's (a rounding to the dtype afte
 every op). The oracle is the reference's torch backend (gather + repeat_kv +
 causal_attention, oracle/paged.py) run in either arithmetic.
 
-Against the torch backend, 2e-2 absolute is asserted as it stands on the benchmark-
-shaped batches (the whole 256-sequence Llama-3-8B decode batch, the whole mixed
-step, long contexts), whose outputs average many keys and stay small. The short
+Against the torch backend, 2e-2 absolute is asserted as it stands on the
+benchmark-shaped batches (the whole 256-sequence Llama-3-8B decode batch, the whole
+mixed step, long contexts), whose outputs average many keys and stay small. The short
 synthetic cases (a handful of keys, |o| up to ~4) add one step of the stored dtype
 at the element's magnitude (bf16 2^-7 relative, fp16 2^-10): one bf16 step at |o| in
 [2, 4) is 0.0156, and the torch backend's own roundings put it up to 0.0234 away
