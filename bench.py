@@ -30,10 +30,10 @@ TRAFFIC_FILE = ROOT / "profiles" / "decode_llama3_8b_traffic.txt"
 
 
 def algorithmic_bytes(batch) -> int:
-    """Every visible K/V byte once, Q in and O out, block ids and lengths."""
+    """Every visible K/V byte once (with its row scale when the pools have per-row
+    scales), Q in and O out, block ids and lengths."""
 
-    _, _, hkv, _, dh = batch.key_cache.shape
-    kv = sum(batch.contexts) * hkv * dh * 2 * batch.key_cache.element_size()
+    kv = batch.kv_bytes_read()
     qo = 2 * batch.query.numel() * batch.query.element_size()
     tables = sum((c + 15) // 16 for c in batch.contexts) * 4
     return kv + qo + tables + 4 * batch.num_seqs
@@ -443,6 +443,8 @@ def main() -> int:
             "small_fp32_step": lambda: measure_small_fp32_step(device, 50, 10,
                                                                cpu_seconds=cpu_or(2.0)),
             "decode_fp8_kv": lambda: measure_decode_fp8(device, args.seed, 50, 10),
+            "decode_fp8_kv_rows": lambda: measure_decode_fp8(device, args.seed, 50, 10,
+                                                             rows=True),
             "decode_small_batches": lambda: measure_decode_small_batches(device, args.seed, 50,
                                                                          10),
             "decode_serving_shape": lambda: measure_decode_serving_shape(device, args.seed, 50,
@@ -703,16 +705,20 @@ def measure_prefill_long(device, seconds: float = 1.0) -> dict:
     return result
 
 
-def measure_decode_fp8(device, seed: int, steps: int, warmup: int) -> dict:
+def measure_decode_fp8(device, seed: int, steps: int, warmup: int, rows: bool = False) -> dict:
     """The headline decode workload with fp8 e4m3 K/V pools (bf16 queries and output):
-    half the K/V bytes per decode token."""
+    half the K/V bytes per decode token. rows: one fp32 scale per pool row, whose
+    4 bytes per key row count in the algorithmic bytes."""
 
     import torch
 
     from tokserve_amd import workloads
     from tokserve_amd.kernels import ops
 
-    batch = workloads.decode_llama3_8b_fp8(device, seed=seed)
+    if rows:
+        batch = workloads.decode_llama3_8b_fp8_rows(device, seed=seed)
+    else:
+        batch = workloads.decode_llama3_8b_fp8(device, seed=seed)
     out = torch.empty_like(batch.query)
     order = ops.longest_first(batch.contexts, device)
 
@@ -720,14 +726,16 @@ def measure_decode_fp8(device, seed: int, steps: int, warmup: int) -> dict:
         ops.paged_attention_decode(
             batch.query, batch.key_cache, batch.value_cache, batch.block_tables,
             batch.seq_lens, layer_index=0, max_seq_len=batch.max_seq_len, out=out,
-            seq_order=order, k_scale=batch.k_scale, v_scale=batch.v_scale)
+            seq_order=order, **batch.scale_kwargs)
 
     ms = _time_ms(step, steps, warmup)
     nbytes = algorithmic_bytes(batch)
+    scales = ("one fp32 scale per pool row (rows scaled by 2^U[-6, 0] first)" if rows
+              else "one scale per pool")
     return {
         "workload": "decode_llama3_8b_fp8: the headline decode batch (256 seqs, ctx "
                     "log-uniform [128, 8192], Hq 32 / Hkv 8, Dh 128, block 16) with e4m3 K/V "
-                    "pools, bf16 queries",
+                    f"pools, {scales}, bf16 queries",
         "ms_per_step": round(ms, 5),
         "algorithmic_bytes": nbytes,
         "gbps": round(nbytes / (ms * 1e-3) / 1e9, 1),

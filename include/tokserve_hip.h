@@ -327,6 +327,90 @@ int32_t tks_rope_append_paged_decode_fp8(
     tks_stream_t stream);
 
 /* ------------------------------------------------------------------------
+ * fp8 K/V pools with one fp32 scale per pool row (a further variant behind
+ * PagedKVStorage, tokserve/engine/paged/storage.py:40-56, where the reference
+ * keeps pools in the model dtype). Codes as above in [L, NB, Hkv, BS, Dh];
+ * k_scales and v_scales are float [L, NB, Hkv, BS] beside them, one per (token,
+ * KV head) slot, written by the appends:
+ *   s       = amax / 448, amax = max |x_d| over the row's Dh values (NaN if one
+ *             is NaN), and s = 1 where that is 0, NaN or infinite
+ *   stored  = e4m3(clamp(x / s, -448, 448))   round to nearest even, NaN kept
+ *   decoded = float(stored) * s
+ * x is the row in `dtype` (the rotated key row rounded to `dtype` when RoPE is
+ * fused in). Every entry takes the arguments of its per-pool-scale counterpart
+ * with the two scale arrays in place of k_scale and v_scale; attention computes
+ * exactly the function of its counterpart on the decoded pools, in fp32, with
+ * each key's scale applied to its scores and each value's to its probabilities.
+ * Rows no sequence has written are never read into an output (their codes and
+ * scales may hold anything). The decode's fused RoPE + append runs as the append
+ * launch followed by the attention launch.
+ */
+int32_t tks_kv_append_fp8_rows(const void *key, int64_t key_token_stride,
+                               int64_t key_head_stride, const void *value,
+                               int64_t value_token_stride, int64_t value_head_stride,
+                               int64_t num_tokens, void *key_cache, void *value_cache,
+                               float *k_scales, float *v_scales, int32_t num_layers,
+                               int64_t num_blocks, int32_t num_kv_heads, int32_t block_size,
+                               int32_t head_dim, int32_t layer_index, const int64_t *slot_mapping,
+                               int32_t dtype, tks_stream_t stream);
+
+int32_t tks_paged_gather_fp8_rows(const void *key_cache, const void *value_cache,
+                                  const float *k_scales, const float *v_scales, int32_t num_layers,
+                                  int64_t num_blocks, int32_t num_kv_heads, int32_t block_size,
+                                  int32_t head_dim, int32_t layer_index,
+                                  const int32_t *block_tables, int32_t block_table_stride,
+                                  const int32_t *seq_lens, const int32_t *cu_seqlens,
+                                  int32_t num_seqs, int32_t max_seq_len, void *key_out,
+                                  void *value_out, int64_t out_token_stride,
+                                  int64_t out_head_stride, int32_t dtype, tks_stream_t stream);
+
+int32_t tks_paged_attention_decode_fp8_rows(
+    const void *query, int64_t q_seq_stride, int64_t q_head_stride, const void *key_cache,
+    const void *value_cache, const float *k_scales, const float *v_scales, int32_t num_layers,
+    int64_t num_blocks, int32_t num_kv_heads, int32_t block_size, int32_t head_dim,
+    int32_t layer_index, const int32_t *block_tables, int32_t block_table_stride,
+    const int32_t *seq_lens, const int32_t *seq_order, int32_t num_seqs, int32_t num_q_heads,
+    int32_t max_seq_len, float scale, int32_t pages_per_split, void *out,
+    int64_t out_seq_stride, int64_t out_head_stride, void *workspace, int64_t workspace_bytes,
+    int32_t dtype, tks_stream_t stream);
+
+/* The workspace size is tks_paged_attention_prefill_fp8_workspace_bytes'. */
+int32_t tks_paged_attention_prefill_fp8_rows(
+    const void *query, int64_t q_token_stride, int64_t q_head_stride, const void *key_cache,
+    const void *value_cache, const float *k_scales, const float *v_scales, int32_t num_layers,
+    int64_t num_blocks, int32_t num_kv_heads, int32_t block_size, int32_t head_dim,
+    int32_t layer_index, const int32_t *block_tables, int32_t block_table_stride,
+    const int32_t *seq_lens, const int32_t *cu_seqlens_q, const int32_t *seq_order,
+    int32_t num_seqs, int64_t num_tokens, int32_t num_q_heads, int32_t max_query_len,
+    int32_t max_seq_len, float scale, void *out, int64_t out_token_stride,
+    int64_t out_head_stride, void *workspace, int64_t workspace_bytes, int32_t dtype,
+    tks_stream_t stream);
+
+int32_t tks_rope_kv_append_fp8_rows(
+    const void *query, void *query_out, int64_t q_token_stride, int64_t q_head_stride,
+    int64_t qo_token_stride, int64_t qo_head_stride, int32_t num_q_heads, const void *key,
+    void *key_out, int64_t k_token_stride, int64_t k_head_stride, int64_t ko_token_stride,
+    int64_t ko_head_stride, const void *value, int64_t v_token_stride, int64_t v_head_stride,
+    int32_t num_kv_heads, int64_t num_tokens, int32_t head_dim, const int64_t *positions,
+    const void *cos_cache, const void *sin_cache, int64_t cache_len, void *key_cache,
+    void *value_cache, float *k_scales, float *v_scales, int32_t num_layers, int64_t num_blocks,
+    int32_t block_size, int32_t layer_index, const int64_t *slot_mapping, int32_t dtype,
+    tks_stream_t stream);
+
+int32_t tks_rope_append_paged_decode_fp8_rows(
+    const void *query, int64_t q_seq_stride, int64_t q_head_stride, const void *key,
+    int64_t k_seq_stride, int64_t k_head_stride, const void *value, int64_t v_seq_stride,
+    int64_t v_head_stride, const int64_t *positions, const void *cos_cache,
+    const void *sin_cache, int64_t cache_len, const int64_t *slot_mapping, void *key_cache,
+    void *value_cache, float *k_scales, float *v_scales, int32_t num_layers,
+    int64_t num_blocks, int32_t num_kv_heads, int32_t block_size, int32_t head_dim,
+    int32_t layer_index, const int32_t *block_tables, int32_t block_table_stride,
+    const int32_t *seq_lens, const int32_t *seq_order, int32_t num_seqs, int32_t num_q_heads,
+    int32_t max_seq_len, float scale, int32_t pages_per_split, void *out,
+    int64_t out_seq_stride, int64_t out_head_stride, void *workspace, int64_t workspace_bytes,
+    int32_t dtype, tks_stream_t stream);
+
+/* ------------------------------------------------------------------------
  * RMSNorm over the last dimension.
  * Replaces triton_rms_norm (tokserve/kernels/rmsnorm.py:6-45, kernel
  * tokserve/kernels/_triton_rmsnorm.py:10-38) and RMSNorm.forward

@@ -63,3 +63,31 @@ void oracle_e4m3_encode_array(const float *x, int64_t n, float scale, uint8_t *o
 void oracle_e4m3_decode_array(const uint8_t *codes, int64_t n, float *out) {
   for (int64_t i = 0; i < n; ++i) out[i] = oracle_e4m3_decode(codes[i]);
 }
+
+/*
+ * Per-row scales (the build's second fp8 pool variant; one scale per pool row,
+ * i.e. per (token, KV head)): for a row x of n values
+ *   amax = max |x_i| (NaN when any x_i is NaN),
+ *   s    = amax / 448, replaced by 1 when it is 0, NaN or infinite,
+ *   code = e4m3(clamp(x_i / s, -448, 448)),
+ * so the row's largest finite magnitude maps to code magnitude 448.
+ */
+float oracle_e4m3_row_scale(const float *x, int64_t n) {
+  float amax = 0.0f;
+  for (int64_t i = 0; i < n; ++i) {
+    if (isnan(x[i])) return 1.0f;
+    const float a = fabsf(x[i]);
+    if (a > amax) amax = a;
+  }
+  const float s = amax / 448.0f;
+  return (s > 0.0f && isfinite(s)) ? s : 1.0f;
+}
+
+void oracle_e4m3_encode_rows(const float *x, int64_t rows, int64_t n, uint8_t *out,
+                             float *scales) {
+  for (int64_t r = 0; r < rows; ++r) {
+    const float s = oracle_e4m3_row_scale(x + r * n, n);
+    scales[r] = s;
+    oracle_e4m3_encode_array(x + r * n, n, s, out + r * n);
+  }
+}

@@ -51,7 +51,7 @@ class Record:
 class Engine:
     def __init__(self, state: dict[str, torch.Tensor], config: dict, *, num_blocks: int,
                  block_size: int, max_running: int,
-                 kv_quant: tuple[float, float] | None = None) -> None:
+                 kv_quant: tuple[float, float] | str | None = None) -> None:
         self.state, self.config = state, config
         self.kv_quant = kv_quant
         self.block_size, self.num_blocks, self.max_running = block_size, num_blocks, max_running

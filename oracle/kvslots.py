@@ -52,6 +52,8 @@ def _load() -> ctypes.CDLL:
         lib.oracle_e4m3_encode_array.argtypes = [_p, _i64, ctypes.c_float, _p]
         lib.oracle_e4m3_decode_array.restype = None
         lib.oracle_e4m3_decode_array.argtypes = [_p, _i64, _p]
+        lib.oracle_e4m3_encode_rows.restype = None
+        lib.oracle_e4m3_encode_rows.argtypes = [_p, _i64, _i64, _p, _p]
         _lib = lib
     return _lib
 
@@ -158,3 +160,18 @@ def e4m3_decode(codes: torch.Tensor) -> torch.Tensor:
     out = torch.empty(codes.shape, dtype=torch.float32)
     _load().oracle_e4m3_decode_array(codes.data_ptr(), codes.numel(), out.data_ptr())
     return out
+
+
+def e4m3_encode_rows(x: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """(uint8 codes, float32 scales) of x (..., n) with one scale per row, from e4m3.c:
+    s = max|row| / 448 (1 when that is 0, NaN or infinite), codes of x / s."""
+
+    _cpu(x)
+    values = x.to(torch.float32).contiguous()
+    n = values.shape[-1]
+    rows = values.numel() // n if n else 0
+    out = torch.empty(values.shape, dtype=torch.uint8)
+    scales = torch.empty(values.shape[:-1], dtype=torch.float32)
+    _load().oracle_e4m3_encode_rows(values.data_ptr(), rows, n, out.data_ptr(),
+                                    scales.data_ptr())
+    return out, scales

@@ -20,7 +20,8 @@ from dataclasses import dataclass, field
 import torch
 from torch.nn import functional
 
-from oracle.paged import dequantize_e4m3, quantize_e4m3
+from oracle.paged import (dequantize_e4m3, dequantize_e4m3_rows, quantize_e4m3,
+                          quantize_e4m3_rows)
 from oracle.torch_path import apply_rope, gqa_attention, rms_norm
 
 
@@ -38,11 +39,13 @@ class SequenceKV:
 
 def forward(state: dict[str, torch.Tensor], config: dict, token_ids: torch.Tensor,
             cache: SequenceKV | None = None,
-            kv_quant: tuple[float, float] | None = None) -> torch.Tensor:
+            kv_quant: tuple[float, float] | str | None = None) -> torch.Tensor:
     """token_ids (1, T) -> logits (1, T, V); appends the T tokens' K/V to `cache`.
 
     kv_quant = (k_scale, v_scale) models fp8 e4m3 pools: every K/V row attention
-    sees has been through quantize_e4m3 / dequantize_e4m3 with those scales.
+    sees has been through quantize_e4m3 / dequantize_e4m3 with those scales;
+    kv_quant = "row" models fp8 pools with one scale per (token, KV head) row
+    (quantize_e4m3_rows / dequantize_e4m3_rows).
     """
 
     hq, hkv = config["num_attention_heads"], config["num_key_value_heads"]
@@ -63,7 +66,10 @@ def forward(state: dict[str, torch.Tensor], config: dict, token_ids: torch.Tenso
         k = k.reshape(1, length, hkv, dh).transpose(1, 2)
         v = v.reshape(1, length, hkv, dh).transpose(1, 2)
         q, k = apply_rope(q, k, positions, theta=theta)
-        if kv_quant is not None:
+        if kv_quant == "row":
+            k = dequantize_e4m3_rows(*quantize_e4m3_rows(k), k.dtype)
+            v = dequantize_e4m3_rows(*quantize_e4m3_rows(v), v.dtype)
+        elif kv_quant is not None:
             k = dequantize_e4m3(quantize_e4m3(k, kv_quant[0]), kv_quant[0], k.dtype)
             v = dequantize_e4m3(quantize_e4m3(v, kv_quant[1]), kv_quant[1], v.dtype)
         if cache is not None:

@@ -139,3 +139,32 @@ def dequantize_e4m3(codes: torch.Tensor, scale: float, dtype: torch.dtype) -> to
     """float(code) * scale in fp32, rounded once to dtype."""
 
     return (codes.to(torch.float32) * scale).to(dtype)
+
+
+# fp8 pools with one scale per pool row (per token and KV head), the second pool
+# variant: the scales sit beside the pools as float32 [L, NB, Hkv, BS].
+
+
+def row_scales_e4m3(x: torch.Tensor) -> torch.Tensor:
+    """float32 scale of each row of x (..., Dh): max|x| / 448, 1 where that is 0, NaN or
+    infinite (a NaN anywhere in the row makes the maximum NaN)."""
+
+    amax = x.to(torch.float32).abs().amax(dim=-1)
+    s = amax / FP8_MAX
+    return torch.where((s > 0) & torch.isfinite(s), s, torch.ones_like(s))
+
+
+def quantize_e4m3_rows(x: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """(e4m3(clamp(x / s, -448, 448)) as torch.float8_e4m3fn, s) with s = row_scales_e4m3(x)."""
+
+    s = row_scales_e4m3(x)
+    codes = (x.to(torch.float32) / s.unsqueeze(-1)).clamp(-FP8_MAX, FP8_MAX)
+    return codes.to(torch.float8_e4m3fn), s
+
+
+def dequantize_e4m3_rows(codes: torch.Tensor, scales: torch.Tensor,
+                         dtype: torch.dtype) -> torch.Tensor:
+    """float(code) * s (s per row, the scales shaped like codes without the last axis) in
+    fp32, rounded once to dtype."""
+
+    return (codes.to(torch.float32) * scales.unsqueeze(-1)).to(dtype)

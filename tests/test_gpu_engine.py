@@ -38,12 +38,17 @@ def _fixture_model(device) -> LlamaModel:
 
 def _manager(model, device, *, num_blocks, block_size, dtype=torch.float32, kv_dtype=None,
              scales=(1.0, 1.0)):
+    """scales: the fp8 pool scales (k_scale, v_scale), or "row" for one scale per row."""
+
     config = model.config
+    per_row = scales == "row"
     return PagedKVCacheManager(num_layers=config.num_hidden_layers, num_blocks=num_blocks,
                                num_key_value_heads=config.num_key_value_heads,
                                block_size=block_size, head_dim=config.head_dim, device=device,
-                               dtype=dtype, kv_dtype=kv_dtype, k_scale=scales[0],
-                               v_scale=scales[1])
+                               dtype=dtype, kv_dtype=kv_dtype,
+                               k_scale=1.0 if per_row else scales[0],
+                               v_scale=1.0 if per_row else scales[1],
+                               scale_granularity="row" if per_row else "pool")
 
 
 def test_model_reproduces_reference_fixture(device) -> None:
@@ -376,10 +381,11 @@ def test_decode_graph_replays_match_eager_and_oracle(device) -> None:
     assert with_graphs == {rid: reference.finished[rid].generated for rid, _, _ in specs}
 
 
-@pytest.mark.parametrize("scales", [(1.0, 1.0), (0.25, 0.5)])
+@pytest.mark.parametrize("scales", [(1.0, 1.0), (0.25, 0.5), "row"])
 def test_engine_fp8_kv_pools_fp32_tokens_identical(device, scales) -> None:
-    """fp8 e4m3 K/V pools under the fp32 fixture model: the engine's greedy tokens and
-    records equal the oracle engine whose K/V rows go through the same e4m3 rounding."""
+    """fp8 e4m3 K/V pools under the fp32 fixture model (per-pool scales, or one scale per
+    pool row): the engine's greedy tokens and records equal the oracle engine whose K/V
+    rows go through the same e4m3 rounding."""
 
     g = torch.Generator().manual_seed(300)
     specs = []

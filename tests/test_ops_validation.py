@@ -66,11 +66,11 @@ def test_workspace_growth_keeps_replaced_buffers_alive() -> None:
 
 def test_every_operator_is_registered_with_its_writes_marked() -> None:
     """Each C-ABI kernel family is a torch.library operator; the tensors it writes (KV
-    pools, outputs, in-place rotations) are marked mutable in its schema, and nothing
-    else is."""
+    pools and their per-row scales, outputs, in-place rotations) are marked mutable in
+    its schema, and nothing else is."""
 
     writes = {
-        "kv_append": {"key_cache", "value_cache"},
+        "kv_append": {"key_cache", "value_cache", "k_scales", "v_scales"},
         "paged_gather": {"key_out", "value_out"},
         "paged_attention_decode": {"out", "workspace"},
         "paged_attention_decode_noalloc": {"out"},
@@ -78,9 +78,9 @@ def test_every_operator_is_registered_with_its_writes_marked() -> None:
         "rms_norm": {"out", "residual_out"},
         "rope": {"query_out", "key_out"},
         "rope_": {"query", "key"},
-        "rope_kv_append": {"key_cache", "value_cache", "query_out", "key_out"},
-        "rope_kv_append_": {"query", "key_cache", "value_cache", "key_out"},
-        "rope_append_paged_decode": {"key_cache", "value_cache", "out", "workspace"},
+        "rope_kv_append": {"key_cache", "value_cache", "query_out", "key_out", "k_scales", "v_scales"},
+        "rope_kv_append_": {"query", "key_cache", "value_cache", "key_out", "k_scales", "v_scales"},
+        "rope_append_paged_decode": {"key_cache", "value_cache", "out", "workspace", "k_scales", "v_scales"},
         "greedy_argmax": {"out"},
         "silu_mul": {"out"},
         "vector_add": {"out"},
@@ -211,4 +211,37 @@ def test_fused_decode_sequence_order_and_workspace_must_be_device_tensors(
         call(workspace=torch.zeros(64, dtype=torch.uint8))
     with pytest.raises(ValueError, match="contiguous uint8"):
         call(workspace=torch.zeros(64, dtype=torch.int32, device=meta))
+    assert meta_as_device == []
+
+
+def test_row_scales_are_checked_before_launch(meta_as_device) -> None:
+    """Per-row scale arrays: both or neither, fp8 pools only, float32 (L, NB, Hkv, BS)
+    contiguous on the pools' device, and no pool scales beside them."""
+
+    meta = torch.device("meta")
+    query, _, _, tables, lens = _decode_args(meta)
+    kc = torch.zeros(1, 4, 2, 16, 8, dtype=ops.FP8_POOL_DTYPE, device=meta)
+    vc = torch.zeros_like(kc)
+    ks = torch.ones(1, 4, 2, 16, device=meta)
+
+    def call(pool=kc, **kwargs):
+        ops.paged_attention_decode(query, pool, pool if pool is not kc else vc, tables, lens,
+                                   layer_index=0, max_seq_len=1, **kwargs)
+
+    call(k_scales=ks, v_scales=ks.clone())
+    assert meta_as_device == ["paged_attention_decode"]
+    meta_as_device.clear()
+    for kwargs, error, message in (
+        (dict(k_scales=ks), ValueError, "go together"),
+        (dict(k_scales=ks, v_scales=ks.double()), TypeError, "float32"),
+        (dict(k_scales=ks, v_scales=ks[..., :8]), ValueError, "contiguous"),
+        (dict(k_scales=ks, v_scales=ks.transpose(2, 3).contiguous().transpose(2, 3)), ValueError,
+         "contiguous"),
+        (dict(k_scales=ks, v_scales=torch.ones(1, 4, 2, 16)), ValueError, "HIP device"),
+        (dict(k_scales=ks, v_scales=ks, k_scale=2.0), ValueError, "must stay 1"),
+        (dict(pool=torch.zeros(1, 4, 2, 16, 8, device=meta), k_scales=ks, v_scales=ks),
+         ValueError, "fp8 KV pools only"),
+    ):
+        with pytest.raises(error, match=message):
+            call(**kwargs)
     assert meta_as_device == []

@@ -450,3 +450,70 @@ def test_e4m3_planted_truncation_is_caught() -> None:
     rounded = kvslots.e4m3_decode(kvslots.e4m3_encode(x))
     assert not torch.equal(truncated, rounded)
     assert torch.equal(kvslots.e4m3_encode(x), paged.quantize_e4m3(x, 1.0).view(torch.uint8))
+
+
+# fp8 pools with one scale per pool row: the torch restatement against the C
+# quantizer, closed forms of the scale rule, and a planted mistake.
+
+
+def _row_cases() -> torch.Tensor:
+    g = torch.Generator().manual_seed(17)
+    magnitude = 2.0 ** torch.randint(-30, 30, (400, 1), generator=g).float()
+    x = torch.randn(400, 64, generator=g) * magnitude
+    x[0] = 0.0
+    x[1, 5] = float("nan")
+    x[2, 9] = float("inf")
+    x[3, 2] = -float("inf")
+    x[4] = -x[4].abs()
+    x[5] = torch.randn(64, generator=g) * 1e-41     # subnormal row
+    x[6] = 3e38                                     # amax / 448 finite, x / s = 448
+    x[7] = 448.0
+    x[8, 0] = -0.0
+    return x
+
+
+def test_e4m3_row_quantizer_matches_c() -> None:
+    x = _row_cases()
+    codes, scales = kvslots.e4m3_encode_rows(x)
+    t_codes, t_scales = paged.quantize_e4m3_rows(x)
+    assert torch.equal(scales, t_scales)
+    assert torch.equal(codes, t_codes.view(torch.uint8))
+
+
+def test_e4m3_row_scale_closed_forms() -> None:
+    """s = max|row| / 448 for finite nonzero rows, so every such row's largest magnitude
+    is code 448 (0x7E / 0xFE) and every element decodes within half an e4m3 step of x
+    (2^-4 relative, 2^-10 s absolute below the normal range); zero, NaN and infinite
+    maxima give s = 1."""
+
+    x = _row_cases()
+    codes, scales = kvslots.e4m3_encode_rows(x)
+    amax = x.abs().amax(dim=1)
+    regular = torch.isfinite(amax) & (amax > 0)
+    assert torch.equal(scales[regular], (amax / 448.0)[regular])
+    assert torch.equal(scales[~regular], torch.ones(int((~regular).sum())))
+    assert int((~regular).sum()) == 4  # rows 0, 1, 2, 3
+    top = x.abs().argmax(dim=1)
+    top_codes = codes[torch.arange(x.shape[0]), top]
+    assert torch.all(top_codes[regular] & 0x7F == 0x7E)
+    decoded = paged.dequantize_e4m3_rows(codes.view(torch.float8_e4m3fn), scales, torch.float32)
+    finite = regular.unsqueeze(1).expand_as(x)
+    bound = torch.maximum(x.abs() * 2.0 ** -4, scales.unsqueeze(1) * 2.0 ** -10)
+    assert torch.all((decoded - x).abs()[finite] <= bound[finite])
+    assert torch.isnan(decoded[1, 5]) and int(codes[2, 9]) == 0x7E and int(codes[3, 2]) == 0xFE
+
+
+def test_e4m3_row_quantizer_planted_mistakes_are_caught() -> None:
+    """A scale from the signed maximum (max x instead of max |x|), or one that keeps 0 for
+    an all-zero row, disagrees with the C quantizer."""
+
+    x = _row_cases()
+    codes, scales = kvslots.e4m3_encode_rows(x)
+    signed = x.amax(dim=1) / 448.0
+    signed = torch.where((signed > 0) & torch.isfinite(signed), signed, torch.ones_like(signed))
+    assert not torch.equal(signed, scales)
+    assert not torch.equal(torch.clamp(x / signed.unsqueeze(1), -448, 448)
+                           .to(torch.float8_e4m3fn).view(torch.uint8), codes)
+    zero_kept = torch.where(torch.isfinite(x.abs().amax(dim=1)), x.abs().amax(dim=1) / 448.0,
+                            torch.ones(x.shape[0]))
+    assert not torch.equal(zero_kept, scales)

@@ -157,6 +157,8 @@ struct DecodeArgs {
   int64_t o_ss, o_hs;
   float *ws_m, *ws_l, *ws_acc;
   float v_scale = 1.f;  // V decode factor of fp8 pools (1 otherwise)
+  // fp8 pools with one scale per pool row ([L, NB, Hkv, BS]; null: per-pool scales).
+  const float *k_rs = nullptr, *v_rs = nullptr;
   // RoPE + KV append fused into the decode (launch_decode_mfma with rope = true):
   // sequence b's query is rotated in registers at positions[b] (q itself is not
   // written); its new key row (rotated) and value row go to pool slot slots[b]

@@ -71,6 +71,17 @@ __device__ __forceinline__ bf16_t from_float<bf16_t>(float f) {
   return bf16_t{f32_to_bf16_bits(f)};
 }
 
+// The fp32 value as a register holds it. An empty asm the compiler cannot look
+// through: a product computed before it is rounded to fp32 and cannot be fused
+// with an fp16 conversion after it. (The compiler turns fp16(a * b) into one
+// mixed-precision FMA, v_fma_mixlo_f16, which rounds the exact product to fp16
+// once; that differs from rounding the fp32 product whenever the product is
+// inexact in fp32, and #pragma clang fp contract(off) does not prevent it.)
+__device__ __forceinline__ float fp32_value(float f) {
+  __asm__("" : "+v"(f));
+  return f;
+}
+
 // Round a float through T and back (the `.to(dtype)` of the torch path).
 template <typename T>
 __device__ __forceinline__ float round_through(float f) {

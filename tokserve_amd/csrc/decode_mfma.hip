@@ -300,7 +300,10 @@ __device__ __forceinline__ void write_staged_rows(const DecodeArgs &a, int b, in
 // sequence's last page stages the rotated key row and the value row in LDS, uses
 // them in place of what it loads of their slot and writes them to the pool after
 // its page loop, so no workgroup reads pool memory written in the same launch.
-template <typename T, typename KV, int DH, int G, bool ROPE>
+// ROWS: fp8 pools with one scale per pool row (a.k_rs, a.v_rs); lane r of a page
+// loads its token's two scales with the page, multiplies its scores by the key
+// scale and its probabilities (after they enter the row sum) by the value scale.
+template <typename T, typename KV, int DH, int G, bool ROPE, bool ROWS = false>
 __global__ __launch_bounds__(64 * kWaves) void decode_mfma_kernel(DecodeArgs a) {
   using S = DecodeShape<DH, G>;
   constexpr int BS = S::BS, NC = S::NC, LPR = S::LPR, TG = S::TG, HPL = S::HPL;
@@ -434,9 +437,22 @@ __global__ __launch_bounds__(64 * kWaves) void decode_mfma_kernel(DecodeArgs a) 
   }
   const float scale_log2 = a.scale_log2;
 
+  // Row scales of token r of a page: ks_row[blk * rows_per_block].
+  const int64_t rows_per_block = a.pool.block_stride / DH;
+  const float *ks_row = nullptr;
+  const float *vs_row = nullptr;
+  if constexpr (ROWS) {
+    const int64_t base = (a.pool.layer_base + (int64_t)kvh * a.pool.head_stride) / DH + r;
+    ks_row = a.k_rs + base;
+    vs_row = a.v_rs + base;
+  }
   // Every page is read once: non-temporal loads.
-  auto load_page = [&](int blk_reg, int idx, raw (&kr)[NC], raw (&vr)[4]) {
+  auto load_page = [&](int blk_reg, int idx, raw (&kr)[NC], raw (&vr)[4], float &ks, float &vs) {
     const int64_t blk = clamp_block(__builtin_amdgcn_readlane(blk_reg, idx), a.pool.num_blocks);
+    if constexpr (ROWS) {
+      ks = ks_row[blk * rows_per_block];
+      vs = vs_row[blk * rows_per_block];
+    }
     const KV *kp = kc + blk * a.pool.block_stride + k_off;
     const KV *vp = vc + blk * a.pool.block_stride + v_off;
     if constexpr (kSlab) {
@@ -474,7 +490,8 @@ __global__ __launch_bounds__(64 * kWaves) void decode_mfma_kernel(DecodeArgs a) 
         if (tg * 4 + j == new_off) vr[j] = load_chunk<T, KV>(new_v_s + dc * 8);
     }
   };
-  auto consume = [&](auto check_end, const raw (&kr)[NC], raw (&vr)[4], int p) {
+  auto consume = [&](auto check_end, const raw (&kr)[NC], raw (&vr)[4], int p, float ks,
+                     float vs) {
     constexpr bool kCheckEnd = decltype(check_end)::value;
     typename M::f4 s4 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -482,12 +499,17 @@ __global__ __launch_bounds__(64 * kWaves) void decode_mfma_kernel(DecodeArgs a) 
     float sv[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) sv[i] = s4[i] * scale_log2;
+    if constexpr (ROWS) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) sv[i] *= ks;
+    }
     // The sequence's last page (uniform): keys past len score -inf, and their V
     // rows, whatever the pool holds there, are zeroed, since 0 * NaN is NaN.
     if (kCheckEnd && (p + 1) * BS > len) {
       const bool valid = p * BS + r < len;
 #pragma unroll
       for (int i = 0; i < 4; ++i) sv[i] = valid ? sv[i] : -INFINITY;
+      if constexpr (ROWS) vs = valid ? vs : 0.f;  // an unwritten row's scale may be NaN
 #pragma unroll
       for (int j = 0; j < 4; ++j)
         if (p * BS + tg * 4 + j >= len) vr[j] = IO::zero();
@@ -518,7 +540,7 @@ __global__ __launch_bounds__(64 * kWaves) void decode_mfma_kernel(DecodeArgs a) 
     for (int i = 0; i < 4; ++i) {
       const float pv = fast_exp2(sv[i] - mref[i]);
       l[i] += pv;
-      p_s[wave][grp * 4 + i][r] = pv;
+      p_s[wave][grp * 4 + i][r] = ROWS ? pv * vs : pv;
     }
     wave_lds_sync();
     pair vp[2][8];
@@ -560,15 +582,17 @@ __global__ __launch_bounds__(64 * kWaves) void decode_mfma_kernel(DecodeArgs a) 
     // ring never holds more than the one page being consumed.
     __builtin_amdgcn_s_waitcnt(kWaitVmcntZero);
     raw kb[D][NC], vb[D][4];
+    float ksr[D] = {}, vsr[D] = {};
 #pragma unroll
     for (int j = 0; j < D - 1; ++j)
-      if (j < n) load_page(blk_reg, j, kb[j], vb[j]);
+      if (j < n) load_page(blk_reg, j, kb[j], vb[j], ksr[j], vsr[j]);
     int i = 0;  // page i sits in ring slot i % D
     for (; i + 2 * D - 1 <= n; i += D) {
 #pragma unroll
       for (int j = 0; j < D; ++j) {
-        load_page(blk_reg, i + j + D - 1, kb[(j + D - 1) % D], vb[(j + D - 1) % D]);
-        consume(BoolConst<false>{}, kb[j], vb[j], c0 + i + j);
+        load_page(blk_reg, i + j + D - 1, kb[(j + D - 1) % D], vb[(j + D - 1) % D],
+                  ksr[(j + D - 1) % D], vsr[(j + D - 1) % D]);
+        consume(BoolConst<false>{}, kb[j], vb[j], c0 + i + j, ksr[j], vsr[j]);
       }
     }
     // Fewer than 2D - 1 pages left; those before i + D - 1 are already loaded.
@@ -576,9 +600,10 @@ __global__ __launch_bounds__(64 * kWaves) void decode_mfma_kernel(DecodeArgs a) 
     for (int j = 0; j < 2 * D - 2; ++j) {
       if (i + j < n) {
         if (i + j + D - 1 < n)
-          load_page(blk_reg, i + j + D - 1, kb[(j + D - 1) % D], vb[(j + D - 1) % D]);
+          load_page(blk_reg, i + j + D - 1, kb[(j + D - 1) % D], vb[(j + D - 1) % D],
+                    ksr[(j + D - 1) % D], vsr[(j + D - 1) % D]);
         if constexpr (ROPE) substitute_new_rows(kb[j % D], vb[j % D], c0 + i + j);
-        consume(BoolConst<true>{}, kb[j % D], vb[j % D], c0 + i + j);
+        consume(BoolConst<true>{}, kb[j % D], vb[j % D], c0 + i + j, ksr[j % D], vsr[j % D]);
       }
     }
   }
@@ -650,10 +675,16 @@ int32_t launch_typed(const DecodeArgs &a, int32_t num_seqs, int32_t num_kv_heads
   // KV heads vary fastest (consecutive workgroups, dealt round-robin over the
   // XCDs, carry equal work), splits slowest.
   const dim3 grid(num_kv_heads, num_seqs, a.max_splits);
-#define TKS_DECODE(DH, GG)                                                    \
-  if (head_dim == DH && G == GG) {                                            \
-    decode_mfma_kernel<T, KV, DH, GG, ROPE><<<grid, 64 * kWaves, 0, s>>>(a);  \
-    return check_launch();                                                    \
+#define TKS_DECODE(DH, GG)                                                          \
+  if (head_dim == DH && G == GG) {                                                  \
+    if constexpr (sizeof(KV) == 1 && !ROPE) {                                       \
+      if (a.k_rs != nullptr) {                                                      \
+        decode_mfma_kernel<T, KV, DH, GG, false, true><<<grid, 64 * kWaves, 0, s>>>(a); \
+        return check_launch();                                                      \
+      }                                                                             \
+    }                                                                               \
+    decode_mfma_kernel<T, KV, DH, GG, ROPE><<<grid, 64 * kWaves, 0, s>>>(a);        \
+    return check_launch();                                                          \
   }
   TKS_DECODE(128, 4)
   TKS_DECODE(128, 8)

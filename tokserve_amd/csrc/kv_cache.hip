@@ -170,6 +170,7 @@ __device__ __forceinline__ void quantize_chunk(const T *src, uint8_t *dst, float
   encode_e4m3<E>(x, scale, dst);
 }
 
+// float(code) * scale rounded to fp32, then to T.
 template <typename T, int E>
 __device__ __forceinline__ void dequantize_chunk(const uint8_t *src, T *dst, float scale) {
   float f[E];
@@ -179,7 +180,7 @@ __device__ __forceinline__ void dequantize_chunk(const uint8_t *src, T *dst, flo
     f[0] = to_float(fp8e4m3_t{src[0]});
   }
 #pragma unroll
-  for (int i = 0; i < E; ++i) f[i] = f[i] * scale;
+  for (int i = 0; i < E; ++i) f[i] = fp32_value(f[i] * scale);
   if constexpr (E == 16) {
     constexpr int N = Vec<T>::N;
 #pragma unroll

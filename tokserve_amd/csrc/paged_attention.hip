@@ -66,6 +66,9 @@ struct GenericArgs {
   float *ws_m, *ws_l, *ws_acc;
   int32_t vec_rows;  // K/V rows are 16-byte aligned and head_dim is a multiple of 16 bytes
   float v_scale = 1.f;  // V decode factor of fp8 pools (1 otherwise)
+  // fp8 pools with one scale per pool row ([L, NB, Hkv, BS], the pool row's element
+  // offset / head_dim); null: per-pool scales.
+  const float *k_rs = nullptr, *v_rs = nullptr;
 };
 
 // The split's keys are dealt to the four waves 64 at a time (wave w takes keys
@@ -144,7 +147,15 @@ __global__ __launch_bounds__(kGenThreads) void attn_generic_kernel(GenericArgs a
   };
   float kv[DHMAX];
   float vv[64][DPL];
+  // Row scales of this lane's key (scores) and value (probabilities); 1 and 1 for
+  // per-pool scales. A lane past the step's keys reads row 0's and is masked.
+  const bool rows = a.k_rs != nullptr;
+  float ks_lane = 1.f, vs_lane = 1.f;
   auto load_step = [&](int64_t rb, int n) {
+    if (rows) {
+      ks_lane = a.k_rs[rb / DH];
+      vs_lane = lane < n ? a.v_rs[rb / DH] : 0.f;
+    }
     if (a.vec_rows) {
 #pragma unroll
       for (int d = 0; d < DHMAX; d += V) {
@@ -214,7 +225,7 @@ __global__ __launch_bounds__(kGenThreads) void attn_generic_kernel(GenericArgs a
           s += qd.z * kv[d + 2];
           s += qd.w * kv[d + 3];
         }
-        const float sv = valid ? s * a.scale_log2 : -INFINITY;
+        const float sv = valid ? s * a.scale_log2 * ks_lane : -INFINITY;
         const float mt = wave_max(sv);
         const float mn = fmaxf(m[g], mt);
         const float alpha = fast_exp2(m[g] - mn);
@@ -227,7 +238,7 @@ __global__ __launch_bounds__(kGenThreads) void attn_generic_kernel(GenericArgs a
     }
 #pragma unroll
     for (int g = 0; g < kGenMaxG; ++g)
-      if (g < G) p_s[wave][g][lane] = pv[g];
+      if (g < G) p_s[wave][g][lane] = rows ? pv[g] * vs_lane : pv[g];
 #pragma unroll
     for (int g = 0; g < kGenMaxG; ++g)
       if (g < G) {
@@ -315,7 +326,8 @@ __global__ __launch_bounds__(256) void decode_pages_kernel(
     const fp8e4m3_t *__restrict__ kc, const fp8e4m3_t *__restrict__ vc, PoolView pool,
     int32_t num_kv_heads, const int32_t *__restrict__ bt, int32_t bt_stride,
     const int32_t *__restrict__ seq_lens, int32_t num_seqs, T *__restrict__ k_out,
-    T *__restrict__ v_out, int32_t *__restrict__ table_out) {
+    T *__restrict__ v_out, int32_t *__restrict__ table_out, const float *__restrict__ k_rs,
+    const float *__restrict__ v_rs) {
   const int64_t chunks = static_cast<int64_t>(pool.block_size) * pool.head_dim / 16;
   const int64_t per_page = chunks * num_kv_heads;
   const int64_t item = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
@@ -335,10 +347,21 @@ __global__ __launch_bounds__(256) void decode_pages_kernel(
   const int64_t dst = slot * pool.block_stride + h * pool.head_stride + c;
   float f[16];
   constexpr int N = Vec<T>::N;
+  // Row scales (one per 16-element chunk's row: head_dim is a multiple of 16).
+  const float ks = k_rs ? k_rs[src / pool.head_dim] : 1.f;
+  const float vs = v_rs ? v_rs[src / pool.head_dim] : 1.f;
   unpack<fp8e4m3_t>(ld16(kc + src), f);
+  if (k_rs) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) f[i] *= ks;
+  }
 #pragma unroll
   for (int i = 0; i < 16; i += N) st16(k_out + dst + i, pack<T>(f + i));
   unpack<fp8e4m3_t>(ld16(vc + src), f);
+  if (v_rs) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) f[i] *= vs;
+  }
 #pragma unroll
   for (int i = 0; i < 16; i += N) st16(v_out + dst + i, pack<T>(f + i));
 }
@@ -533,8 +556,11 @@ int32_t decode_impl(const void *query, int64_t q_seq_stride, int64_t q_head_stri
                     int32_t max_seq_len, float scale, int32_t pages_per_split, void *out,
                     int64_t out_seq_stride, int64_t out_head_stride, void *workspace,
                     int64_t workspace_bytes, bool fp8_pools, float k_scale, float v_scale,
-                    int32_t dtype, tks_stream_t stream, const RopeAppend *ra = nullptr) {
+                    int32_t dtype, tks_stream_t stream, const RopeAppend *ra = nullptr,
+                    const float *k_rs = nullptr, const float *v_rs = nullptr) {
   if (!valid_dtype(dtype)) return TKS_ERR_TYPE;
+  if ((k_rs != nullptr) != (v_rs != nullptr) || (k_rs != nullptr && !fp8_pools))
+    return TKS_ERR_VALUE;
   if (!pool_ok(num_layers, num_blocks, num_kv_heads, block_size, head_dim) || num_seqs < 0 ||
       num_q_heads <= 0 || num_q_heads % num_kv_heads != 0 || max_seq_len < 0 ||
       pages_per_split < 0 || !valid_scale(k_scale) || !valid_scale(v_scale))
@@ -570,14 +596,23 @@ int32_t decode_impl(const void *query, int64_t q_seq_stride, int64_t q_head_stri
     // the RoPE + append launch writes the rotated queries into `out`, which the
     // decode then reads as its query (each workgroup reads its rows before it, or
     // the merge, writes them).
-    const bool fused = mfma &&
+    // Row-scaled pools always take the two launches.
+    const bool fused = mfma && k_rs == nullptr &&
                        aligned16(ra->key) && aligned16(ra->value) && aligned16(ra->cos_cache) &&
                        aligned16(ra->sin_cache) && ra->k_ss % 8 == 0 && ra->k_hs % 8 == 0 &&
                        ra->v_ss % 8 == 0 && ra->v_hs % 8 == 0;
     if (!fused) {
       void *kc = const_cast<void *>(key_cache), *vc = const_cast<void *>(value_cache);
       const int32_t st0 =
-          fp8_pools
+          k_rs != nullptr
+              ? tks_rope_kv_append_fp8_rows(
+                    query, out, q_seq_stride, q_head_stride, out_seq_stride, out_head_stride,
+                    num_q_heads, ra->key, nullptr, ra->k_ss, ra->k_hs, 0, 0, ra->value,
+                    ra->v_ss, ra->v_hs, num_kv_heads, num_seqs, head_dim, ra->positions,
+                    ra->cos_cache, ra->sin_cache, ra->cache_len, kc, vc,
+                    const_cast<float *>(k_rs), const_cast<float *>(v_rs), num_layers,
+                    num_blocks, block_size, layer_index, ra->slot_mapping, dtype, stream)
+          : fp8_pools
               ? tks_rope_kv_append_fp8(query, out, q_seq_stride, q_head_stride, out_seq_stride,
                                        out_head_stride, num_q_heads, ra->key, nullptr, ra->k_ss,
                                        ra->k_hs, 0, 0, ra->value, ra->v_ss, ra->v_hs,
@@ -597,7 +632,7 @@ int32_t decode_impl(const void *query, int64_t q_seq_stride, int64_t q_head_stri
                          block_tables, block_table_stride, seq_lens, seq_order, num_seqs,
                          num_q_heads, max_seq_len, scale, pages_per_split, out, out_seq_stride,
                          out_head_stride, workspace, workspace_bytes, fp8_pools, k_scale, v_scale,
-                         dtype, stream);
+                         dtype, stream, nullptr, k_rs, v_rs);
     }
   }
 
@@ -608,6 +643,8 @@ int32_t decode_impl(const void *query, int64_t q_seq_stride, int64_t q_head_stri
                  scale_log2, pps,          max_splits,    key_cap,     out,
                  out_seq_stride, out_head_stride, w.m,    w.l,         w.acc,
                  v_scale};
+    a.k_rs = k_rs;
+    a.v_rs = v_rs;
     if (ra != nullptr) {
       a.positions = ra->positions;
       a.cos_t = ra->cos_cache;
@@ -630,6 +667,8 @@ int32_t decode_impl(const void *query, int64_t q_seq_stride, int64_t q_head_stri
                   G,         scale_log2,   pps,           max_splits, key_cap,  out,
                   out_seq_stride, out_head_stride, w.m,   w.l,        w.acc,
                   vec_rows_ok(key_cache, value_cache, head_dim, kv_elem), v_scale};
+    a.k_rs = k_rs;
+    a.v_rs = v_rs;
     st = launch_generic(a, dtype, num_seqs, num_kv_heads, fp8_pools, s);
   }
   if (st != TKS_OK || max_splits == 1) return st;
@@ -657,9 +696,13 @@ int32_t prefill_impl(const void *query, int64_t q_token_stride, int64_t q_head_s
                      const int32_t *cu_seqlens_q, const int32_t *seq_order, int32_t num_seqs,
                      int64_t num_tokens, int32_t num_q_heads, int32_t max_query_len,
                      int32_t max_seq_len, float scale, void *out, int64_t out_token_stride,
-                     int64_t out_head_stride, bool fp8_pools, void *workspace, int64_t workspace_bytes, float k_scale,
-                     float v_scale, int32_t dtype, tks_stream_t stream) {
+                     int64_t out_head_stride, bool fp8_pools, void *workspace,
+                     int64_t workspace_bytes, float k_scale, float v_scale, int32_t dtype,
+                     tks_stream_t stream, const float *k_rs = nullptr,
+                     const float *v_rs = nullptr) {
   if (!valid_dtype(dtype)) return TKS_ERR_TYPE;
+  if ((k_rs != nullptr) != (v_rs != nullptr) || (k_rs != nullptr && !fp8_pools))
+    return TKS_ERR_VALUE;
   if (!pool_ok(num_layers, num_blocks, num_kv_heads, block_size, head_dim) || num_seqs < 0 ||
       num_tokens < 0 || num_q_heads <= 0 || num_q_heads % num_kv_heads != 0 ||
       max_query_len < 0 || max_seq_len < 0 || max_query_len > max_seq_len ||
@@ -710,11 +753,11 @@ int32_t prefill_impl(const void *query, int64_t q_token_stride, int64_t q_head_s
     if (dtype == TKS_BFLOAT16)
       decode_pages_kernel<bf16_t><<<grid, 256, 0, s>>>(
           k8, v8, pool, num_kv_heads, block_tables, block_table_stride, seq_lens, num_seqs,
-          static_cast<bf16_t *>(sp.k), static_cast<bf16_t *>(sp.v), sp.table);
+          static_cast<bf16_t *>(sp.k), static_cast<bf16_t *>(sp.v), sp.table, k_rs, v_rs);
     else
       decode_pages_kernel<_Float16><<<grid, 256, 0, s>>>(
           k8, v8, pool, num_kv_heads, block_tables, block_table_stride, seq_lens, num_seqs,
-          static_cast<_Float16 *>(sp.k), static_cast<_Float16 *>(sp.v), sp.table);
+          static_cast<_Float16 *>(sp.k), static_cast<_Float16 *>(sp.v), sp.table, k_rs, v_rs);
     const int32_t st = check_launch();
     if (st != TKS_OK) return st;
     const PoolView scratch = make_pool(0, scratch_blocks, num_kv_heads, block_size, head_dim);
@@ -732,6 +775,8 @@ int32_t prefill_impl(const void *query, int64_t q_token_stride, int64_t q_head_s
                 G,         scale_log2,     pps,           1,          key_cap,     out,         out_token_stride,
                 out_head_stride, nullptr,  nullptr,       nullptr,
                 vec_rows_ok(key_cache, value_cache, head_dim, kv_elem), v_scale};
+  a.k_rs = k_rs;
+  a.v_rs = v_rs;
   return launch_generic(a, dtype, static_cast<int32_t>(num_tokens), num_kv_heads, fp8_pools, s);
 }
 
@@ -946,4 +991,73 @@ extern "C" int32_t tks_paged_attention_prefill_fp8(
                       num_q_heads, max_query_len, max_seq_len, scale, out, out_token_stride,
                       out_head_stride, true, workspace, workspace_bytes, k_scale, v_scale, dtype,
                       stream);
+}
+
+// ------------------------------------------------------------------------
+// fp8 pools with one scale per pool row: the per-pool entries with the scale
+// arrays in place of the two scales (which are then 1).
+// ------------------------------------------------------------------------
+
+extern "C" int32_t tks_paged_attention_decode_fp8_rows(
+    const void *query, int64_t q_seq_stride, int64_t q_head_stride, const void *key_cache,
+    const void *value_cache, const float *k_scales, const float *v_scales, int32_t num_layers,
+    int64_t num_blocks, int32_t num_kv_heads, int32_t block_size, int32_t head_dim,
+    int32_t layer_index, const int32_t *block_tables, int32_t block_table_stride,
+    const int32_t *seq_lens, const int32_t *seq_order, int32_t num_seqs, int32_t num_q_heads,
+    int32_t max_seq_len, float scale, int32_t pages_per_split, void *out,
+    int64_t out_seq_stride, int64_t out_head_stride, void *workspace, int64_t workspace_bytes,
+    int32_t dtype, tks_stream_t stream) {
+  if (num_seqs > 0 && (!k_scales || !v_scales)) return TKS_ERR_VALUE;
+  return decode_impl(query, q_seq_stride, q_head_stride, key_cache, value_cache, num_layers,
+                     num_blocks, num_kv_heads, block_size, head_dim, layer_index, block_tables,
+                     block_table_stride, seq_lens, seq_order, num_seqs, num_q_heads, max_seq_len,
+                     scale, pages_per_split, out, out_seq_stride, out_head_stride, workspace,
+                     workspace_bytes, true, 1.f, 1.f, dtype, stream, nullptr, k_scales,
+                     v_scales);
+}
+
+extern "C" int32_t tks_paged_attention_prefill_fp8_rows(
+    const void *query, int64_t q_token_stride, int64_t q_head_stride, const void *key_cache,
+    const void *value_cache, const float *k_scales, const float *v_scales, int32_t num_layers,
+    int64_t num_blocks, int32_t num_kv_heads, int32_t block_size, int32_t head_dim,
+    int32_t layer_index, const int32_t *block_tables, int32_t block_table_stride,
+    const int32_t *seq_lens, const int32_t *cu_seqlens_q, const int32_t *seq_order,
+    int32_t num_seqs, int64_t num_tokens, int32_t num_q_heads, int32_t max_query_len,
+    int32_t max_seq_len, float scale, void *out, int64_t out_token_stride,
+    int64_t out_head_stride, void *workspace, int64_t workspace_bytes, int32_t dtype,
+    tks_stream_t stream) {
+  if (num_seqs > 0 && num_tokens > 0 && (!k_scales || !v_scales)) return TKS_ERR_VALUE;
+  return prefill_impl(query, q_token_stride, q_head_stride, key_cache, value_cache, num_layers,
+                      num_blocks, num_kv_heads, block_size, head_dim, layer_index, block_tables,
+                      block_table_stride, seq_lens, cu_seqlens_q, seq_order, num_seqs, num_tokens,
+                      num_q_heads, max_query_len, max_seq_len, scale, out, out_token_stride,
+                      out_head_stride, true, workspace, workspace_bytes, 1.f, 1.f, dtype, stream,
+                      k_scales, v_scales);
+}
+
+extern "C" int32_t tks_rope_append_paged_decode_fp8_rows(
+    const void *query, int64_t q_seq_stride, int64_t q_head_stride, const void *key,
+    int64_t k_seq_stride, int64_t k_head_stride, const void *value, int64_t v_seq_stride,
+    int64_t v_head_stride, const int64_t *positions, const void *cos_cache,
+    const void *sin_cache, int64_t cache_len, const int64_t *slot_mapping, void *key_cache,
+    void *value_cache, float *k_scales, float *v_scales, int32_t num_layers,
+    int64_t num_blocks, int32_t num_kv_heads, int32_t block_size, int32_t head_dim,
+    int32_t layer_index, const int32_t *block_tables, int32_t block_table_stride,
+    const int32_t *seq_lens, const int32_t *seq_order, int32_t num_seqs, int32_t num_q_heads,
+    int32_t max_seq_len, float scale, int32_t pages_per_split, void *out,
+    int64_t out_seq_stride, int64_t out_head_stride, void *workspace, int64_t workspace_bytes,
+    int32_t dtype, tks_stream_t stream) {
+  if (!valid_dtype(dtype)) return TKS_ERR_TYPE;
+  if (head_dim < 2 || head_dim % 2 != 0 || cache_len <= 0 || num_seqs < 0) return TKS_ERR_VALUE;
+  if (num_seqs > 0 && (!key || !value || !positions || !cos_cache || !sin_cache ||
+                       !slot_mapping || !k_scales || !v_scales))
+    return TKS_ERR_VALUE;
+  const RopeAppend ra{key,       k_seq_stride, k_head_stride, value,     v_seq_stride,
+                      v_head_stride, positions, cos_cache,  sin_cache, cache_len,
+                      slot_mapping};
+  return decode_impl(query, q_seq_stride, q_head_stride, key_cache, value_cache, num_layers,
+                     num_blocks, num_kv_heads, block_size, head_dim, layer_index, block_tables,
+                     block_table_stride, seq_lens, seq_order, num_seqs, num_q_heads, max_seq_len,
+                     scale, pages_per_split, out, out_seq_stride, out_head_stride, workspace,
+                     workspace_bytes, true, 1.f, 1.f, dtype, stream, &ra, k_scales, v_scales);
 }

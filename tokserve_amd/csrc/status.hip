@@ -14,7 +14,7 @@ void set_hip_error(hipError_t err) {
 }
 }  // namespace tks
 
-extern "C" int32_t tks_abi_version(void) { return 11; }
+extern "C" int32_t tks_abi_version(void) { return 12; }
 
 extern "C" const char *tks_status_string(int32_t status) {
   switch (status) {

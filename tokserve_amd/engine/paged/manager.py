@@ -40,12 +40,14 @@ class PagedKVCacheManager:
         kv_dtype: torch.dtype | None = None,
         k_scale: float = 1.0,
         v_scale: float = 1.0,
+        scale_granularity: str = "pool",
     ) -> None:
         self.allocator = PhysicalBlockAllocator(num_blocks)
         self.storage = PagedKVStorage(
             num_layers=num_layers, num_blocks=num_blocks, num_key_value_heads=num_key_value_heads,
             block_size=block_size, head_dim=head_dim, device=device, dtype=dtype,
             kv_dtype=kv_dtype, k_scale=k_scale, v_scale=v_scale,
+            scale_granularity=scale_granularity,
         )
         self._registry: dict[str, SequencePagedKVCache] = {}
 

@@ -10,7 +10,11 @@ A pool variant the reference lacks: `kv_dtype=torch.float8_e4m3fn` stores
 K and V as OCP fp8 e4m3 with one fp32 scale per pool (stored =
 e4m3(clamp(x / scale, -448, 448)), decoded = float(stored) * scale), half the
 bytes of bf16 pools. The API is unchanged: writes take rows in `dtype`, reads
-and attention see the decoded values.
+and attention see the decoded values. With `scale_granularity="row"` every pool
+row (one token of one KV head) gets a scale of its own, s = max|row| / 448
+(1 for an all-zero or non-finite maximum), kept beside the pools as float32
+[L, NB, Hkv, BS] arrays that the append kernels write and the attention and
+gather kernels read (4 bytes per Dh code bytes: 1/32 more at Dh 128).
 """
 
 from __future__ import annotations
@@ -38,6 +42,7 @@ class PagedKVStorage:
         kv_dtype: torch.dtype | None = None,
         k_scale: float = 1.0,
         v_scale: float = 1.0,
+        scale_granularity: str = "pool",
     ) -> None:
         for name, size in (
             ("num_layers", num_layers),
@@ -65,9 +70,20 @@ class PagedKVStorage:
                 raise ValueError("k_scale and v_scale must be positive finite floats")
         elif self.k_scale != 1.0 or self.v_scale != 1.0:
             raise ValueError("k_scale and v_scale apply to fp8 pools only")
+        if scale_granularity not in ("pool", "row"):
+            raise ValueError('scale_granularity must be "pool" or "row"')
+        if scale_granularity == "row" and (self.kv_dtype != ops.FP8_POOL_DTYPE
+                                           or self.k_scale != 1.0 or self.v_scale != 1.0):
+            raise ValueError("per-row scales need fp8 pools and no pool scales")
+        self.scale_granularity = scale_granularity
         shape = (num_layers, num_blocks, num_key_value_heads, block_size, head_dim)
         self._key_storage = torch.empty(shape, device=self.device, dtype=self.kv_dtype)
         self._value_storage = torch.empty(shape, device=self.device, dtype=self.kv_dtype)
+        self._key_scales: torch.Tensor | None = None
+        self._value_scales: torch.Tensor | None = None
+        if scale_granularity == "row":
+            self._key_scales = torch.ones(shape[:4], device=self.device, dtype=torch.float32)
+            self._value_scales = torch.ones(shape[:4], device=self.device, dtype=torch.float32)
 
     @property
     def storage_shape(self) -> tuple[int, ...]:
@@ -86,9 +102,24 @@ class PagedKVStorage:
         return self._value_storage
 
     @property
-    def scales(self) -> dict[str, float]:
-        """Pool decode factors as the kernels' keyword arguments."""
+    def key_scales(self) -> torch.Tensor | None:
+        """Per-row K scales, float32 [L, NB, Hkv, BS] (None with per-pool scales)."""
 
+        return self._key_scales
+
+    @property
+    def value_scales(self) -> torch.Tensor | None:
+        """Per-row V scales, float32 [L, NB, Hkv, BS] (None with per-pool scales)."""
+
+        return self._value_scales
+
+    @property
+    def scales(self) -> dict[str, float | torch.Tensor]:
+        """Decode factors as the kernels' keyword arguments: the pool scales, or the
+        per-row scale arrays."""
+
+        if self._key_scales is not None:
+            return {"k_scales": self._key_scales, "v_scales": self._value_scales}
         return {"k_scale": self.k_scale, "v_scale": self.v_scale}
 
     # ------------------------------------------------------------- single slot

@@ -15,7 +15,7 @@ from pathlib import Path
 import torch
 
 LIBRARY_NAME = "libtokserve_hip.so"
-ABI_VERSION = 11
+ABI_VERSION = 12
 
 TKS_OK = 0
 TKS_ERR_VALUE = -1
@@ -141,6 +141,46 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         [_c_void_p, _i64, _i64, _c_void_p, _c_void_p, _i32, _i64, _i32, _i32, _i32, _i32,
          _c_void_p, _i32, _c_void_p, _c_void_p, _c_void_p, _i32, _i64, _i32, _i32, _i32, _f32,
          _c_void_p, _i64, _i64, _c_void_p, _i64, _f32, _f32, _i32, _c_void_p],
+    ),
+    # fp8 pools with one scale per pool row: the scale arrays follow the pools.
+    "tks_kv_append_fp8_rows": (
+        _i32,
+        [_c_void_p, _i64, _i64, _c_void_p, _i64, _i64, _i64, _c_void_p, _c_void_p,
+         _c_void_p, _c_void_p, _i32, _i64, _i32, _i32, _i32, _i32, _c_void_p, _i32, _c_void_p],
+    ),
+    "tks_paged_gather_fp8_rows": (
+        _i32,
+        [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _i32, _i64, _i32, _i32, _i32, _i32,
+         _c_void_p, _i32, _c_void_p, _c_void_p, _i32, _i32, _c_void_p, _c_void_p, _i64, _i64,
+         _i32, _c_void_p],
+    ),
+    "tks_paged_attention_decode_fp8_rows": (
+        _i32,
+        [_c_void_p, _i64, _i64, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _i32, _i64, _i32,
+         _i32, _i32, _i32, _c_void_p, _i32, _c_void_p, _c_void_p, _i32, _i32, _i32, _f32, _i32,
+         _c_void_p, _i64, _i64, _c_void_p, _i64, _i32, _c_void_p],
+    ),
+    "tks_paged_attention_prefill_fp8_rows": (
+        _i32,
+        [_c_void_p, _i64, _i64, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _i32, _i64, _i32,
+         _i32, _i32, _i32, _c_void_p, _i32, _c_void_p, _c_void_p, _c_void_p, _i32, _i64, _i32,
+         _i32, _i32, _f32, _c_void_p, _i64, _i64, _c_void_p, _i64, _i32, _c_void_p],
+    ),
+    "tks_rope_kv_append_fp8_rows": (
+        _i32,
+        [_c_void_p, _c_void_p, _i64, _i64, _i64, _i64, _i32,
+         _c_void_p, _c_void_p, _i64, _i64, _i64, _i64,
+         _c_void_p, _i64, _i64, _i32, _i64, _i32, _c_void_p, _c_void_p, _c_void_p, _i64,
+         _c_void_p, _c_void_p, _c_void_p, _c_void_p, _i32, _i64, _i32, _i32, _c_void_p, _i32,
+         _c_void_p],
+    ),
+    "tks_rope_append_paged_decode_fp8_rows": (
+        _i32,
+        [_c_void_p, _i64, _i64, _c_void_p, _i64, _i64, _c_void_p, _i64, _i64,
+         _c_void_p, _c_void_p, _c_void_p, _i64, _c_void_p,
+         _c_void_p, _c_void_p, _c_void_p, _c_void_p, _i32, _i64, _i32, _i32, _i32, _i32,
+         _c_void_p, _i32, _c_void_p, _c_void_p, _i32, _i32, _i32, _f32, _i32,
+         _c_void_p, _i64, _i64, _c_void_p, _i64, _i32, _c_void_p],
     ),
 }
 

@@ -65,6 +65,39 @@ def _pool_scales(pool: torch.Tensor, k_scale: float, v_scale: float) -> tuple[fl
     return k_scale, v_scale
 
 
+def _row_scales(
+    operation: str,
+    key_cache: torch.Tensor,
+    k_scales: torch.Tensor | None,
+    v_scales: torch.Tensor | None,
+    k_scale: float,
+    v_scale: float,
+) -> tuple[torch.Tensor | None, torch.Tensor | None]:
+    """Per-row scales of fp8 pools: float32 (L, NB, Hkv, BS) each, on the pools'
+    device, contiguous, or both None (per-pool scales k_scale / v_scale apply).
+
+    Row (l, b, h, r) of a pool holds e4m3(clamp(x / s, -448, 448)) with
+    s = k_scales[l, b, h, r] (v_scales for the value pool), decoded as code * s;
+    the pool scales must then stay 1.
+    """
+
+    if k_scales is None and v_scales is None:
+        return None, None
+    if k_scales is None or v_scales is None:
+        raise ValueError(f"{operation}: k_scales and v_scales go together")
+    if not is_fp8_pool(key_cache):
+        raise ValueError("per-row scales apply to fp8 KV pools only")
+    if k_scale != 1.0 or v_scale != 1.0:
+        raise ValueError("per-row scales replace k_scale and v_scale, which must stay 1")
+    require_hip(operation, key_cache, k_scales, v_scales)
+    for name, scales in (("k_scales", k_scales), ("v_scales", v_scales)):
+        if scales.dtype != torch.float32:
+            raise TypeError(f"{name} must be float32")
+        if scales.shape != key_cache.shape[:4] or not scales.is_contiguous():
+            raise ValueError(f"{name} must be a contiguous (L, NB, Hkv, BS) tensor")
+    return k_scales, v_scales
+
+
 def _last_dim_contiguous(tensor: torch.Tensor, name: str) -> torch.Tensor:
     return tensor if tensor.stride(-1) == 1 else tensor.contiguous()
 
@@ -89,11 +122,16 @@ def kv_append(
     *,
     k_scale: float = 1.0,
     v_scale: float = 1.0,
+    k_scales: torch.Tensor | None = None,
+    v_scales: torch.Tensor | None = None,
 ) -> None:
     """Scatter K/V rows (N, Hkv, Dh) into the pools at slot_mapping (int64, N).
 
-    fp8 pools quantize the rows with the pool scales (k_scale, v_scale); pools
-    in a float dtype take rows of that dtype, copied bit for bit.
+    fp8 pools quantize the rows with the pool scales (k_scale, v_scale), or, given
+    k_scales / v_scales (float32 (L, NB, Hkv, BS)), each row with a scale of its
+    own, s = max|row| / 448 (1 for an all-zero or non-finite maximum), written to
+    the row's entry of k_scales / v_scales. Pools in a float dtype take rows of
+    that dtype, copied bit for bit.
     """
 
     require_hip("kv_append", key, value, key_cache, value_cache, slot_mapping)
@@ -106,6 +144,7 @@ def kv_append(
         raise ValueError("key rows must match the pool's (Hkv, Dh)")
     fp8 = is_fp8_pool(key_cache)
     k_scale, v_scale = _pool_scales(key_cache, k_scale, v_scale)
+    k_scales, v_scales = _row_scales("kv_append", key_cache, k_scales, v_scales, k_scale, v_scale)
     if value.dtype != key.dtype or (not fp8 and key.dtype != key_cache.dtype):
         raise ValueError("keys and values must match the storage dtype")
     if slot_mapping.shape != (key.shape[0],):
@@ -113,7 +152,8 @@ def kv_append(
     slots = _int_tensor(slot_mapping, torch.int64, "slot_mapping")
     key = _last_dim_contiguous(key, "key")
     value = _last_dim_contiguous(value, "value")
-    _ops.kv_append(key, value, key_cache, value_cache, slots, layer_index, k_scale, v_scale)
+    _ops.kv_append(key, value, key_cache, value_cache, slots, layer_index, k_scale, v_scale,
+                   k_scales, v_scales)
 
 
 def paged_gather(
@@ -129,12 +169,15 @@ def paged_gather(
     *,
     k_scale: float = 1.0,
     v_scale: float = 1.0,
+    k_scales: torch.Tensor | None = None,
+    v_scales: torch.Tensor | None = None,
 ) -> None:
     """Copy each sequence's K/V in logical order into key_out/value_out.
 
     key_out/value_out are (S_total, Hkv, Dh) views (any token/head strides, Dh
     contiguous); sequence b fills rows cu_seqlens[b] .. cu_seqlens[b]+seq_lens[b]-1.
-    fp8 pools are decoded with their scales into the outputs' float dtype.
+    fp8 pools are decoded with their scales (per pool, or per row with
+    k_scales / v_scales) into the outputs' float dtype.
     """
 
     require_hip(
@@ -157,10 +200,12 @@ def paged_gather(
         raise ValueError("outputs must be contiguous in head_dim")
     fp8 = is_fp8_pool(key_cache)
     k_scale, v_scale = _pool_scales(key_cache, k_scale, v_scale)
+    k_scales, v_scales = _row_scales("paged_gather", key_cache, k_scales, v_scales, k_scale,
+                                     v_scale)
     if value_out.dtype != key_out.dtype or (not fp8 and key_out.dtype != key_cache.dtype):
         raise ValueError("outputs must match the storage dtype")
     _ops.paged_gather(key_cache, value_cache, tables, lens, cu, layer_index, max_seq_len,
-                      key_out, value_out, k_scale, v_scale)
+                      key_out, value_out, k_scale, v_scale, k_scales, v_scales)
 
 
 # ----------------------------------------------------------------------------
@@ -234,6 +279,8 @@ def paged_attention_decode(
     seq_order: torch.Tensor | None = None,
     k_scale: float = 1.0,
     v_scale: float = 1.0,
+    k_scales: torch.Tensor | None = None,
+    v_scales: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """One query token per sequence: query (B, Hq, Dh) -> out (B, Hq, Dh).
 
@@ -245,7 +292,7 @@ def paged_attention_decode(
     `seq_order` (int32 permutation of 0..B-1, see longest_first) is the order in
     which sequences reach workgroups; longest-first avoids a tail of long
     sequences. Results do not depend on it. fp8 pools are decoded with
-    (k_scale, v_scale).
+    (k_scale, v_scale), or per row with k_scales / v_scales.
     """
 
     require_hip("paged_attention_decode", query, key_cache, value_cache, block_tables, seq_lens)
@@ -256,6 +303,8 @@ def paged_attention_decode(
         raise ValueError("query must have shape (B, Hq, Dh) with the pool's Dh")
     fp8 = is_fp8_pool(key_cache)
     k_scale, v_scale = _pool_scales(key_cache, k_scale, v_scale)
+    k_scales, v_scales = _row_scales("paged_attention_decode", key_cache, k_scales, v_scales,
+                                     k_scale, v_scale)
     if not fp8 and query.dtype != key_cache.dtype:
         raise ValueError("query and paged storage must use the same dtype")
     num_seqs, num_q_heads, _ = query.shape
@@ -274,7 +323,7 @@ def paged_attention_decode(
     _check_workspace("paged_attention_decode", query, workspace)
     _ops.paged_attention_decode(query, key_cache, value_cache, tables, lens, order, layer_index,
                                 max_seq_len, float(scale), pages_per_split, k_scale, v_scale, out,
-                                workspace)
+                                workspace, k_scales, v_scales)
     return out
 
 
@@ -335,6 +384,8 @@ def paged_attention_prefill(
     seq_order: torch.Tensor | None = None,
     k_scale: float = 1.0,
     v_scale: float = 1.0,
+    k_scales: torch.Tensor | None = None,
+    v_scales: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """Causal attention of packed query chunks (N, Hq, Dh) over their paged KV.
 
@@ -343,7 +394,7 @@ def paged_attention_prefill(
     position seq_lens[b] - q_len_b + i. `seq_order` (int32 permutation of 0..B-1,
     e.g. longest_first of seq_lens) is the order in which sequences reach
     workgroups; results do not depend on it. fp8 pools are decoded with
-    (k_scale, v_scale).
+    (k_scale, v_scale), or per row with k_scales / v_scales.
     """
 
     require_hip(
@@ -357,6 +408,8 @@ def paged_attention_prefill(
         raise ValueError("query must have shape (N, Hq, Dh) with the pool's Dh")
     fp8 = is_fp8_pool(key_cache)
     k_scale, v_scale = _pool_scales(key_cache, k_scale, v_scale)
+    k_scales, v_scales = _row_scales("paged_attention_prefill", key_cache, k_scales, v_scales,
+                                     k_scale, v_scale)
     if not fp8 and query.dtype != key_cache.dtype:
         raise ValueError("query and paged storage must use the same dtype")
     num_q_heads = query.shape[1]
@@ -376,7 +429,7 @@ def paged_attention_prefill(
     order = _seq_order("paged_attention_prefill", lens, seq_order)
     _ops.paged_attention_prefill(query, key_cache, value_cache, tables, lens, cu, order,
                                  layer_index, max_query_len, max_seq_len, float(scale), k_scale,
-                                 v_scale, out)
+                                 v_scale, out, k_scales, v_scales)
     return out
 
 
@@ -538,13 +591,16 @@ def rope_kv_append(
     key_out: torch.Tensor | None = None,
     k_scale: float = 1.0,
     v_scale: float = 1.0,
+    k_scales: torch.Tensor | None = None,
+    v_scales: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """Packed step: rotate query (N, Hq, Dh) into query_out (in place by default), rotate
     key (N, Hkv, Dh) and append it with value (N, Hkv, Dh) to the pools at slot_mapping.
 
     One launch, bit-identical to rope() followed by kv_append() of the rotated keys.
     key_out, when given, also receives the rotated keys. Pools in the rows' dtype, or
-    fp8 pools quantized with k_scale / v_scale as kv_append() does.
+    fp8 pools quantized with k_scale / v_scale, or per row into k_scales / v_scales, as
+    kv_append() does.
     """
 
     require_hip("rope_kv_append", query, key, value, positions, key_cache, value_cache,
@@ -558,6 +614,8 @@ def rope_kv_append(
     if key.shape != (tokens, num_kv_heads, head_dim) or query.shape[2] != head_dim:
         raise ValueError("key and value rows must match the pool's (Hkv, Dh)")
     k_scale, v_scale = _pool_scales(key_cache, k_scale, v_scale)
+    k_scales, v_scales = _row_scales("rope_kv_append", key_cache, k_scales, v_scales, k_scale,
+                                     v_scale)
     pool_dtype = query.dtype if is_fp8_pool(key_cache) else key_cache.dtype
     if len({query.dtype, key.dtype, value.dtype, pool_dtype, table.dtype}) != 1:
         raise ValueError("query, key, value, pools and the rotary table must share a dtype")
@@ -579,10 +637,12 @@ def rope_kv_append(
         raise ValueError("key_out must match key and be contiguous in head_dim")
     if query_out is query:
         _ops.rope_kv_append_(query, key, value, pos, table.cos, table.sin, key_cache,
-                             value_cache, slots, layer_index, key_out, k_scale, v_scale)
+                             value_cache, slots, layer_index, key_out, k_scale, v_scale,
+                             k_scales, v_scales)
     else:
         _ops.rope_kv_append(query, key, value, pos, table.cos, table.sin, key_cache, value_cache,
-                            slots, layer_index, query_out, key_out, k_scale, v_scale)
+                            slots, layer_index, query_out, key_out, k_scale, v_scale, k_scales,
+                            v_scales)
     return query_out
 
 
@@ -607,6 +667,8 @@ def rope_append_paged_decode(
     seq_order: torch.Tensor | None = None,
     k_scale: float = 1.0,
     v_scale: float = 1.0,
+    k_scales: torch.Tensor | None = None,
+    v_scales: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """A decode step's RoPE, KV append and attention in one call: query (B, Hq, Dh) is
     rotated at positions (B,) (read only), the rotated key and the value rows (B, Hkv, Dh)
@@ -614,8 +676,9 @@ def rope_append_paged_decode(
     out (B, Hq, Dh) receives the attention over seq_lens[b] keys.
 
     Bit-identical to rope_kv_append() followed by paged_attention_decode() with the
-    same arguments (one launch on the MFMA decode kernel). Pools in the rows' dtype, or
-    fp8 pools with their scales.
+    same arguments (one launch on the MFMA decode kernel; with per-row scales the append
+    is a launch of its own ahead of the attention). Pools in the rows' dtype, or fp8
+    pools with their scales (per pool, or per row with k_scales / v_scales).
     """
 
     require_hip("rope_append_paged_decode", query, key, value, positions, key_cache,
@@ -624,6 +687,8 @@ def rope_append_paged_decode(
         key_cache, value_cache
     )
     k_scale, v_scale = _pool_scales(key_cache, k_scale, v_scale)
+    k_scales, v_scales = _row_scales("rope_append_paged_decode", key_cache, k_scales, v_scales,
+                                     k_scale, v_scale)
     if query.ndim != 3 or key.ndim != 3 or value.shape != key.shape:
         raise ValueError("query (B, Hq, Dh), key and value (B, Hkv, Dh) expected")
     num_seqs, num_q_heads, _ = query.shape
@@ -658,7 +723,8 @@ def rope_append_paged_decode(
     _check_workspace("rope_append_paged_decode", query, workspace)
     _ops.rope_append_paged_decode(query, key, value, pos, table.cos, table.sin, slots, key_cache,
                                   value_cache, tables, lens, order, layer_index, max_seq_len,
-                                  float(scale), pages_per_split, out, workspace, k_scale, v_scale)
+                                  float(scale), pages_per_split, out, workspace, k_scale, v_scale,
+                                  k_scales, v_scales)
     return out
 
 

@@ -46,18 +46,21 @@ FP8_POOL_DTYPE = torch.float8_e4m3fn
 SCHEMAS = {
     "kv_append": (
         "kv_append(Tensor key, Tensor value, Tensor(a!) key_cache, Tensor(b!) value_cache, "
-        "Tensor slot_mapping, int layer_index, float k_scale, float v_scale) -> ()"
+        "Tensor slot_mapping, int layer_index, float k_scale, float v_scale, "
+        "Tensor(c!)? k_scales=None, Tensor(d!)? v_scales=None) -> ()"
     ),
     "paged_gather": (
         "paged_gather(Tensor key_cache, Tensor value_cache, Tensor block_tables, "
         "Tensor seq_lens, Tensor cu_seqlens, int layer_index, int max_seq_len, "
-        "Tensor(a!) key_out, Tensor(b!) value_out, float k_scale, float v_scale) -> ()"
+        "Tensor(a!) key_out, Tensor(b!) value_out, float k_scale, float v_scale, "
+        "Tensor? k_scales=None, Tensor? v_scales=None) -> ()"
     ),
     "paged_attention_decode": (
         "paged_attention_decode(Tensor query, Tensor key_cache, Tensor value_cache, "
         "Tensor block_tables, Tensor seq_lens, Tensor? seq_order, int layer_index, "
         "int max_seq_len, float scale, int pages_per_split, float k_scale, float v_scale, "
-        "Tensor(a!) out, Tensor(b!)? workspace) -> ()"
+        "Tensor(a!) out, Tensor(b!)? workspace, Tensor? k_scales=None, "
+        "Tensor? v_scales=None) -> ()"
     ),
     "paged_attention_decode_noalloc": (
         "paged_attention_decode_noalloc(Tensor query, Tensor key_cache, Tensor value_cache, "
@@ -69,7 +72,7 @@ SCHEMAS = {
         "Tensor block_tables, Tensor seq_lens, Tensor cu_seqlens_q, Tensor? seq_order, "
         "int layer_index, "
         "int max_query_len, int max_seq_len, float scale, float k_scale, float v_scale, "
-        "Tensor(a!) out) -> ()"
+        "Tensor(a!) out, Tensor? k_scales=None, Tensor? v_scales=None) -> ()"
     ),
     "rms_norm": (
         "rms_norm(Tensor input, Tensor weight, float epsilon, Tensor? residual, "
@@ -86,44 +89,51 @@ SCHEMAS = {
         "rope_kv_append(Tensor query, Tensor key, Tensor value, Tensor positions, Tensor cos, "
         "Tensor sin, Tensor(a!) key_cache, Tensor(b!) value_cache, Tensor slot_mapping, "
         "int layer_index, Tensor(c!) query_out, Tensor(d!)? key_out, float k_scale=1.0, "
-        "float v_scale=1.0) -> ()"
+        "float v_scale=1.0, Tensor(e!)? k_scales=None, Tensor(f!)? v_scales=None) -> ()"
     ),
     "rope_kv_append_": (
         "rope_kv_append_(Tensor(a!) query, Tensor key, Tensor value, Tensor positions, "
         "Tensor cos, Tensor sin, Tensor(b!) key_cache, Tensor(c!) value_cache, "
         "Tensor slot_mapping, int layer_index, Tensor(d!)? key_out, float k_scale=1.0, "
-        "float v_scale=1.0) -> ()"
+        "float v_scale=1.0, Tensor(e!)? k_scales=None, Tensor(f!)? v_scales=None) -> ()"
     ),
     "rope_append_paged_decode": (
         "rope_append_paged_decode(Tensor query, Tensor key, Tensor value, Tensor positions, "
         "Tensor cos, Tensor sin, Tensor slot_mapping, Tensor(a!) key_cache, "
         "Tensor(b!) value_cache, Tensor block_tables, Tensor seq_lens, Tensor? seq_order, "
         "int layer_index, int max_seq_len, float scale, int pages_per_split, Tensor(c!) out, "
-        "Tensor(d!)? workspace, float k_scale=1.0, float v_scale=1.0) -> ()"
+        "Tensor(d!)? workspace, float k_scale=1.0, float v_scale=1.0, "
+        "Tensor(e!)? k_scales=None, Tensor(f!)? v_scales=None) -> ()"
     ),
     "greedy_argmax": "greedy_argmax(Tensor logits, Tensor(a!) out) -> ()",
     "silu_mul": "silu_mul(Tensor gate_up, Tensor(a!) out) -> ()",
     "vector_add": "vector_add(Tensor x, Tensor y, Tensor(a!) out) -> ()",
 }
 
-# Entry points behind each operator (the *_fp8 ones serve e4m3 pools).
+# Entry points behind each operator (the *_fp8 ones serve e4m3 pools with one scale per
+# pool, the *_fp8_rows ones e4m3 pools with one scale per pool row).
 ENTRY_POINTS = {
-    "kv_append": ("tks_kv_append", "tks_kv_append_fp8"),
-    "paged_gather": ("tks_paged_gather", "tks_paged_gather_fp8"),
+    "kv_append": ("tks_kv_append", "tks_kv_append_fp8", "tks_kv_append_fp8_rows"),
+    "paged_gather": ("tks_paged_gather", "tks_paged_gather_fp8", "tks_paged_gather_fp8_rows"),
     "paged_attention_decode": ("tks_paged_attention_decode_workspace_bytes",
-                               "tks_paged_attention_decode", "tks_paged_attention_decode_fp8"),
+                               "tks_paged_attention_decode", "tks_paged_attention_decode_fp8",
+                               "tks_paged_attention_decode_fp8_rows"),
     "paged_attention_decode_noalloc": ("tks_paged_attention_decode_noalloc",
                                        "tks_paged_attention_decode_noalloc_max_workspace_bytes"),
     "paged_attention_prefill": ("tks_paged_attention_prefill",
                                 "tks_paged_attention_prefill_fp8_workspace_bytes",
-                                "tks_paged_attention_prefill_fp8"),
+                                "tks_paged_attention_prefill_fp8",
+                                "tks_paged_attention_prefill_fp8_rows"),
     "rms_norm": ("tks_rms_norm",),
     "rope": ("tks_rope",),
     "rope_": ("tks_rope",),
-    "rope_kv_append": ("tks_rope_kv_append", "tks_rope_kv_append_fp8"),
-    "rope_kv_append_": ("tks_rope_kv_append", "tks_rope_kv_append_fp8"),
+    "rope_kv_append": ("tks_rope_kv_append", "tks_rope_kv_append_fp8",
+                       "tks_rope_kv_append_fp8_rows"),
+    "rope_kv_append_": ("tks_rope_kv_append", "tks_rope_kv_append_fp8",
+                        "tks_rope_kv_append_fp8_rows"),
     "rope_append_paged_decode": ("tks_rope_append_paged_decode",
                                  "tks_rope_append_paged_decode_fp8",
+                                 "tks_rope_append_paged_decode_fp8_rows",
                                  "tks_paged_attention_decode_workspace_bytes"),
     "greedy_argmax": ("tks_argmax",),
     "silu_mul": ("tks_silu_mul",),
@@ -181,14 +191,19 @@ def decode_workspace_bytes(num_seqs: int, num_q_heads: int, num_kv_heads: int, h
 # Device kernels
 
 
-def _kv_append(key, value, key_cache, value_cache, slot_mapping, layer_index, k_scale, v_scale):
+def _kv_append(key, value, key_cache, value_cache, slot_mapping, layer_index, k_scale, v_scale,
+               k_scales=None, v_scales=None):
     dims = _pool_dims(key_cache)
-    common = (key.data_ptr(), key.stride(0), key.stride(1),
-              value.data_ptr(), value.stride(0), value.stride(1), key.shape[0],
-              key_cache.data_ptr(), value_cache.data_ptr(), *dims, layer_index,
-              slot_mapping.data_ptr())
+    rows = (key.data_ptr(), key.stride(0), key.stride(1),
+            value.data_ptr(), value.stride(0), value.stride(1), key.shape[0],
+            key_cache.data_ptr(), value_cache.data_ptr())
+    common = (*rows, *dims, layer_index, slot_mapping.data_ptr())
     library = _lib.load()
-    if key_cache.dtype == FP8_POOL_DTYPE:
+    if k_scales is not None:
+        status = library.tks_kv_append_fp8_rows(*rows, k_scales.data_ptr(), v_scales.data_ptr(),
+                                                *dims, layer_index, slot_mapping.data_ptr(),
+                                                _code(key), _stream(key))
+    elif key_cache.dtype == FP8_POOL_DTYPE:
         status = library.tks_kv_append_fp8(*common, k_scale, v_scale, _code(key), _stream(key))
     else:
         status = library.tks_kv_append(*common, _code(key), _stream(key))
@@ -196,13 +211,19 @@ def _kv_append(key, value, key_cache, value_cache, slot_mapping, layer_index, k_
 
 
 def _paged_gather(key_cache, value_cache, block_tables, seq_lens, cu_seqlens, layer_index,
-                  max_seq_len, key_out, value_out, k_scale, v_scale):
-    common = (key_cache.data_ptr(), value_cache.data_ptr(), *_pool_dims(key_cache), layer_index,
-              block_tables.data_ptr(), block_tables.shape[1], seq_lens.data_ptr(),
-              cu_seqlens.data_ptr(), block_tables.shape[0], max_seq_len,
-              key_out.data_ptr(), value_out.data_ptr(), key_out.stride(0), key_out.stride(1))
+                  max_seq_len, key_out, value_out, k_scale, v_scale, k_scales=None,
+                  v_scales=None):
+    rest = (*_pool_dims(key_cache), layer_index,
+            block_tables.data_ptr(), block_tables.shape[1], seq_lens.data_ptr(),
+            cu_seqlens.data_ptr(), block_tables.shape[0], max_seq_len,
+            key_out.data_ptr(), value_out.data_ptr(), key_out.stride(0), key_out.stride(1))
+    common = (key_cache.data_ptr(), value_cache.data_ptr(), *rest)
     library = _lib.load()
-    if key_cache.dtype == FP8_POOL_DTYPE:
+    if k_scales is not None:
+        status = library.tks_paged_gather_fp8_rows(
+            key_cache.data_ptr(), value_cache.data_ptr(), k_scales.data_ptr(),
+            v_scales.data_ptr(), *rest, _code(key_out), _stream(key_cache))
+    elif key_cache.dtype == FP8_POOL_DTYPE:
         status = library.tks_paged_gather_fp8(*common, k_scale, v_scale, _code(key_out),
                                               _stream(key_cache))
     else:
@@ -221,7 +242,7 @@ def _decode_common(query, key_cache, value_cache, block_tables, seq_lens, seq_or
 
 def _paged_attention_decode(query, key_cache, value_cache, block_tables, seq_lens, seq_order,
                             layer_index, max_seq_len, scale, pages_per_split, k_scale, v_scale,
-                            out, workspace_tensor):
+                            out, workspace_tensor, k_scales=None, v_scales=None):
     _, _, num_kv_heads, block_size, head_dim = _pool_dims(key_cache)
     if workspace_tensor is None:
         nbytes = decode_workspace_bytes(query.shape[0], query.shape[1], num_kv_heads, head_dim,
@@ -231,7 +252,12 @@ def _paged_attention_decode(query, key_cache, value_cache, block_tables, seq_len
                             layer_index, max_seq_len, scale, pages_per_split, out)
     ws = (_lib.ptr(workspace_tensor), 0 if workspace_tensor is None else workspace_tensor.numel())
     library = _lib.load()
-    if key_cache.dtype == FP8_POOL_DTYPE:
+    if k_scales is not None:
+        # The row entry takes the scale arrays right after the pools.
+        status = library.tks_paged_attention_decode_fp8_rows(
+            *common[:5], k_scales.data_ptr(), v_scales.data_ptr(), *common[5:], *ws,
+            _code(query), _stream(query))
+    elif key_cache.dtype == FP8_POOL_DTYPE:
         status = library.tks_paged_attention_decode_fp8(*common, *ws, k_scale, v_scale,
                                                         _code(query), _stream(query))
     else:
@@ -251,7 +277,7 @@ def _paged_attention_decode_noalloc(query, key_cache, value_cache, block_tables,
 
 def _paged_attention_prefill(query, key_cache, value_cache, block_tables, seq_lens,
                              cu_seqlens_q, seq_order, layer_index, max_query_len, max_seq_len,
-                             scale, k_scale, v_scale, out):
+                             scale, k_scale, v_scale, out, k_scales=None, v_scales=None):
     dims = _pool_dims(key_cache)
     num_seqs = seq_lens.shape[0]
     common = (query.data_ptr(), query.stride(0), query.stride(1),
@@ -269,9 +295,15 @@ def _paged_attention_prefill(query, key_cache, value_cache, block_tables, seq_le
         if nbytes < 0:
             raise ValueError("invalid fp8 prefill workspace query")
         scratch = workspace(query.device, nbytes, "prefill_fp8_pages")
-        status = library.tks_paged_attention_prefill_fp8(
-            *common, _lib.ptr(scratch), 0 if scratch is None else scratch.numel(), k_scale,
-            v_scale, _code(query), _stream(query))
+        ws = (_lib.ptr(scratch), 0 if scratch is None else scratch.numel())
+        if k_scales is not None:
+            # The row entry takes the scale arrays right after the pools.
+            status = library.tks_paged_attention_prefill_fp8_rows(
+                *common[:5], k_scales.data_ptr(), v_scales.data_ptr(), *common[5:], *ws,
+                _code(query), _stream(query))
+        else:
+            status = library.tks_paged_attention_prefill_fp8(
+                *common, *ws, k_scale, v_scale, _code(query), _stream(query))
     else:
         status = library.tks_paged_attention_prefill(*common, _code(query), _stream(query))
     _lib.check(status, "paged_attention_prefill")
@@ -309,12 +341,19 @@ def _rope_inplace(query, key, positions, cos, sin):
 
 
 def _rope_kv_append_launch(query, query_out, key, value, positions, cos, sin, key_cache,
-                           value_cache, slot_mapping, layer_index, key_out, k_scale, v_scale):
+                           value_cache, slot_mapping, layer_index, key_out, k_scale, v_scale,
+                           k_scales, v_scales):
     num_layers, num_blocks, num_kv_heads, block_size, head_dim = _pool_dims(key_cache)
     library = _lib.load()
     fp8 = key_cache.dtype == FP8_POOL_DTYPE
-    scales = (k_scale, v_scale) if fp8 else ()
-    entry = library.tks_rope_kv_append_fp8 if fp8 else library.tks_rope_kv_append
+    pools = (key_cache.data_ptr(), value_cache.data_ptr())
+    if k_scales is not None:
+        entry, scales = library.tks_rope_kv_append_fp8_rows, ()
+        pools += (k_scales.data_ptr(), v_scales.data_ptr())
+    elif fp8:
+        entry, scales = library.tks_rope_kv_append_fp8, (k_scale, v_scale)
+    else:
+        entry, scales = library.tks_rope_kv_append, ()
     status = entry(
         query.data_ptr(), query_out.data_ptr(), query.stride(0), query.stride(1),
         query_out.stride(0), query_out.stride(1), query.shape[1],
@@ -322,27 +361,31 @@ def _rope_kv_append_launch(query, query_out, key, value, positions, cos, sin, ke
         0 if key_out is None else key_out.stride(0), 0 if key_out is None else key_out.stride(1),
         value.data_ptr(), value.stride(0), value.stride(1), num_kv_heads, query.shape[0],
         head_dim, positions.data_ptr(), cos.data_ptr(), sin.data_ptr(), cos.shape[0],
-        key_cache.data_ptr(), value_cache.data_ptr(), num_layers, num_blocks, block_size,
+        *pools, num_layers, num_blocks, block_size,
         layer_index, slot_mapping.data_ptr(), *scales, _code(query), _stream(query))
     _lib.check(status, "rope_kv_append")
 
 
 def _rope_kv_append(query, key, value, positions, cos, sin, key_cache, value_cache,
-                    slot_mapping, layer_index, query_out, key_out, k_scale=1.0, v_scale=1.0):
+                    slot_mapping, layer_index, query_out, key_out, k_scale=1.0, v_scale=1.0,
+                    k_scales=None, v_scales=None):
     _rope_kv_append_launch(query, query_out, key, value, positions, cos, sin, key_cache,
-                           value_cache, slot_mapping, layer_index, key_out, k_scale, v_scale)
+                           value_cache, slot_mapping, layer_index, key_out, k_scale, v_scale,
+                           k_scales, v_scales)
 
 
 def _rope_kv_append_inplace(query, key, value, positions, cos, sin, key_cache, value_cache,
-                            slot_mapping, layer_index, key_out, k_scale=1.0, v_scale=1.0):
+                            slot_mapping, layer_index, key_out, k_scale=1.0, v_scale=1.0,
+                            k_scales=None, v_scales=None):
     _rope_kv_append_launch(query, query, key, value, positions, cos, sin, key_cache,
-                           value_cache, slot_mapping, layer_index, key_out, k_scale, v_scale)
+                           value_cache, slot_mapping, layer_index, key_out, k_scale, v_scale,
+                           k_scales, v_scales)
 
 
 def _rope_append_paged_decode(query, key, value, positions, cos, sin, slot_mapping, key_cache,
                               value_cache, block_tables, seq_lens, seq_order, layer_index,
                               max_seq_len, scale, pages_per_split, out, workspace_tensor,
-                              k_scale=1.0, v_scale=1.0):
+                              k_scale=1.0, v_scale=1.0, k_scales=None, v_scales=None):
     num_layers, num_blocks, num_kv_heads, block_size, head_dim = _pool_dims(key_cache)
     if workspace_tensor is None:
         nbytes = decode_workspace_bytes(query.shape[0], query.shape[1], num_kv_heads, head_dim,
@@ -350,15 +393,20 @@ def _rope_append_paged_decode(query, key, value, positions, cos, sin, slot_mappi
         workspace_tensor = workspace(query.device, nbytes, "decode")
     library = _lib.load()
     fp8 = key_cache.dtype == FP8_POOL_DTYPE
-    scales = (k_scale, v_scale) if fp8 else ()
-    entry = (library.tks_rope_append_paged_decode_fp8 if fp8
-             else library.tks_rope_append_paged_decode)
+    pools = (key_cache.data_ptr(), value_cache.data_ptr())
+    if k_scales is not None:
+        entry, scales = library.tks_rope_append_paged_decode_fp8_rows, ()
+        pools += (k_scales.data_ptr(), v_scales.data_ptr())
+    elif fp8:
+        entry, scales = library.tks_rope_append_paged_decode_fp8, (k_scale, v_scale)
+    else:
+        entry, scales = library.tks_rope_append_paged_decode, ()
     status = entry(
         query.data_ptr(), query.stride(0), query.stride(1),
         key.data_ptr(), key.stride(0), key.stride(1),
         value.data_ptr(), value.stride(0), value.stride(1),
         positions.data_ptr(), cos.data_ptr(), sin.data_ptr(), cos.shape[0],
-        slot_mapping.data_ptr(), key_cache.data_ptr(), value_cache.data_ptr(),
+        slot_mapping.data_ptr(), *pools,
         num_layers, num_blocks, num_kv_heads, block_size, head_dim, layer_index,
         block_tables.data_ptr(), block_tables.shape[1], seq_lens.data_ptr(), _lib.ptr(seq_order),
         query.shape[0], query.shape[1], max_seq_len, scale, pages_per_split,

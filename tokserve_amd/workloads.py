@@ -40,6 +40,16 @@ class PagedBatch:
     query_lens: list[int]         # host copy of per-sequence query counts
     k_scale: float = 1.0          # pool decode factors (fp8 pools)
     v_scale: float = 1.0
+    k_scales: torch.Tensor | None = None  # per-row decode factors (1, NB, Hkv, BS) float32
+    v_scales: torch.Tensor | None = None
+
+    @property
+    def scale_kwargs(self) -> dict:
+        """The pools' decode factors as the operators' keyword arguments."""
+
+        if self.k_scales is not None:
+            return {"k_scales": self.k_scales, "v_scales": self.v_scales}
+        return {"k_scale": self.k_scale, "v_scale": self.v_scale}
 
     @property
     def num_seqs(self) -> int:
@@ -57,7 +67,10 @@ class PagedBatch:
         """Algorithmic K+V bytes one decode pass reads: every visible key once."""
 
         _, _, hkv, _, dh = self.key_cache.shape
-        return sum(self.contexts) * hkv * dh * 2 * self.key_cache.element_size()
+        per_row = dh * self.key_cache.element_size()
+        if self.k_scales is not None:
+            per_row += self.k_scales.element_size()  # each row's scale is read with it
+        return sum(self.contexts) * hkv * 2 * per_row
 
 
 def _tables(
@@ -94,11 +107,15 @@ def paged_batch(
     kv_dtype: torch.dtype | None = None,
     k_scale: float = 1.0,
     v_scale: float = 1.0,
+    scale_granularity: str = "pool",
 ) -> PagedBatch:
     """Build a batch where sequence b has contexts[b] keys, the last query_lens[b] of them queried.
 
     kv_dtype=torch.float8_e4m3fn stores the (same) pools as fp8:
-    e4m3(clamp(x / scale, -448, 448)) with the given per-pool scales.
+    e4m3(clamp(x / scale, -448, 448)) with the given per-pool scales, or, with
+    scale_granularity="row", each pool row (token, KV head) scaled by a seeded
+    factor 2^U[-6, 0] first (values stay O(1)) and stored with a scale of its own,
+    s = max|row| / 448.
     """
 
     device = torch.device(device)
@@ -116,12 +133,32 @@ def paged_batch(
     else:
         key_cache = torch.randn(shape, generator=generator).to(dtype).to(device)
         value_cache = torch.randn(shape, generator=generator).to(dtype).to(device)
+    k_scales = v_scales = None
+    if scale_granularity not in ("pool", "row"):
+        raise ValueError('scale_granularity must be "pool" or "row"')
     if kv_dtype is not None and kv_dtype != dtype:
         if kv_dtype != torch.float8_e4m3fn:
             raise ValueError("kv_dtype must be the batch dtype or torch.float8_e4m3fn")
-        key_cache = (key_cache.float() / k_scale).clamp(-448.0, 448.0).to(kv_dtype)
-        value_cache = (value_cache.float() / v_scale).clamp(-448.0, 448.0).to(kv_dtype)
+        if scale_granularity == "row":
+            if k_scale != 1.0 or v_scale != 1.0:
+                raise ValueError("per-row scales take no pool scales")
+            row_gen = torch.Generator().manual_seed(seed + 2)
+            pools = []
+            for pool in (key_cache, value_cache):
+                factor = 2.0 ** (-6.0 * torch.rand(shape[:4], generator=row_gen))
+                rows = pool.float() * factor.to(pool.device).unsqueeze(-1)
+                amax = rows.abs().amax(dim=-1)
+                s = amax / 448.0
+                s = torch.where((s > 0) & torch.isfinite(s), s, torch.ones_like(s))
+                codes = (rows / s.unsqueeze(-1)).clamp(-448.0, 448.0).to(kv_dtype)
+                pools.append((codes, s.contiguous()))
+            (key_cache, k_scales), (value_cache, v_scales) = pools
+        else:
+            key_cache = (key_cache.float() / k_scale).clamp(-448.0, 448.0).to(kv_dtype)
+            value_cache = (value_cache.float() / v_scale).clamp(-448.0, 448.0).to(kv_dtype)
     else:
+        if scale_granularity == "row":
+            raise ValueError("per-row scales need fp8 pools")
         k_scale = v_scale = 1.0
     n_tokens = sum(query_lens)
     query = torch.randn((n_tokens, num_q_heads, head_dim), generator=generator).to(dtype)
@@ -138,6 +175,8 @@ def paged_batch(
         query_lens=list(query_lens),
         k_scale=float(k_scale),
         v_scale=float(v_scale),
+        k_scales=k_scales,
+        v_scales=v_scales,
     )
 
 
@@ -179,6 +218,22 @@ def decode_llama3_8b_fp8(
         contexts, [1] * num_seqs, num_q_heads=32, num_kv_heads=8, head_dim=128,
         block_size=16, dtype=torch.bfloat16, device=device, seed=seed + 7,
         pool_on_device_rng=torch.device(device).type == "cuda", kv_dtype=torch.float8_e4m3fn,
+    )
+
+
+def decode_llama3_8b_fp8_rows(
+    device: torch.device | str, *, seed: int = 0, num_seqs: int = 256
+) -> PagedBatch:
+    """The Llama-3-8B decode workload with fp8 e4m3 K/V pools and one scale per pool row
+    (each row first scaled by 2^U[-6, 0], so the scales span two decades)."""
+
+    gen = torch.Generator().manual_seed(seed)
+    contexts = log_uniform_contexts(num_seqs, 128, 8192, gen)
+    return paged_batch(
+        contexts, [1] * num_seqs, num_q_heads=32, num_kv_heads=8, head_dim=128,
+        block_size=16, dtype=torch.bfloat16, device=device, seed=seed + 7,
+        pool_on_device_rng=torch.device(device).type == "cuda", kv_dtype=torch.float8_e4m3fn,
+        scale_granularity="row",
     )
 
 
