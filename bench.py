@@ -1252,17 +1252,30 @@ def e2e_cpu_baseline(model, specs, target_seconds: float) -> dict:
 
 
 def copy_calibration(device, gib: int = 1, repeats: int = 5) -> None:
-    """A plain device copy of known size, for scaling rocprofv3 FETCH_SIZE/WRITE_SIZE:
-    each launch reads and writes exactly `gib` GiB."""
+    """Kernels of known HBM bytes, for scaling rocprofv3 read/write counters: a plain
+    device copy (`gib` GiB read and written per launch), then this library's
+    tks_vector_add over two `gib`/2 GiB fp32 inputs (`gib` GiB read, `gib`/2 written)."""
 
     import torch
+
+    from tokserve_amd.kernels import ops
 
     src = torch.empty(gib << 30, dtype=torch.uint8, device=device).fill_(1)
     dst = torch.empty_like(src)
     for _ in range(repeats):
         dst.copy_(src)
     torch.cuda.synchronize()
-    print(json.dumps({"copy_calibration_bytes_per_launch": gib << 30, "launches": repeats}),
+    del src, dst
+    half = (gib << 30) // 8  # fp32 elements of gib / 2 GiB
+    x = torch.ones(half, dtype=torch.float32, device=device)
+    y = torch.ones_like(x)
+    out = torch.empty_like(x)
+    for _ in range(repeats):
+        ops.vector_add(x, y, out=out)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_calibration_bytes_per_launch": gib << 30,
+                      "vector_add_read_bytes_per_launch": 2 * half * 4,
+                      "vector_add_write_bytes_per_launch": half * 4, "launches": repeats}),
           flush=True)
 
 
