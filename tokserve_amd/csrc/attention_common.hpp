@@ -104,6 +104,54 @@ __device__ __forceinline__ float merge_splits(const float *__restrict__ ws_m,
   return o;
 }
 
+typedef __attribute__((address_space(3))) void lds_void;
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+// Byte address of an LDS object, as LDS instructions take it.
+template <typename P>
+__device__ __forceinline__ uint32_t lds_address(P *p) {
+  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_void *)(p)));
+}
+
+// One 16-byte HBM -> LDS load per lane: lane i's bytes land at lds + 16 * i
+// (lds is wave-uniform). The compiler cannot tell which LDS bytes such a load
+// writes, so it makes every later LDS access of the wave wait for all of them;
+// kernels that keep such loads in flight read their LDS through inline asm.
+// AUX is the load's cache policy (kLdsNonTemporal: data read once, streamed).
+constexpr int kLdsNonTemporal = 2;
+template <int AUX = 0>
+__device__ __forceinline__ void load_lds16(const void *src, void *lds) {
+#if __HIP_DEVICE_COMPILE__
+  __builtin_amdgcn_global_load_lds(src, (lds_void *)lds, 16, 0, AUX);
+#endif
+}
+
+// Max and sum over lanes l, l^16, l^32, l^48 (the four k-groups of an MFMA
+// operand row), with the gfx950 cross-row lane swaps.
+//
+// The gfx950-only builtins and asm sit behind __HIP_DEVICE_COMPILE__: the
+// host pass instantiates the kernel templates too, and a target builtin it
+// does not know silently drops the kernel's launch stub.
+__device__ __forceinline__ float xgroup_max(float x) {
+#if __HIP_DEVICE_COMPILE__
+  auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = nan_max(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = nan_max(__uint_as_float(b[0]), __uint_as_float(b[1]));
+#endif
+  return x;
+}
+__device__ __forceinline__ float xgroup_sum(float x) {
+#if __HIP_DEVICE_COMPILE__
+  auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = __uint_as_float(b[0]) + __uint_as_float(b[1]);
+#endif
+  return x;
+}
+
 template <typename T>
 struct Mfma;
 template <>
@@ -114,6 +162,10 @@ struct Mfma<bf16_t> {
   static __device__ __forceinline__ f4 run(v8 a, v8 b, f4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
   }
+  typedef __bf16 v4 __attribute__((ext_vector_type(4)));
+  static __device__ __forceinline__ f4 run16(v4 a, v4 b, f4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, c, 0, 0, 0);
+  }
 };
 template <>
 struct Mfma<_Float16> {
@@ -122,6 +174,10 @@ struct Mfma<_Float16> {
   typedef float f4 __attribute__((ext_vector_type(4)));
   static __device__ __forceinline__ f4 run(v8 a, v8 b, f4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+  }
+  typedef _Float16 v4 __attribute__((ext_vector_type(4)));
+  static __device__ __forceinline__ f4 run16(v4 a, v4 b, f4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
   }
 };
 

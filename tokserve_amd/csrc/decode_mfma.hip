@@ -669,6 +669,495 @@ __global__ __launch_bounds__(64 * kWaves) void decode_mfma_kernel(DecodeArgs a) 
   }
 }
 
+// ---------------------------------------------------------------------------
+// P.V on the matrix cores, for pools in the model dtype (bf16 / fp16).
+//
+// Per page the score MFMA runs with its operands swapped: S (16 tokens x 16 head
+// columns) = K . Q^T with v_mfma_f32_16x16x32 (A = the page's K rows, B = Q^T,
+// column n being query head n % G), so lane (grp, r) holds the scores of tokens
+// grp*4 .. +3 for head column r. After exp2 these are exactly the B operand of
+// v_mfma_f32_16x16x16 for
+//   O^T (16 dims x 16 head columns) += V^T (16 dims x 16 tokens) . P^T,
+// one MFMA per 16 dims: P never goes through LDS, and the P.V dot products leave
+// the VALU. K and V pages go HBM -> LDS with global_load_lds (a two-page ring per
+// wave, the 16-byte chunks of each row XOR-swizzled as in the prefill kernel, so
+// that neither operand read has bank conflicts) and come back as MFMA operands:
+// K rows through ds_read_b128, V^T through ds_read_b64_tr_b16 (within each 16-lane
+// group, lane j receives dim j of tokens 4g .. 4g+3 when lane 4e + q addresses dims
+// 4q .. 4q+3 of token 4g + e). Every LDS read, and every wait for the page loads,
+// is explicit inline asm: the compiler cannot tell ring slots apart and would wait
+// for all loads in flight. A head column's softmax state is the same in the four
+// lanes that hold it (the page maximum across the lane groups takes two lane
+// swaps), so rescaling its accumulators stays in the lane.
+constexpr int kPvRing = 2;  // pages per wave: the one consumed and the next in flight
+// Every page is read once: non-temporal loads.
+constexpr int kPvLoadPolicy = kLdsNonTemporal;
+
+template <int DH>
+struct PvSwizzle {
+  static __device__ __forceinline__ int k(int row) {
+    return DH == 128 ? (row & 15) : ((row >> 1) & 7);
+  }
+  static __device__ __forceinline__ int v(int row) {
+    return DH == 128 ? 2 * (row & 7) : (row & 7);
+  }
+};
+
+#define TKS_S(x) #x
+#define TKS_RD128(o, a, off) "ds_read_b128 %" TKS_S(o) ", %" TKS_S(a) " offset:%" TKS_S(off) "\n\t"
+#define TKS_RDTR(o, a, off) "ds_read_b64_tr_b16 %" TKS_S(o) ", %" TKS_S(a) " offset:%" TKS_S(off) "\n\t"
+
+// A page's operands from LDS ring offset OFF (bytes), after waiting until at most
+// VM vector-memory operations of the wave are in flight (the page's loads are then
+// done): keys() the K rows (one 16-byte read per 32 dims), values() the V^T
+// operands (one 8-byte transposed read per 16 dims). The results are valid after
+// wait(). (Compiled for the device only.)
+template <int DH>
+struct PvReads;
+template <>
+struct PvReads<128> {
+  template <int VM, int OFF>
+  static __device__ __forceinline__ void keys(const uint32_t (&ka)[4], u32x4 (&k)[4]) {
+#if __HIP_DEVICE_COMPILE__
+    asm volatile("s_waitcnt vmcnt(%8)\n\t"
+                 TKS_RD128(0, 4, 9) TKS_RD128(1, 5, 9) TKS_RD128(2, 6, 9) TKS_RD128(3, 7, 9)
+                 : "=&v"(k[0]), "=&v"(k[1]), "=&v"(k[2]), "=&v"(k[3])
+                 : "v"(ka[0]), "v"(ka[1]), "v"(ka[2]), "v"(ka[3]), "n"(VM), "i"(OFF)
+                 : "memory");
+#else
+    (void)ka, (void)k;
+#endif
+  }
+  template <int VM, int OFF>
+  static __device__ __forceinline__ void values(const uint32_t (&va)[8], u32x2 (&v)[8]) {
+#if __HIP_DEVICE_COMPILE__
+    asm volatile("s_waitcnt vmcnt(%16)\n\t"
+                 TKS_RDTR(0, 8, 17) TKS_RDTR(1, 9, 17) TKS_RDTR(2, 10, 17) TKS_RDTR(3, 11, 17)
+                 TKS_RDTR(4, 12, 17) TKS_RDTR(5, 13, 17) TKS_RDTR(6, 14, 17) TKS_RDTR(7, 15, 17)
+                 : "=&v"(v[0]), "=&v"(v[1]), "=&v"(v[2]), "=&v"(v[3]), "=&v"(v[4]), "=&v"(v[5]),
+                   "=&v"(v[6]), "=&v"(v[7])
+                 : "v"(va[0]), "v"(va[1]), "v"(va[2]), "v"(va[3]), "v"(va[4]), "v"(va[5]),
+                   "v"(va[6]), "v"(va[7]), "n"(VM), "i"(OFF)
+                 : "memory");
+#else
+    (void)va, (void)v;
+#endif
+  }
+  static __device__ __forceinline__ void wait(u32x4 (&k)[4]) {
+#if __HIP_DEVICE_COMPILE__
+    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(k[0]), "+v"(k[1]), "+v"(k[2]), "+v"(k[3])::"memory");
+#else
+    (void)k;
+#endif
+  }
+  static __device__ __forceinline__ void wait(u32x2 (&v)[8]) {
+#if __HIP_DEVICE_COMPILE__
+    asm volatile("s_waitcnt lgkmcnt(0)"
+                 : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3]), "+v"(v[4]), "+v"(v[5]),
+                   "+v"(v[6]), "+v"(v[7])::"memory");
+#else
+    (void)v;
+#endif
+  }
+};
+template <>
+struct PvReads<64> {
+  template <int VM, int OFF>
+  static __device__ __forceinline__ void keys(const uint32_t (&ka)[2], u32x4 (&k)[2]) {
+#if __HIP_DEVICE_COMPILE__
+    asm volatile("s_waitcnt vmcnt(%4)\n\t" TKS_RD128(0, 2, 5) TKS_RD128(1, 3, 5)
+                 : "=&v"(k[0]), "=&v"(k[1])
+                 : "v"(ka[0]), "v"(ka[1]), "n"(VM), "i"(OFF)
+                 : "memory");
+#else
+    (void)ka, (void)k;
+#endif
+  }
+  template <int VM, int OFF>
+  static __device__ __forceinline__ void values(const uint32_t (&va)[4], u32x2 (&v)[4]) {
+#if __HIP_DEVICE_COMPILE__
+    asm volatile("s_waitcnt vmcnt(%8)\n\t"
+                 TKS_RDTR(0, 4, 9) TKS_RDTR(1, 5, 9) TKS_RDTR(2, 6, 9) TKS_RDTR(3, 7, 9)
+                 : "=&v"(v[0]), "=&v"(v[1]), "=&v"(v[2]), "=&v"(v[3])
+                 : "v"(va[0]), "v"(va[1]), "v"(va[2]), "v"(va[3]), "n"(VM), "i"(OFF)
+                 : "memory");
+#else
+    (void)va, (void)v;
+#endif
+  }
+  static __device__ __forceinline__ void wait(u32x4 (&k)[2]) {
+#if __HIP_DEVICE_COMPILE__
+    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(k[0]), "+v"(k[1])::"memory");
+#else
+    (void)k;
+#endif
+  }
+  static __device__ __forceinline__ void wait(u32x2 (&v)[4]) {
+#if __HIP_DEVICE_COMPILE__
+    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3])::"memory");
+#else
+    (void)v;
+#endif
+  }
+};
+
+#undef TKS_RD128
+#undef TKS_RDTR
+#undef TKS_S
+
+// LDS reads that complete before the statement ends, for the fused append's staged
+// rows (asm, so they stay inside the branch that needs them instead of being
+// hoisted where the compiler would make them wait for the page loads in flight).
+__device__ __forceinline__ uint4 lds_read16_now(const void *p) {
+  u32x4 v = {0u, 0u, 0u, 0u};
+#if __HIP_DEVICE_COMPILE__
+  asm volatile("ds_read_b128 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(v) : "v"(lds_address(p)) : "memory");
+#else
+  (void)p;
+#endif
+  return make_uint4(v[0], v[1], v[2], v[3]);
+}
+__device__ __forceinline__ uint32_t lds_read2_now(const void *p) {
+  uint32_t v = 0u;
+#if __HIP_DEVICE_COMPILE__
+  asm volatile("ds_read_u16 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(v) : "v"(lds_address(p)) : "memory");
+#else
+  (void)p;
+#endif
+  return v;
+}
+
+template <int N>
+struct IntConst {
+  static constexpr int value = N;
+};
+
+template <typename T, int DH, int G, bool ROPE>
+__global__ __launch_bounds__(64 * kWaves) void decode_pv_kernel(DecodeArgs a) {
+  constexpr int BS = 16, NC = DH / 32, DT = DH / 16, CPR = DH / 8;
+  constexpr int kPage = BS * DH;                      // elements of one K (or V) page
+  constexpr int kPageBytes = kPage * (int)sizeof(T);
+  constexpr int kStageBytes = 2 * kPageBytes;         // K page, then V page
+  constexpr int L = kPageBytes / (16 * 64);           // HBM -> LDS loads per page tile
+  constexpr int D = kPvRing;
+  static_assert(D == 2, "the waits count one page in flight behind the consumed one");
+  static_assert(16 % G == 0 && (DH == 64 || DH == 128), "shape");
+  using M = Mfma<T>;
+  using Swz = PvSwizzle<DH>;
+  using Reads = PvReads<DH>;
+  typedef typename M::f4 f4;
+  typedef typename M::v4 v4;
+  // The ring, reused after the page loop for the waves' partial results.
+  constexpr int kRingBytes = kWaves * D * kStageBytes;
+  constexpr int kMergeBytes = kWaves * G * (DH + 2) * (int)sizeof(float);
+  static_assert(kMergeBytes <= kRingBytes, "merge area");
+  __shared__ __attribute__((aligned(16))) char ring[kRingBytes];
+  __shared__ __attribute__((aligned(16))) T new_k_s[ROPE ? DH : 1];
+  __shared__ __attribute__((aligned(16))) T new_v_s[ROPE ? DH : 1];
+  __shared__ __attribute__((aligned(16))) T q_s[G * DH];
+
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const int r = lane & 15;    // K rows: token r; S and O^T: head column r
+  const int grp = lane >> 4;  // K: dims grp*8 of each 32; S: tokens grp*4 .. +3; O^T: dims
+
+  const int kvh = blockIdx.x;
+  const int split = blockIdx.z;
+  const int b = a.seq_order ? min(max(a.seq_order[blockIdx.y], 0), (int)gridDim.y - 1)
+                            : (int)blockIdx.y;
+  // A length above the host bound is clamped so no access can leave its buffer.
+  const int len = min(a.seq_lens[b], a.key_cap);
+  const int n_pages = (len + BS - 1) / BS;
+  const int p_begin = split * a.pages_per_split;
+  T *out = static_cast<T *>(a.out);
+  if (p_begin >= n_pages) {
+    if (split == 0) {  // empty sequence: defined all-zero output
+      for (int i = threadIdx.x; i < G * DH; i += 64 * kWaves)
+        out[b * a.o_ss + (int64_t)(kvh * G + i / DH) * a.o_hs + i % DH] = from_float<T>(0.f);
+      if constexpr (ROPE) {
+        if (n_pages == 0 && threadIdx.x < 64 &&
+            stage_new_rows<T, T, DH, BS>(a, b, kvh, threadIdx.x, new_k_s, new_v_s)) {
+          wave_lds_sync();
+          write_staged_rows<T, T, DH, BS>(a, b, kvh, threadIdx.x, new_k_s, new_v_s);
+        }
+      }
+    }
+    return;
+  }
+  const int p_end = min(n_pages, p_begin + a.pages_per_split);
+  const int per_wave = (p_end - p_begin + kWaves - 1) / kWaves;
+  const int w_begin = p_begin + wave * per_wave;
+  const int w_end = min(p_end, w_begin + per_wave);
+
+  // Q^T operands through LDS as in decode_mfma_kernel (rotated there when the RoPE
+  // is fused in; the wave holding the sequence's last page stages the new rows).
+  typename M::v8 qa[NC];
+  const int32_t *bt_row = a.bt + (int64_t)b * a.bt_stride;
+  bool staged = false;
+  bool patch = false;
+  const int new_off = ROPE ? (len - 1) % BS : 0;
+  {
+    const int t = threadIdx.x;
+    if constexpr (ROPE) {
+      constexpr int HALF = DH / 2;
+      if (w_begin < w_end && w_end == n_pages) {  // wave-uniform
+        staged = stage_new_rows<T, T, DH, BS>(a, b, kvh, lane, new_k_s, new_v_s);
+        patch = staged && a.seq_lens[b] == len;
+        wave_lds_sync();
+      }
+      if (t < G * HALF / 8) {
+        const int64_t pos = min(max(a.positions[b], (int64_t)0), a.table_len - 1);
+        const int h = t / (HALF / 8), j = (t % (HALF / 8)) * 8;
+        const T *qrow =
+            static_cast<const T *>(a.q) + b * a.q_ss + (int64_t)(kvh * G + h) * a.q_hs;
+        float cf[8], sf[8], o1[8], o2[8];
+        load_table<T, 8>(static_cast<const T *>(a.cos_t) + pos * HALF,
+                         static_cast<const T *>(a.sin_t) + pos * HALF, j, cf, sf);
+        rotate_values<T, 8>(qrow + j, cf, sf, HALF, o1, o2);
+        st16(&q_s[h * DH + j], pack<T>(o1));
+        st16(&q_s[h * DH + j + HALF], pack<T>(o2));
+      }
+    } else {
+      if (t < G * DH / 8) {
+        const int h = t / (DH / 8), j = (t % (DH / 8)) * 8;
+        const T *qrow =
+            static_cast<const T *>(a.q) + b * a.q_ss + (int64_t)(kvh * G + h) * a.q_hs;
+        st16(&q_s[h * DH + j], ld16(qrow + j));
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int c = 0; c < NC; ++c) qa[c] = as_v8<T>(ld16(&q_s[(r % G) * DH + c * 32 + grp * 8]));
+  }
+
+  const char *kcb = reinterpret_cast<const char *>(static_cast<const T *>(a.kc) + a.pool.layer_base +
+                                                   (int64_t)kvh * a.pool.head_stride);
+  const char *vcb = reinterpret_cast<const char *>(static_cast<const T *>(a.vc) + a.pool.layer_base +
+                                                   (int64_t)kvh * a.pool.head_stride);
+  const int64_t block_bytes = a.pool.block_stride * (int64_t)sizeof(T);
+  // Load j of a page tile fills 16-byte LDS slot j*64 + lane = row * CPR + physical
+  // chunk, with logical chunk physical ^ swizzle(row) of that row.
+  uint32_t k_src[L], v_src[L];
+#pragma unroll
+  for (int j = 0; j < L; ++j) {
+    const int slot = j * 64 + lane;
+    const int row = slot / CPR;
+    k_src[j] = (row * DH + ((slot % CPR) ^ Swz::k(row)) * 8) * (int)sizeof(T);
+    v_src[j] = (row * DH + ((slot % CPR) ^ Swz::v(row)) * 8) * (int)sizeof(T);
+  }
+  // Operand addresses in ring slot 0 of this wave (slot 1 and the V page are
+  // immediate offsets). K: lane (grp, r) reads token r, dims c*32 + grp*8 .. +8.
+  // V^T: lane (grp, r) addresses token grp*4 + r/4, dims t*16 + 4 (r % 4) .. +3.
+  char *wring = ring + wave * D * kStageBytes;
+  const uint32_t ring0 = lds_address(wring);
+  uint32_t ka[NC], va[DT];
+#pragma unroll
+  for (int c = 0; c < NC; ++c) ka[c] = ring0 + (r * CPR + ((c * 4 + grp) ^ Swz::k(r))) * 16;
+#pragma unroll
+  for (int t = 0; t < DT; ++t) {
+    const int row = grp * 4 + r / 4;
+    const int lc = t * 2 + (r % 4) / 2;
+    va[t] = ring0 + (row * CPR + (lc ^ Swz::v(row))) * 16 + (r & 1) * 8;
+  }
+
+  f4 acc[DT];
+#pragma unroll
+  for (int t = 0; t < DT; ++t) acc[t] = f4{0.f, 0.f, 0.f, 0.f};
+  // Softmax state of head column r (equal in the column's four lanes): m = the
+  // reference max in log2 units (-inf before the first key), thr = m + 8 (a score
+  // above it moves the reference), mref = the value subtracted before exp2 (m, or
+  // 0 while m is -inf), l = this lane's share of the sum (its tokens of each page).
+  float m = -INFINITY, l = 0.f, thr = -INFINITY, mref = 0.f;
+  const float scale_log2 = a.scale_log2;
+
+  // Page idx of the chunk's block-id register into ring slot SLOT: its K tile, then
+  // its V tile (2 L loads, in that order).
+  auto issue = [&](auto slot_c, int blk_reg, int idx) {
+    constexpr int SLOT = decltype(slot_c)::value;
+    const int64_t blk = clamp_block(__builtin_amdgcn_readlane(blk_reg, idx), a.pool.num_blocks);
+    const char *kp = kcb + blk * block_bytes;
+    const char *vp = vcb + blk * block_bytes;
+#pragma unroll
+    for (int j = 0; j < L; ++j)
+      load_lds16<kPvLoadPolicy>(kp + k_src[j], wring + SLOT * kStageBytes + j * 1024);
+#pragma unroll
+    for (int j = 0; j < L; ++j)
+      load_lds16<kPvLoadPolicy>(vp + v_src[j], wring + SLOT * kStageBytes + kPageBytes + j * 1024);
+  };
+  // later: the next page's 2 L loads were issued after this page's.
+  auto consume = [&](auto check_end, auto slot_c, int p, bool later) {
+    constexpr bool kCheckEnd = decltype(check_end)::value;
+    constexpr int SLOT = decltype(slot_c)::value;
+    constexpr int KOFF = SLOT * kStageBytes, VOFF = KOFF + kPageBytes;
+    u32x4 kr[NC];
+    if (later)
+      Reads::template keys<3 * L, KOFF>(ka, kr);
+    else
+      Reads::template keys<L, KOFF>(ka, kr);
+    Reads::wait(kr);
+    if constexpr (ROPE) {
+      // The new token's K row in place of what was loaded of its slot.
+      if (patch && p == n_pages - 1 && r == new_off) {
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+          const uint4 u = lds_read16_now(new_k_s + c * 32 + grp * 8);
+          kr[c] = u32x4{u.x, u.y, u.z, u.w};
+        }
+      }
+    }
+    f4 s4 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int c = 0; c < NC; ++c)
+      s4 = M::run(as_v8<T>(make_uint4(kr[c][0], kr[c][1], kr[c][2], kr[c][3])), qa[c], s4);
+    // This page's V^T operands: requested now, used after the softmax.
+    u32x2 vt[DT];
+    if (later)
+      Reads::template values<2 * L, VOFF>(va, vt);
+    else
+      Reads::template values<0, VOFF>(va, vt);
+    float sv[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) sv[i] = s4[i] * scale_log2;
+    // The sequence's last page (uniform): keys past len score -inf, and their V
+    // values, whatever the pool holds there, become 0 below (0 * NaN is NaN).
+    const bool tail = kCheckEnd && (p + 1) * BS > len;
+    if (tail) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) sv[i] = p * BS + grp * 4 + i < len ? sv[i] : -INFINITY;
+    }
+    bool over = false;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) over = over || sv[i] > thr;
+    // A score more than 8 above its column's reference (every column on the first
+    // page): page maxima, new references, l and the accumulators rescaled.
+    if (__builtin_amdgcn_ballot_w64(over) != 0) {
+      const float mx = xgroup_max(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3])));
+      const bool bump = mx > thr;
+      const float alpha = bump ? fast_exp2(m - mx) : 1.f;
+      m = bump ? mx : m;
+      thr = m + 8.f;
+      mref = m == -INFINITY ? 0.f : m;
+      l *= alpha;
+#pragma unroll
+      for (int t = 0; t < DT; ++t)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[t][i] *= alpha;
+    }
+    float pv[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) pv[i] = fast_exp2(sv[i] - mref);
+    l += (pv[0] + pv[1]) + (pv[2] + pv[3]);
+    v4 pb;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) pb[i] = static_cast<typename M::elem>(pv[i]);
+    Reads::wait(vt);
+    if (tail) {
+      const int base = p * BS + grp * 4;
+      const uint32_t keep_lo = (base < len ? 0x0000FFFFu : 0u) | (base + 1 < len ? 0xFFFF0000u : 0u);
+      const uint32_t keep_hi = (base + 2 < len ? 0x0000FFFFu : 0u) | (base + 3 < len ? 0xFFFF0000u : 0u);
+#pragma unroll
+      for (int t = 0; t < DT; ++t) {
+        vt[t][0] &= keep_lo;
+        vt[t][1] &= keep_hi;
+      }
+    }
+    if constexpr (ROPE) {
+      // The new token's V row: element e of lane (grp, r) is token grp*4 + e.
+      const int e = new_off - grp * 4;
+      if (patch && p == n_pages - 1 && e >= 0 && e < 4) {
+#pragma unroll
+        for (int t = 0; t < DT; ++t) {
+          const uint32_t nv = lds_read2_now(new_v_s + t * 16 + r);
+          const int w = e >> 1, sh = (e & 1) * 16;
+          vt[t][w] = (vt[t][w] & ~(0xFFFFu << sh)) | (nv << sh);
+        }
+      }
+    }
+#pragma unroll
+    for (int t = 0; t < DT; ++t) {
+      v4 vop;
+      __builtin_memcpy(&vop, &vt[t], 8);
+      acc[t] = M::run16(vop, pb, acc[t]);
+    }
+  };
+
+  for (int c0 = w_begin; c0 < w_end; c0 += 64) {
+    const int n = min(w_end, c0 + 64) - c0;
+    const int blk_reg = lane < n ? bt_row[c0 + lane] : 0;
+    // The block ids, and everything else, before any page load is in flight: the
+    // waits below count only page loads.
+    __builtin_amdgcn_s_waitcnt(0);
+    issue(IntConst<0>{}, blk_reg, 0);
+    int i = 0;  // page i sits in ring slot i % 2
+    for (; i + 3 <= n; i += 2) {
+      issue(IntConst<1>{}, blk_reg, i + 1);
+      consume(BoolConst<false>{}, IntConst<0>{}, c0 + i, true);
+      issue(IntConst<0>{}, blk_reg, i + 2);
+      consume(BoolConst<false>{}, IntConst<1>{}, c0 + i + 1, true);
+    }
+    // One or two pages left; page i is in flight.
+    const bool two = i + 1 < n;
+    if (two) issue(IntConst<1>{}, blk_reg, i + 1);
+    consume(BoolConst<true>{}, IntConst<0>{}, c0 + i, two);
+    if (two) consume(BoolConst<true>{}, IntConst<1>{}, c0 + i + 1, false);
+  }
+
+  // The staged rows to the pool, once this wave has read the page that holds their slot.
+  if constexpr (ROPE) {
+    if (staged) write_staged_rows<T, T, DH, BS>(a, b, kvh, lane, new_k_s, new_v_s);
+  }
+
+  // Per-wave state, in the ring's memory once every wave is done with it: l summed
+  // over the four lane groups; lanes of columns r < G hold head r's dims
+  // t*16 + grp*4 .. +3.
+  l = xgroup_sum(l);
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  float *m_s = reinterpret_cast<float *>(ring);        // [kWaves][G]
+  float *l_s = m_s + kWaves * G;                        // [kWaves][G]
+  float *acc_s = l_s + kWaves * G;                      // [kWaves][G][DH]
+  if (r < G) {
+    if (grp == 0) {
+      m_s[wave * G + r] = m;
+      l_s[wave * G + r] = l;
+    }
+#pragma unroll
+    for (int t = 0; t < DT; ++t)
+      *reinterpret_cast<float4 *>(&acc_s[(wave * G + r) * DH + t * 16 + grp * 4]) =
+          make_float4(acc[t][0], acc[t][1], acc[t][2], acc[t][3]);
+  }
+  __syncthreads();
+
+  // Merge the waves (a wave without pages has m = -inf, l = 0, acc = 0).
+  const bool single = a.max_splits == 1;
+  for (int i = threadIdx.x; i < G * DH; i += 64 * kWaves) {
+    const int h = i / DH, d = i % DH;
+    float M_ = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) M_ = fmaxf(M_, m_s[w * G + h]);
+    float L_ = 0.f, o = 0.f;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) {
+      const float e = m_s[w * G + h] == -INFINITY ? 0.f : fast_exp2(m_s[w * G + h] - M_);
+      L_ += e * l_s[w * G + h];
+      o += e * acc_s[(w * G + h) * DH + d];
+    }
+    if (single) {
+      out[b * a.o_ss + (int64_t)(kvh * G + h) * a.o_hs + d] = from_float<T>(o / L_);
+    } else {
+      const int64_t w = ((int64_t)b * a.num_q_heads + kvh * G + h) * a.max_splits + split;
+      if (d == 0) {
+        a.ws_m[w] = M_;
+        a.ws_l[w] = L_;
+      }
+      a.ws_acc[w * DH + d] = o;
+    }
+  }
+}
+
+// Pools in the model dtype take the P.V-on-MFMA kernel.
+constexpr bool kPvMfma = true;
+
 template <typename T, typename KV, bool ROPE = false>
 int32_t launch_typed(const DecodeArgs &a, int32_t num_seqs, int32_t num_kv_heads, int32_t G,
                      int32_t head_dim, hipStream_t s) {
@@ -682,6 +1171,10 @@ int32_t launch_typed(const DecodeArgs &a, int32_t num_seqs, int32_t num_kv_heads
         decode_mfma_kernel<T, KV, DH, GG, false, true><<<grid, 64 * kWaves, 0, s>>>(a); \
         return check_launch();                                                      \
       }                                                                             \
+    }                                                                               \
+    if constexpr (sizeof(KV) != 1 && kPvMfma) {                                     \
+      decode_pv_kernel<T, DH, GG, ROPE><<<grid, 64 * kWaves, 0, s>>>(a);            \
+      return check_launch();                                                        \
     }                                                                               \
     decode_mfma_kernel<T, KV, DH, GG, ROPE><<<grid, 64 * kWaves, 0, s>>>(a);        \
     return check_launch();                                                          \

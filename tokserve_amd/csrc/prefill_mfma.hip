@@ -49,23 +49,6 @@ constexpr bool kPairSteps = DH == 128;
 template <int DH>
 constexpr int kStagesOf = kPairSteps<DH> ? 4 : 3;
 
-typedef __attribute__((address_space(3))) void lds_void;
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-
-template <typename P>
-__device__ __forceinline__ uint32_t lds_address(P *p) {
-  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_void *)(p)));
-}
-
-// One 16-byte HBM -> LDS load per lane: lane i's bytes land at lds + 16 * i
-// (lds is wave-uniform).
-__device__ __forceinline__ void load_lds16(const void *src, void *lds) {
-#if __HIP_DEVICE_COMPILE__
-  __builtin_amdgcn_global_load_lds(src, (lds_void *)lds, 16, 0, 0);
-#endif
-}
-
 // Makes a wave-uniform value an SGPR that is ready here: every scalar load
 // behind it completes before this point, so no wait for such a load can land
 // inside the main loop (a scalar-load wait also waits for all pending LDS
@@ -92,31 +75,6 @@ template <int N>
 __device__ __forceinline__ void wait_loads_and_barrier() {
   static_assert(N >= 0 && N < 64, "vmcnt");
   asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(N) : "memory");
-}
-
-// Max and sum over lanes l, l^16, l^32, l^48 (the four k-groups of an MFMA
-// operand row), with the gfx950 cross-row lane swaps.
-//
-// The gfx950-only builtins and asm sit behind __HIP_DEVICE_COMPILE__: the
-// host pass instantiates the kernel templates too, and a target builtin it
-// does not know silently drops the kernel's launch stub.
-__device__ __forceinline__ float xgroup_max(float x) {
-#if __HIP_DEVICE_COMPILE__
-  auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  x = nan_max(__uint_as_float(a[0]), __uint_as_float(a[1]));
-  auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  x = nan_max(__uint_as_float(b[0]), __uint_as_float(b[1]));
-#endif
-  return x;
-}
-__device__ __forceinline__ float xgroup_sum(float x) {
-#if __HIP_DEVICE_COMPILE__
-  auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  x = __uint_as_float(a[0]) + __uint_as_float(a[1]);
-  auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  x = __uint_as_float(b[0]) + __uint_as_float(b[1]);
-#endif
-  return x;
 }
 
 #define TKS_S(x) #x
