@@ -689,7 +689,9 @@ __global__ __launch_bounds__(64 * kWaves) void decode_mfma_kernel(DecodeArgs a) 
 // for all loads in flight. A head column's softmax state is the same in the four
 // lanes that hold it (the page maximum across the lane groups takes two lane
 // swaps), so rescaling its accumulators stays in the lane.
-constexpr int kPvRing = 2;  // pages per wave: the one consumed and the next in flight
+// Pages per wave in the ring: the one consumed and those in flight behind it.
+template <int DH>
+constexpr int kPvRing = DH == 64 ? 3 : 2;
 // Every page is read once: non-temporal loads.
 constexpr int kPvLoadPolicy = kLdsNonTemporal;
 
@@ -839,8 +841,8 @@ __global__ __launch_bounds__(64 * kWaves) void decode_pv_kernel(DecodeArgs a) {
   constexpr int kPageBytes = kPage * (int)sizeof(T);
   constexpr int kStageBytes = 2 * kPageBytes;         // K page, then V page
   constexpr int L = kPageBytes / (16 * 64);           // HBM -> LDS loads per page tile
-  constexpr int D = kPvRing;
-  static_assert(D == 2, "the waits count one page in flight behind the consumed one");
+  constexpr int D = kPvRing<DH>;
+  static_assert(D == 2 || D == 3, "ring depth");
   static_assert(16 % G == 0 && (DH == 64 || DH == 128), "shape");
   using M = Mfma<T>;
   using Swz = PvSwizzle<DH>;
@@ -984,13 +986,15 @@ __global__ __launch_bounds__(64 * kWaves) void decode_pv_kernel(DecodeArgs a) {
     for (int j = 0; j < L; ++j)
       load_lds16<kPvLoadPolicy>(vp + v_src[j], wring + SLOT * kStageBytes + kPageBytes + j * 1024);
   };
-  // later: the next page's 2 L loads were issued after this page's.
-  auto consume = [&](auto check_end, auto slot_c, int p, bool later) {
+  // after: pages whose loads (2 L each) were issued after this page's (0 .. D-1).
+  auto consume = [&](auto check_end, auto slot_c, int p, int after) {
     constexpr bool kCheckEnd = decltype(check_end)::value;
     constexpr int SLOT = decltype(slot_c)::value;
     constexpr int KOFF = SLOT * kStageBytes, VOFF = KOFF + kPageBytes;
     u32x4 kr[NC];
-    if (later)
+    if (D > 2 && after >= 2)
+      Reads::template keys<5 * L, KOFF>(ka, kr);
+    else if (after >= 1)
       Reads::template keys<3 * L, KOFF>(ka, kr);
     else
       Reads::template keys<L, KOFF>(ka, kr);
@@ -1011,7 +1015,9 @@ __global__ __launch_bounds__(64 * kWaves) void decode_pv_kernel(DecodeArgs a) {
       s4 = M::run(as_v8<T>(make_uint4(kr[c][0], kr[c][1], kr[c][2], kr[c][3])), qa[c], s4);
     // This page's V^T operands: requested now, used after the softmax.
     u32x2 vt[DT];
-    if (later)
+    if (D > 2 && after >= 2)
+      Reads::template values<4 * L, VOFF>(va, vt);
+    else if (after >= 1)
       Reads::template values<2 * L, VOFF>(va, vt);
     else
       Reads::template values<0, VOFF>(va, vt);
@@ -1088,18 +1094,33 @@ __global__ __launch_bounds__(64 * kWaves) void decode_pv_kernel(DecodeArgs a) {
     // waits below count only page loads.
     __builtin_amdgcn_s_waitcnt(0);
     issue(IntConst<0>{}, blk_reg, 0);
-    int i = 0;  // page i sits in ring slot i % 2
-    for (; i + 3 <= n; i += 2) {
-      issue(IntConst<1>{}, blk_reg, i + 1);
-      consume(BoolConst<false>{}, IntConst<0>{}, c0 + i, true);
-      issue(IntConst<0>{}, blk_reg, i + 2);
-      consume(BoolConst<false>{}, IntConst<1>{}, c0 + i + 1, true);
+    if (D > 2 && n > 1) issue(IntConst<1 % D>{}, blk_reg, 1);
+    int i = 0;  // page i sits in ring slot i % D
+    // Steady state: D pages per iteration, each consumed with the next D - 1 in flight.
+    for (; i + 2 * D - 1 <= n; i += D) {
+      issue(IntConst<(D - 1) % D>{}, blk_reg, i + D - 1);
+      consume(BoolConst<false>{}, IntConst<0>{}, c0 + i, D - 1);
+      issue(IntConst<D % D>{}, blk_reg, i + D);
+      consume(BoolConst<false>{}, IntConst<1 % D>{}, c0 + i + 1, D - 1);
+      if constexpr (D > 2) {
+        issue(IntConst<(D + 1) % D>{}, blk_reg, i + D + 1);
+        consume(BoolConst<false>{}, IntConst<2 % D>{}, c0 + i + 2, D - 1);
+      }
     }
-    // One or two pages left; page i is in flight.
-    const bool two = i + 1 < n;
-    if (two) issue(IntConst<1>{}, blk_reg, i + 1);
-    consume(BoolConst<true>{}, IntConst<0>{}, c0 + i, two);
-    if (two) consume(BoolConst<true>{}, IntConst<1>{}, c0 + i + 1, false);
+    // Fewer than 2 D - 1 pages left; those before i + D - 1 are in flight.
+    auto drain = [&](auto j_c) {
+      constexpr int j = decltype(j_c)::value;
+      if (i + j < n) {
+        if (i + j + D - 1 < n) issue(IntConst<(j + D - 1) % D>{}, blk_reg, i + j + D - 1);
+        consume(BoolConst<true>{}, IntConst<j % D>{}, c0 + i + j, min(D - 1, n - 1 - (i + j)));
+      }
+    };
+    drain(IntConst<0>{});
+    drain(IntConst<1>{});
+    if constexpr (D > 2) {
+      drain(IntConst<2>{});
+      drain(IntConst<3>{});
+    }
   }
 
   // The staged rows to the pool, once this wave has read the page that holds their slot.
