@@ -690,8 +690,34 @@ __global__ __launch_bounds__(64 * kWaves) void decode_mfma_kernel(DecodeArgs a) 
 // lanes that hold it (the page maximum across the lane groups takes two lane
 // swaps), so rescaling its accumulators stays in the lane.
 // Pages per wave in the ring: the one consumed and those in flight behind it.
+template <int DH, typename KV>
+constexpr int D_of() {
+  return DH == 64 ? 3 : 2;
+}
+
+// e4m3 K rows in LDS: 8-byte reads of 16 rows at one column would share banks, so
+// the 16-byte chunks of row r are XOR-swizzled by r / 2 (Dh 128: 128-byte rows) or
+// r / 4 (Dh 64: 64-byte rows). e4m3 V pages stay in load order: they are read back
+// 16 bytes per lane, contiguously, to be decoded.
 template <int DH>
-constexpr int kPvRing = DH == 64 ? 3 : 2;
+__device__ __forceinline__ int pv_k8_swizzle(int row) {
+  return DH == 128 ? ((row >> 1) & 7) : ((row >> 2) & 3);
+}
+
+// 16 e4m3 codes (four words) decoded exactly to T, as two 16-byte chunks of T.
+template <typename T>
+__device__ __forceinline__ void decode_fp8_chunk(u32x4 w, u32x4 &lo, u32x4 &hi) {
+  uint32_t o[8];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const auto p0 = Dot2<T>::template from_fp8<false>(w[k]);
+    const auto p1 = Dot2<T>::template from_fp8<true>(w[k]);
+    __builtin_memcpy(&o[2 * k], &p0, 4);
+    __builtin_memcpy(&o[2 * k + 1], &p1, 4);
+  }
+  lo = u32x4{o[0], o[1], o[2], o[3]};
+  hi = u32x4{o[4], o[5], o[6], o[7]};
+}
 // Every page is read once: non-temporal loads.
 constexpr int kPvLoadPolicy = kLdsNonTemporal;
 
@@ -803,6 +829,105 @@ struct PvReads<64> {
   }
 };
 
+// fp8 pools. keys(): the K rows as e4m3 codes (one 8-byte read per 32 dims).
+// raw_values(): the page's V codes, 16 bytes per lane per 1 KiB of page, in the
+// order the HBM -> LDS loads wrote them (results valid on return). staged_values():
+// the codes decoded to T go to the wave's staging page (two 16-byte writes per 16
+// codes, in the swizzled layout of pools in the model dtype), and the V^T operands are
+// read back from it (valid after PvReads::wait); LDS operations of one wave complete
+// in order, so the reads see the writes.
+#define TKS_RD64(o, a, off) "ds_read_b64 %" TKS_S(o) ", %" TKS_S(a) " offset:%" TKS_S(off) "\n\t"
+#define TKS_WR128(a, d) "ds_write_b128 %" TKS_S(a) ", %" TKS_S(d) "\n\t"
+#define TKS_RDTR0(o, a) "ds_read_b64_tr_b16 %" TKS_S(o) ", %" TKS_S(a) "\n\t"
+template <int DH>
+struct PvReads8;
+template <>
+struct PvReads8<128> {
+  template <int VM, int OFF>
+  static __device__ __forceinline__ void keys(const uint32_t (&ka)[4], u32x2 (&k)[4]) {
+#if __HIP_DEVICE_COMPILE__
+    asm volatile("s_waitcnt vmcnt(%8)\n\t"
+                 TKS_RD64(0, 4, 9) TKS_RD64(1, 5, 9) TKS_RD64(2, 6, 9) TKS_RD64(3, 7, 9)
+                 "s_waitcnt lgkmcnt(0)"
+                 : "=&v"(k[0]), "=&v"(k[1]), "=&v"(k[2]), "=&v"(k[3])
+                 : "v"(ka[0]), "v"(ka[1]), "v"(ka[2]), "v"(ka[3]), "n"(VM), "i"(OFF)
+                 : "memory");
+#else
+    (void)ka, (void)k;
+#endif
+  }
+  template <int VM, int OFF>
+  static __device__ __forceinline__ void raw_values(const uint32_t (&ra)[2], u32x4 (&v)[2]) {
+#if __HIP_DEVICE_COMPILE__
+    asm volatile("s_waitcnt vmcnt(%4)\n\t" TKS_RD128(0, 2, 5) TKS_RD128(1, 3, 5)
+                 "s_waitcnt lgkmcnt(0)"
+                 : "=&v"(v[0]), "=&v"(v[1])
+                 : "v"(ra[0]), "v"(ra[1]), "n"(VM), "i"(OFF)
+                 : "memory");
+#else
+    (void)ra, (void)v;
+#endif
+  }
+  static __device__ __forceinline__ void staged_values(const uint32_t (&wa)[4], const u32x4 (&d)[4],
+                                                       const uint32_t (&va)[8], u32x2 (&v)[8]) {
+#if __HIP_DEVICE_COMPILE__
+    asm volatile(TKS_WR128(8, 12) TKS_WR128(9, 13) TKS_WR128(10, 14) TKS_WR128(11, 15)
+                 TKS_RDTR0(0, 16) TKS_RDTR0(1, 17) TKS_RDTR0(2, 18) TKS_RDTR0(3, 19)
+                 TKS_RDTR0(4, 20) TKS_RDTR0(5, 21) TKS_RDTR0(6, 22) TKS_RDTR0(7, 23)
+                 : "=&v"(v[0]), "=&v"(v[1]), "=&v"(v[2]), "=&v"(v[3]), "=&v"(v[4]), "=&v"(v[5]),
+                   "=&v"(v[6]), "=&v"(v[7])
+                 : "v"(wa[0]), "v"(wa[1]), "v"(wa[2]), "v"(wa[3]), "v"(d[0]), "v"(d[1]),
+                   "v"(d[2]), "v"(d[3]), "v"(va[0]), "v"(va[1]), "v"(va[2]), "v"(va[3]),
+                   "v"(va[4]), "v"(va[5]), "v"(va[6]), "v"(va[7])
+                 : "memory");
+#else
+    (void)wa, (void)d, (void)va, (void)v;
+#endif
+  }
+};
+template <>
+struct PvReads8<64> {
+  template <int VM, int OFF>
+  static __device__ __forceinline__ void keys(const uint32_t (&ka)[2], u32x2 (&k)[2]) {
+#if __HIP_DEVICE_COMPILE__
+    asm volatile("s_waitcnt vmcnt(%4)\n\t" TKS_RD64(0, 2, 5) TKS_RD64(1, 3, 5)
+                 "s_waitcnt lgkmcnt(0)"
+                 : "=&v"(k[0]), "=&v"(k[1])
+                 : "v"(ka[0]), "v"(ka[1]), "n"(VM), "i"(OFF)
+                 : "memory");
+#else
+    (void)ka, (void)k;
+#endif
+  }
+  template <int VM, int OFF>
+  static __device__ __forceinline__ void raw_values(const uint32_t (&ra)[1], u32x4 (&v)[1]) {
+#if __HIP_DEVICE_COMPILE__
+    asm volatile("s_waitcnt vmcnt(%2)\n\t" TKS_RD128(0, 1, 3) "s_waitcnt lgkmcnt(0)"
+                 : "=&v"(v[0])
+                 : "v"(ra[0]), "n"(VM), "i"(OFF)
+                 : "memory");
+#else
+    (void)ra, (void)v;
+#endif
+  }
+  static __device__ __forceinline__ void staged_values(const uint32_t (&wa)[2], const u32x4 (&d)[2],
+                                                       const uint32_t (&va)[4], u32x2 (&v)[4]) {
+#if __HIP_DEVICE_COMPILE__
+    asm volatile(TKS_WR128(4, 6) TKS_WR128(5, 7)
+                 TKS_RDTR0(0, 8) TKS_RDTR0(1, 9) TKS_RDTR0(2, 10) TKS_RDTR0(3, 11)
+                 : "=&v"(v[0]), "=&v"(v[1]), "=&v"(v[2]), "=&v"(v[3])
+                 : "v"(wa[0]), "v"(wa[1]), "v"(d[0]), "v"(d[1]), "v"(va[0]), "v"(va[1]),
+                   "v"(va[2]), "v"(va[3])
+                 : "memory");
+#else
+    (void)wa, (void)d, (void)va, (void)v;
+#endif
+  }
+};
+#undef TKS_RD64
+#undef TKS_WR128
+#undef TKS_RDTR0
+
 #undef TKS_RD128
 #undef TKS_RDTR
 #undef TKS_S
@@ -829,33 +954,61 @@ __device__ __forceinline__ uint32_t lds_read2_now(const void *p) {
   return v;
 }
 
+__device__ __forceinline__ uint32_t lds_read1_now(const void *p) {
+  uint32_t v = 0u;
+#if __HIP_DEVICE_COMPILE__
+  asm volatile("ds_read_u8 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(v) : "v"(lds_address(p)) : "memory");
+#else
+  (void)p;
+#endif
+  return v;
+}
+__device__ __forceinline__ uint2 lds_read8_now(const void *p) {
+  u32x2 v = {0u, 0u};
+#if __HIP_DEVICE_COMPILE__
+  asm volatile("ds_read_b64 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(v) : "v"(lds_address(p)) : "memory");
+#else
+  (void)p;
+#endif
+  return make_uint2(v[0], v[1]);
+}
+
 template <int N>
 struct IntConst {
   static constexpr int value = N;
 };
 
-template <typename T, int DH, int G, bool ROPE>
+template <typename T, typename KV, int DH, int G, bool ROPE>
 __global__ __launch_bounds__(64 * kWaves) void decode_pv_kernel(DecodeArgs a) {
+  constexpr bool kFp8 = sizeof(KV) == 1;
   constexpr int BS = 16, NC = DH / 32, DT = DH / 16, CPR = DH / 8;
-  constexpr int kPage = BS * DH;                      // elements of one K (or V) page
-  constexpr int kPageBytes = kPage * (int)sizeof(T);
-  constexpr int kStageBytes = 2 * kPageBytes;         // K page, then V page
-  constexpr int L = kPageBytes / (16 * 64);           // HBM -> LDS loads per page tile
-  constexpr int D = kPvRing<DH>;
+  constexpr int kPage = BS * DH;                        // elements of one K (or V) page
+  constexpr int kRowBytes = DH * (int)sizeof(KV);       // one pool row as stored
+  constexpr int CPRR = kRowBytes / 16;                  // its 16-byte chunks
+  constexpr int kPageBytes = BS * kRowBytes;
+  constexpr int kStageBytes = 2 * kPageBytes;           // K page, then V page
+  constexpr int L = kPageBytes / (16 * 64);             // HBM -> LDS loads per page tile
+  // fp8 pools: each wave decodes its current V page into a staging page of T, laid
+  // out as a page of a pool in the model dtype (the V^T reads are the same).
+  constexpr int kStagingBytes = kFp8 ? kPage * (int)sizeof(T) : 0;
+  constexpr int kWaveBytes = D_of<DH, KV>() * kStageBytes + kStagingBytes;
+  constexpr int D = D_of<DH, KV>();
   static_assert(D == 2 || D == 3, "ring depth");
-  static_assert(16 % G == 0 && (DH == 64 || DH == 128), "shape");
+  static_assert(16 % G == 0 && (DH == 64 || DH == 128) && L >= 1, "shape");
   using M = Mfma<T>;
+  using IO = PageIO<T, KV>;
   using Swz = PvSwizzle<DH>;
   using Reads = PvReads<DH>;
+  using Reads8 = PvReads8<DH>;
   typedef typename M::f4 f4;
   typedef typename M::v4 v4;
   // The ring, reused after the page loop for the waves' partial results.
-  constexpr int kRingBytes = kWaves * D * kStageBytes;
+  constexpr int kRingBytes = kWaves * kWaveBytes;
   constexpr int kMergeBytes = kWaves * G * (DH + 2) * (int)sizeof(float);
   static_assert(kMergeBytes <= kRingBytes, "merge area");
   __shared__ __attribute__((aligned(16))) char ring[kRingBytes];
-  __shared__ __attribute__((aligned(16))) T new_k_s[ROPE ? DH : 1];
-  __shared__ __attribute__((aligned(16))) T new_v_s[ROPE ? DH : 1];
+  __shared__ __attribute__((aligned(16))) KV new_k_s[ROPE ? DH : 1];
+  __shared__ __attribute__((aligned(16))) KV new_v_s[ROPE ? DH : 1];
   __shared__ __attribute__((aligned(16))) T q_s[G * DH];
 
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -878,9 +1031,9 @@ __global__ __launch_bounds__(64 * kWaves) void decode_pv_kernel(DecodeArgs a) {
         out[b * a.o_ss + (int64_t)(kvh * G + i / DH) * a.o_hs + i % DH] = from_float<T>(0.f);
       if constexpr (ROPE) {
         if (n_pages == 0 && threadIdx.x < 64 &&
-            stage_new_rows<T, T, DH, BS>(a, b, kvh, threadIdx.x, new_k_s, new_v_s)) {
+            stage_new_rows<T, KV, DH, BS>(a, b, kvh, threadIdx.x, new_k_s, new_v_s)) {
           wave_lds_sync();
-          write_staged_rows<T, T, DH, BS>(a, b, kvh, threadIdx.x, new_k_s, new_v_s);
+          write_staged_rows<T, KV, DH, BS>(a, b, kvh, threadIdx.x, new_k_s, new_v_s);
         }
       }
     }
@@ -903,7 +1056,7 @@ __global__ __launch_bounds__(64 * kWaves) void decode_pv_kernel(DecodeArgs a) {
     if constexpr (ROPE) {
       constexpr int HALF = DH / 2;
       if (w_begin < w_end && w_end == n_pages) {  // wave-uniform
-        staged = stage_new_rows<T, T, DH, BS>(a, b, kvh, lane, new_k_s, new_v_s);
+        staged = stage_new_rows<T, KV, DH, BS>(a, b, kvh, lane, new_k_s, new_v_s);
         patch = staged && a.seq_lens[b] == len;
         wave_lds_sync();
       }
@@ -932,34 +1085,53 @@ __global__ __launch_bounds__(64 * kWaves) void decode_pv_kernel(DecodeArgs a) {
     for (int c = 0; c < NC; ++c) qa[c] = as_v8<T>(ld16(&q_s[(r % G) * DH + c * 32 + grp * 8]));
   }
 
-  const char *kcb = reinterpret_cast<const char *>(static_cast<const T *>(a.kc) + a.pool.layer_base +
+  const char *kcb = reinterpret_cast<const char *>(static_cast<const KV *>(a.kc) + a.pool.layer_base +
                                                    (int64_t)kvh * a.pool.head_stride);
-  const char *vcb = reinterpret_cast<const char *>(static_cast<const T *>(a.vc) + a.pool.layer_base +
+  const char *vcb = reinterpret_cast<const char *>(static_cast<const KV *>(a.vc) + a.pool.layer_base +
                                                    (int64_t)kvh * a.pool.head_stride);
-  const int64_t block_bytes = a.pool.block_stride * (int64_t)sizeof(T);
-  // Load j of a page tile fills 16-byte LDS slot j*64 + lane = row * CPR + physical
+  const int64_t block_bytes = a.pool.block_stride * (int64_t)sizeof(KV);
+  auto k_swizzle = [](int row) { return kFp8 ? pv_k8_swizzle<DH>(row) : Swz::k(row); };
+  // Load j of a page tile fills 16-byte LDS slot j*64 + lane = row * CPRR + physical
   // chunk, with logical chunk physical ^ swizzle(row) of that row.
   uint32_t k_src[L], v_src[L];
 #pragma unroll
   for (int j = 0; j < L; ++j) {
     const int slot = j * 64 + lane;
-    const int row = slot / CPR;
-    k_src[j] = (row * DH + ((slot % CPR) ^ Swz::k(row)) * 8) * (int)sizeof(T);
-    v_src[j] = (row * DH + ((slot % CPR) ^ Swz::v(row)) * 8) * (int)sizeof(T);
+    const int row = slot / CPRR;
+    k_src[j] = row * kRowBytes + ((slot % CPRR) ^ k_swizzle(row)) * 16;
+    v_src[j] = row * kRowBytes + ((slot % CPRR) ^ (kFp8 ? 0 : Swz::v(row))) * 16;
   }
-  // Operand addresses in ring slot 0 of this wave (slot 1 and the V page are
+  // Operand addresses in ring slot 0 of this wave (the other slots and the V page are
   // immediate offsets). K: lane (grp, r) reads token r, dims c*32 + grp*8 .. +8.
-  // V^T: lane (grp, r) addresses token grp*4 + r/4, dims t*16 + 4 (r % 4) .. +3.
-  char *wring = ring + wave * D * kStageBytes;
+  // V^T: lane (grp, r) addresses token grp*4 + r/4, dims t*16 + 4 (r % 4) .. +3, in the
+  // V page (pools in the model dtype) or in the staging page (fp8 pools).
+  char *wring = ring + wave * kWaveBytes;
   const uint32_t ring0 = lds_address(wring);
+  const uint32_t stage0 = ring0 + D * kStageBytes;
   uint32_t ka[NC], va[DT];
 #pragma unroll
-  for (int c = 0; c < NC; ++c) ka[c] = ring0 + (r * CPR + ((c * 4 + grp) ^ Swz::k(r))) * 16;
+  for (int c = 0; c < NC; ++c) {
+    if constexpr (kFp8)
+      ka[c] = ring0 + r * kRowBytes + (((2 * c + grp / 2) ^ k_swizzle(r)) * 16) + (grp & 1) * 8;
+    else
+      ka[c] = ring0 + (r * CPR + ((c * 4 + grp) ^ Swz::k(r))) * 16;
+  }
 #pragma unroll
   for (int t = 0; t < DT; ++t) {
     const int row = grp * 4 + r / 4;
     const int lc = t * 2 + (r % 4) / 2;
-    va[t] = ring0 + (row * CPR + (lc ^ Swz::v(row))) * 16 + (r & 1) * 8;
+    va[t] = (kFp8 ? stage0 : ring0) + (row * CPR + (lc ^ Swz::v(row))) * 16 + (r & 1) * 8;
+  }
+  // fp8 pools: lane's 16-byte chunks j*64 + lane of the V page (16 codes of one row)
+  // and where their decoded values go in the staging page.
+  uint32_t vra[L], vwa[2 * L];
+#pragma unroll
+  for (int j = 0; j < L; ++j) {
+    const int slot = j * 64 + lane;
+    const int row = slot / CPRR, k = slot % CPRR;
+    vra[j] = ring0 + slot * 16;
+    vwa[2 * j] = stage0 + (row * CPR + ((2 * k) ^ Swz::v(row))) * 16;
+    vwa[2 * j + 1] = stage0 + (row * CPR + ((2 * k + 1) ^ Swz::v(row))) * 16;
   }
 
   f4 acc[DT];
@@ -991,36 +1163,73 @@ __global__ __launch_bounds__(64 * kWaves) void decode_pv_kernel(DecodeArgs a) {
     constexpr bool kCheckEnd = decltype(check_end)::value;
     constexpr int SLOT = decltype(slot_c)::value;
     constexpr int KOFF = SLOT * kStageBytes, VOFF = KOFF + kPageBytes;
-    u32x4 kr[NC];
-    if (D > 2 && after >= 2)
-      Reads::template keys<5 * L, KOFF>(ka, kr);
-    else if (after >= 1)
-      Reads::template keys<3 * L, KOFF>(ka, kr);
-    else
-      Reads::template keys<L, KOFF>(ka, kr);
-    Reads::wait(kr);
-    if constexpr (ROPE) {
-      // The new token's K row in place of what was loaded of its slot.
-      if (patch && p == n_pages - 1 && r == new_off) {
+    f4 s4 = {0.f, 0.f, 0.f, 0.f};
+    if constexpr (kFp8) {
+      u32x2 kr[NC];
+      if (D > 2 && after >= 2)
+        Reads8::template keys<5 * L, KOFF>(ka, kr);
+      else if (after >= 1)
+        Reads8::template keys<3 * L, KOFF>(ka, kr);
+      else
+        Reads8::template keys<L, KOFF>(ka, kr);
+      if constexpr (ROPE) {
+        // The new token's K codes in place of what was loaded of its slot.
+        if (patch && p == n_pages - 1 && r == new_off) {
 #pragma unroll
-        for (int c = 0; c < NC; ++c) {
-          const uint4 u = lds_read16_now(new_k_s + c * 32 + grp * 8);
-          kr[c] = u32x4{u.x, u.y, u.z, u.w};
+          for (int c = 0; c < NC; ++c) {
+            const uint2 u = lds_read8_now(new_k_s + c * 32 + grp * 8);
+            kr[c] = u32x2{u.x, u.y};
+          }
         }
       }
-    }
-    f4 s4 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int c = 0; c < NC; ++c)
-      s4 = M::run(as_v8<T>(make_uint4(kr[c][0], kr[c][1], kr[c][2], kr[c][3])), qa[c], s4);
-    // This page's V^T operands: requested now, used after the softmax.
+      for (int c = 0; c < NC; ++c)
+        s4 = M::run(IO::k_operand(make_uint2(kr[c][0], kr[c][1])), qa[c], s4);
+    } else {
+      u32x4 kr[NC];
+      if (D > 2 && after >= 2)
+        Reads::template keys<5 * L, KOFF>(ka, kr);
+      else if (after >= 1)
+        Reads::template keys<3 * L, KOFF>(ka, kr);
+      else
+        Reads::template keys<L, KOFF>(ka, kr);
+      Reads::wait(kr);
+      if constexpr (ROPE) {
+        // The new token's K row in place of what was loaded of its slot.
+        if (patch && p == n_pages - 1 && r == new_off) {
+#pragma unroll
+          for (int c = 0; c < NC; ++c) {
+            const uint4 u = lds_read16_now(new_k_s + c * 32 + grp * 8);
+            kr[c] = u32x4{u.x, u.y, u.z, u.w};
+          }
+        }
+      }
+#pragma unroll
+      for (int c = 0; c < NC; ++c)
+        s4 = M::run(as_v8<T>(make_uint4(kr[c][0], kr[c][1], kr[c][2], kr[c][3])), qa[c], s4);
+    }
+    // This page's V^T operands: requested now, used after the softmax. fp8 pools: the
+    // page's codes are decoded into the staging page first.
     u32x2 vt[DT];
-    if (D > 2 && after >= 2)
-      Reads::template values<4 * L, VOFF>(va, vt);
-    else if (after >= 1)
-      Reads::template values<2 * L, VOFF>(va, vt);
-    else
-      Reads::template values<0, VOFF>(va, vt);
+    if constexpr (kFp8) {
+      u32x4 raw[L], dec[2 * L];
+      if (D > 2 && after >= 2)
+        Reads8::template raw_values<4 * L, VOFF>(vra, raw);
+      else if (after >= 1)
+        Reads8::template raw_values<2 * L, VOFF>(vra, raw);
+      else
+        Reads8::template raw_values<0, VOFF>(vra, raw);
+#pragma unroll
+      for (int j = 0; j < L; ++j) decode_fp8_chunk<T>(raw[j], dec[2 * j], dec[2 * j + 1]);
+      Reads8::staged_values(vwa, dec, va, vt);
+    } else {
+      if (D > 2 && after >= 2)
+        Reads::template values<4 * L, VOFF>(va, vt);
+      else if (after >= 1)
+        Reads::template values<2 * L, VOFF>(va, vt);
+      else
+        Reads::template values<0, VOFF>(va, vt);
+    }
     float sv[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) sv[i] = s4[i] * scale_log2;
@@ -1073,7 +1282,15 @@ __global__ __launch_bounds__(64 * kWaves) void decode_pv_kernel(DecodeArgs a) {
       if (patch && p == n_pages - 1 && e >= 0 && e < 4) {
 #pragma unroll
         for (int t = 0; t < DT; ++t) {
-          const uint32_t nv = lds_read2_now(new_v_s + t * 16 + r);
+          uint32_t nv;
+          if constexpr (kFp8) {
+            const auto pr = Dot2<T>::template from_fp8<false>(lds_read1_now(new_v_s + t * 16 + r));
+            uint32_t both;
+            __builtin_memcpy(&both, &pr, 4);
+            nv = both & 0xFFFFu;
+          } else {
+            nv = lds_read2_now(new_v_s + t * 16 + r);
+          }
           const int w = e >> 1, sh = (e & 1) * 16;
           vt[t][w] = (vt[t][w] & ~(0xFFFFu << sh)) | (nv << sh);
         }
@@ -1125,7 +1342,7 @@ __global__ __launch_bounds__(64 * kWaves) void decode_pv_kernel(DecodeArgs a) {
 
   // The staged rows to the pool, once this wave has read the page that holds their slot.
   if constexpr (ROPE) {
-    if (staged) write_staged_rows<T, T, DH, BS>(a, b, kvh, lane, new_k_s, new_v_s);
+    if (staged) write_staged_rows<T, KV, DH, BS>(a, b, kvh, lane, new_k_s, new_v_s);
   }
 
   // Per-wave state, in the ring's memory once every wave is done with it: l summed
@@ -1163,15 +1380,16 @@ __global__ __launch_bounds__(64 * kWaves) void decode_pv_kernel(DecodeArgs a) {
       L_ += e * l_s[w * G + h];
       o += e * acc_s[(w * G + h) * DH + d];
     }
+    // v_scale (1 for pools in the model dtype, an exact no-op) decodes V.
     if (single) {
-      out[b * a.o_ss + (int64_t)(kvh * G + h) * a.o_hs + d] = from_float<T>(o / L_);
+      out[b * a.o_ss + (int64_t)(kvh * G + h) * a.o_hs + d] = from_float<T>(o / L_ * a.v_scale);
     } else {
       const int64_t w = ((int64_t)b * a.num_q_heads + kvh * G + h) * a.max_splits + split;
       if (d == 0) {
         a.ws_m[w] = M_;
         a.ws_l[w] = L_;
       }
-      a.ws_acc[w * DH + d] = o;
+      a.ws_acc[w * DH + d] = o * a.v_scale;
     }
   }
 }
@@ -1193,11 +1411,11 @@ int32_t launch_typed(const DecodeArgs &a, int32_t num_seqs, int32_t num_kv_heads
         return check_launch();                                                      \
       }                                                                             \
     }                                                                               \
-    if constexpr (sizeof(KV) != 1 && kPvMfma) {                                     \
-      decode_pv_kernel<T, DH, GG, ROPE><<<grid, 64 * kWaves, 0, s>>>(a);            \
-      return check_launch();                                                        \
+    if constexpr (kPvMfma) {                                                        \
+      decode_pv_kernel<T, KV, DH, GG, ROPE><<<grid, 64 * kWaves, 0, s>>>(a);        \
+    } else {                                                                        \
+      decode_mfma_kernel<T, KV, DH, GG, ROPE><<<grid, 64 * kWaves, 0, s>>>(a);      \
     }                                                                               \
-    decode_mfma_kernel<T, KV, DH, GG, ROPE><<<grid, 64 * kWaves, 0, s>>>(a);        \
     return check_launch();                                                          \
   }
   TKS_DECODE(128, 4)
