@@ -978,16 +978,26 @@ struct IntConst {
   static constexpr int value = N;
 };
 
-template <typename T, typename KV, int DH, int G, bool ROPE>
+// ROWS: fp8 pools with one scale per pool row (a.k_rs, a.v_rs): a page's 16 K and 16
+// V scales ride in the ring with it; a lane multiplies its scores by its tokens' K
+// scales and its probabilities, after they enter the row sum, by their V scales.
+template <typename T, typename KV, int DH, int G, bool ROPE, bool ROWS = false>
 __global__ __launch_bounds__(64 * kWaves) void decode_pv_kernel(DecodeArgs a) {
   constexpr bool kFp8 = sizeof(KV) == 1;
+  static_assert(!ROWS || (kFp8 && !ROPE), "row scales: fp8 pools, plain decode");
   constexpr int BS = 16, NC = DH / 32, DT = DH / 16, CPR = DH / 8;
   constexpr int kPage = BS * DH;                        // elements of one K (or V) page
   constexpr int kRowBytes = DH * (int)sizeof(KV);       // one pool row as stored
   constexpr int CPRR = kRowBytes / 16;                  // its 16-byte chunks
   constexpr int kPageBytes = BS * kRowBytes;
-  constexpr int kStageBytes = 2 * kPageBytes;           // K page, then V page
+  // ROWS: one load of the page's 16 K and 16 V scales by every lane (lanes 8-63 repeat
+  // lanes 0-7), so the K scales sit at the area's start and the V scales 64 bytes on.
+  constexpr int kScaleBytes = ROWS ? 16 * 64 : 0;
+  constexpr int kStageBytes = 2 * kPageBytes + kScaleBytes;  // K page, V page, scales
   constexpr int L = kPageBytes / (16 * 64);             // HBM -> LDS loads per page tile
+  // A page's loads, in issue order: its scales (ROWS), its K tile, its V tile.
+  constexpr int kTileOps = L;
+  constexpr int kPageOps = 2 * L + (ROWS ? 1 : 0);
   // fp8 pools: each wave decodes its current V page into a staging page of T, laid
   // out as a page of a pool in the model dtype (the V^T reads are the same).
   constexpr int kStagingBytes = kFp8 ? kPage * (int)sizeof(T) : 0;
@@ -1090,6 +1100,16 @@ __global__ __launch_bounds__(64 * kWaves) void decode_pv_kernel(DecodeArgs a) {
   const char *vcb = reinterpret_cast<const char *>(static_cast<const KV *>(a.vc) + a.pool.layer_base +
                                                    (int64_t)kvh * a.pool.head_stride);
   const int64_t block_bytes = a.pool.block_stride * (int64_t)sizeof(KV);
+  // ROWS: the scales of token 0 of this head's page in block 0; a block's are
+  // rows_per_block floats further.
+  const int64_t rows_per_block = a.pool.block_stride / DH;
+  const float *ks_page = nullptr;
+  const float *vs_page = nullptr;
+  if constexpr (ROWS) {
+    const int64_t base = (a.pool.layer_base + (int64_t)kvh * a.pool.head_stride) / DH;
+    ks_page = a.k_rs + base;
+    vs_page = a.v_rs + base;
+  }
   auto k_swizzle = [](int row) { return kFp8 ? pv_k8_swizzle<DH>(row) : Swz::k(row); };
   // Load j of a page tile fills 16-byte LDS slot j*64 + lane = row * CPRR + physical
   // chunk, with logical chunk physical ^ swizzle(row) of that row.
@@ -1151,6 +1171,10 @@ __global__ __launch_bounds__(64 * kWaves) void decode_pv_kernel(DecodeArgs a) {
     const int64_t blk = clamp_block(__builtin_amdgcn_readlane(blk_reg, idx), a.pool.num_blocks);
     const char *kp = kcb + blk * block_bytes;
     const char *vp = vcb + blk * block_bytes;
+    if constexpr (ROWS) {
+      const float *src = ((lane & 7) < 4 ? ks_page : vs_page) + blk * rows_per_block + (lane & 3) * 4;
+      load_lds16<kPvLoadPolicy>(src, wring + SLOT * kStageBytes + 2 * kPageBytes);
+    }
 #pragma unroll
     for (int j = 0; j < L; ++j)
       load_lds16<kPvLoadPolicy>(kp + k_src[j], wring + SLOT * kStageBytes + j * 1024);
@@ -1164,14 +1188,22 @@ __global__ __launch_bounds__(64 * kWaves) void decode_pv_kernel(DecodeArgs a) {
     constexpr int SLOT = decltype(slot_c)::value;
     constexpr int KOFF = SLOT * kStageBytes, VOFF = KOFF + kPageBytes;
     f4 s4 = {0.f, 0.f, 0.f, 0.f};
+    float ks4[4] = {1.f, 1.f, 1.f, 1.f}, vs4[4] = {1.f, 1.f, 1.f, 1.f};
     if constexpr (kFp8) {
       u32x2 kr[NC];
       if (D > 2 && after >= 2)
-        Reads8::template keys<5 * L, KOFF>(ka, kr);
+        Reads8::template keys<kTileOps + 2 * kPageOps, KOFF>(ka, kr);
       else if (after >= 1)
-        Reads8::template keys<3 * L, KOFF>(ka, kr);
+        Reads8::template keys<kTileOps + kPageOps, KOFF>(ka, kr);
       else
-        Reads8::template keys<L, KOFF>(ka, kr);
+        Reads8::template keys<kTileOps, KOFF>(ka, kr);
+      if constexpr (ROWS) {  // this lane's tokens' K scales (the wait above covers them)
+        const uint4 u = lds_read16_now(wring + KOFF + 2 * kPageBytes + grp * 16);
+        ks4[0] = __uint_as_float(u.x);
+        ks4[1] = __uint_as_float(u.y);
+        ks4[2] = __uint_as_float(u.z);
+        ks4[3] = __uint_as_float(u.w);
+      }
       if constexpr (ROPE) {
         // The new token's K codes in place of what was loaded of its slot.
         if (patch && p == n_pages - 1 && r == new_off) {
@@ -1188,11 +1220,11 @@ __global__ __launch_bounds__(64 * kWaves) void decode_pv_kernel(DecodeArgs a) {
     } else {
       u32x4 kr[NC];
       if (D > 2 && after >= 2)
-        Reads::template keys<5 * L, KOFF>(ka, kr);
+        Reads::template keys<kTileOps + 2 * kPageOps, KOFF>(ka, kr);
       else if (after >= 1)
-        Reads::template keys<3 * L, KOFF>(ka, kr);
+        Reads::template keys<kTileOps + kPageOps, KOFF>(ka, kr);
       else
-        Reads::template keys<L, KOFF>(ka, kr);
+        Reads::template keys<kTileOps, KOFF>(ka, kr);
       Reads::wait(kr);
       if constexpr (ROPE) {
         // The new token's K row in place of what was loaded of its slot.
@@ -1214,31 +1246,46 @@ __global__ __launch_bounds__(64 * kWaves) void decode_pv_kernel(DecodeArgs a) {
     if constexpr (kFp8) {
       u32x4 raw[L], dec[2 * L];
       if (D > 2 && after >= 2)
-        Reads8::template raw_values<4 * L, VOFF>(vra, raw);
+        Reads8::template raw_values<2 * kPageOps, VOFF>(vra, raw);
       else if (after >= 1)
-        Reads8::template raw_values<2 * L, VOFF>(vra, raw);
+        Reads8::template raw_values<kPageOps, VOFF>(vra, raw);
       else
         Reads8::template raw_values<0, VOFF>(vra, raw);
+      if constexpr (ROWS) {  // this lane's tokens' V scales
+        const uint4 u = lds_read16_now(wring + KOFF + 2 * kPageBytes + BS * 4 + grp * 16);
+        vs4[0] = __uint_as_float(u.x);
+        vs4[1] = __uint_as_float(u.y);
+        vs4[2] = __uint_as_float(u.z);
+        vs4[3] = __uint_as_float(u.w);
+      }
 #pragma unroll
       for (int j = 0; j < L; ++j) decode_fp8_chunk<T>(raw[j], dec[2 * j], dec[2 * j + 1]);
       Reads8::staged_values(vwa, dec, va, vt);
     } else {
       if (D > 2 && after >= 2)
-        Reads::template values<4 * L, VOFF>(va, vt);
+        Reads::template values<2 * kPageOps, VOFF>(va, vt);
       else if (after >= 1)
-        Reads::template values<2 * L, VOFF>(va, vt);
+        Reads::template values<kPageOps, VOFF>(va, vt);
       else
         Reads::template values<0, VOFF>(va, vt);
     }
     float sv[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) sv[i] = s4[i] * scale_log2;
+    if constexpr (ROWS) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) sv[i] *= ks4[i];
+    }
     // The sequence's last page (uniform): keys past len score -inf, and their V
     // values, whatever the pool holds there, become 0 below (0 * NaN is NaN).
     const bool tail = kCheckEnd && (p + 1) * BS > len;
     if (tail) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) sv[i] = p * BS + grp * 4 + i < len ? sv[i] : -INFINITY;
+      for (int i = 0; i < 4; ++i) {
+        const bool valid = p * BS + grp * 4 + i < len;
+        sv[i] = valid ? sv[i] : -INFINITY;
+        if constexpr (ROWS) vs4[i] = valid ? vs4[i] : 0.f;  // an unwritten row's scale may be NaN
+      }
     }
     bool over = false;
 #pragma unroll
@@ -1264,7 +1311,7 @@ __global__ __launch_bounds__(64 * kWaves) void decode_pv_kernel(DecodeArgs a) {
     l += (pv[0] + pv[1]) + (pv[2] + pv[3]);
     v4 pb;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) pb[i] = static_cast<typename M::elem>(pv[i]);
+    for (int i = 0; i < 4; ++i) pb[i] = static_cast<typename M::elem>(ROWS ? pv[i] * vs4[i] : pv[i]);
     Reads::wait(vt);
     if (tail) {
       const int base = p * BS + grp * 4;
@@ -1407,7 +1454,10 @@ int32_t launch_typed(const DecodeArgs &a, int32_t num_seqs, int32_t num_kv_heads
   if (head_dim == DH && G == GG) {                                                  \
     if constexpr (sizeof(KV) == 1 && !ROPE) {                                       \
       if (a.k_rs != nullptr) {                                                      \
-        decode_mfma_kernel<T, KV, DH, GG, false, true><<<grid, 64 * kWaves, 0, s>>>(a); \
+        if constexpr (kPvMfma)                                                      \
+          decode_pv_kernel<T, KV, DH, GG, false, true><<<grid, 64 * kWaves, 0, s>>>(a); \
+        else                                                                        \
+          decode_mfma_kernel<T, KV, DH, GG, false, true><<<grid, 64 * kWaves, 0, s>>>(a); \
         return check_launch();                                                      \
       }                                                                             \
     }                                                                               \
