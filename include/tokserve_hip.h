@@ -342,8 +342,12 @@ int32_t tks_rope_append_paged_decode_fp8(
  * exactly the function of its counterpart on the decoded pools, in fp32, with
  * each key's scale applied to its scores and each value's to its probabilities.
  * Rows no sequence has written are never read into an output (their codes and
- * scales may hold anything). The decode's fused RoPE + append runs as the append
- * launch followed by the attention launch.
+ * scales may hold anything). The decode's fused RoPE + append runs in the
+ * attention launch, as its per-pool counterpart does, where the MFMA decode takes
+ * the shape (bf16 / fp16 queries, 16-byte aligned new rows): the new rows are
+ * quantized with scales of their own, attended to and written with them, bit for
+ * bit as tks_rope_kv_append_fp8_rows followed by tks_paged_attention_decode_fp8_rows;
+ * elsewhere it runs as those two launches.
  */
 int32_t tks_kv_append_fp8_rows(const void *key, int64_t key_token_stride,
                                int64_t key_head_stride, const void *value,

@@ -8,7 +8,9 @@ pages, a new token that opens a page), the two-launch path the entry takes elsew
 negative slot (nothing appended) and an empty
 sequence (its row is appended, its output is zero). Over fp8 (e4m3) pools the same
 against tks_rope_kv_append_fp8 then tks_paged_attention_decode_fp8, and the fp8
-RoPE + append launch against tks_rope then the quantizing tks_kv_append_fp8.
+RoPE + append launch against tks_rope then the quantizing tks_kv_append_fp8. Over fp8
+pools with one scale per pool row, the fused launch against the per-row
+tks_rope_kv_append_fp8_rows then the decode: outputs, codes and scales bit-identical.
 """
 
 import pytest
@@ -372,3 +374,104 @@ def test_fused_decode_step_argument_errors(device) -> None:
                                      batch.value_cache, slots, batch.block_tables,
                                      batch.seq_lens, layer_index=1,
                                      max_seq_len=batch.max_seq_len)
+
+
+ROWS_CASES = [
+    # dtype, Hq, Hkv, Dh, contexts
+    (torch.bfloat16, 32, 4, 64, [64 + 37 * i for i in range(24)]),  # the e2e shape, G 8
+    (torch.bfloat16, 32, 8, 128, [1, 16, 17, 31, 32, 33, 200, 1025, 4096, 4097]),
+    (torch.float16, 16, 8, 128, [5, 48, 49, 700]),
+    (torch.bfloat16, 32, 4, 128, [90, 900, 33]),     # G 8 at Dh 128
+    (torch.bfloat16, 32, 2, 64, [300, 17, 1]),       # G 16 at Dh 64
+    (torch.float32, 8, 2, 64, [16, 17, 513, 100]),   # fp32: two launches
+]
+
+
+def _rows_inputs(device, dtype, hq, hkv, dh, contexts, seed):
+    batch = workloads.paged_batch(contexts, [1] * len(contexts), num_q_heads=hq,
+                                  num_kv_heads=hkv, head_dim=dh, block_size=16, dtype=dtype,
+                                  device=device, seed=seed, kv_dtype=FP8,
+                                  scale_granularity="row")
+    _, query, key, value, positions, slots, table = _inputs(device, dtype, hq, hkv, dh,
+                                                            contexts, seed)
+    return batch, query, key, value, positions, slots, table
+
+
+def _rows_two_calls(batch, query, key, value, positions, table, slots, **kw):
+    """The reference: the per-row RoPE + quantizing append, then the decode, on copies
+    of the pools and scales."""
+    pools = [t.clone() for t in (batch.key_cache, batch.value_cache, batch.k_scales,
+                                 batch.v_scales)]
+    q_ref = query.clone()
+    ops.rope_kv_append(q_ref, key, value, positions, table, pools[0], pools[1], slots, 0,
+                       k_scales=pools[2], v_scales=pools[3])
+    out = ops.paged_attention_decode(q_ref, pools[0], pools[1], batch.block_tables,
+                                     batch.seq_lens, layer_index=0,
+                                     max_seq_len=kw.pop("max_seq_len", batch.max_seq_len),
+                                     k_scales=pools[2], v_scales=pools[3], **kw)
+    return out, pools
+
+
+def _assert_rows_equal(batch, actual, expected, pools, dtype) -> None:
+    bits = torch.int32 if dtype == torch.float32 else torch.int16
+    assert torch.equal(actual.cpu().view(bits), expected.cpu().view(bits))
+    assert torch.equal(batch.key_cache.view(torch.uint8), pools[0].view(torch.uint8))
+    assert torch.equal(batch.value_cache.view(torch.uint8), pools[1].view(torch.uint8))
+    assert torch.equal(batch.k_scales.view(torch.int32), pools[2].view(torch.int32))
+    assert torch.equal(batch.v_scales.view(torch.int32), pools[3].view(torch.int32))
+
+
+@pytest.mark.parametrize("case", range(len(ROWS_CASES)))
+@pytest.mark.parametrize("pages_per_split", [0, 2])
+def test_fused_decode_step_over_row_scaled_fp8_pools(device, case, pages_per_split) -> None:
+    """One scale per pool row: the fused launch quantizes the new rows with scales of
+    their own (amax / 448), attends with them in place of what their slot held, and
+    writes codes and scales; all of it bit for bit as the per-row append followed by the
+    decode. New rows include a NaN key element, an all-zero value row and large keys."""
+    dtype, hq, hkv, dh, contexts = ROWS_CASES[case]
+    batch, query, key, value, positions, slots, table = _rows_inputs(
+        device, dtype, hq, hkv, dh, contexts, seed=80 + case)
+    key[min(2, len(contexts) - 1), 0, 5] = float("nan")
+    value[min(1, len(contexts) - 1)] = 0.0
+    key[0] *= 300.0
+    order = ops.longest_first(batch.contexts, device)
+    query_before = query.clone()
+    expected, pools = _rows_two_calls(batch, query, key, value, positions, table, slots,
+                                      pages_per_split=pages_per_split, seq_order=order)
+    actual = ops.rope_append_paged_decode(
+        query, key, value, positions, table, batch.key_cache, batch.value_cache, slots,
+        batch.block_tables, batch.seq_lens, layer_index=0, max_seq_len=batch.max_seq_len,
+        pages_per_split=pages_per_split, seq_order=order, k_scales=batch.k_scales,
+        v_scales=batch.v_scales)
+    torch.cuda.synchronize()
+    _assert_rows_equal(batch, actual, expected, pools, dtype)
+    assert torch.equal(query, query_before)
+
+
+def test_fused_decode_step_over_row_scaled_pools_empty_and_negative_slots(device) -> None:
+    """Row scales: an empty sequence still appends its rows (codes and scales) and gets a
+    zero output; a negative slot appends nothing; both as the two calls do."""
+    dtype, hq, hkv, dh = torch.bfloat16, 32, 4, 64
+    contexts = [0, 40, 17, 0, 33]
+    batch = workloads.paged_batch(contexts, [1] * 5, num_q_heads=hq, num_kv_heads=hkv,
+                                  head_dim=dh, block_size=16, dtype=dtype, device=device,
+                                  seed=23, num_blocks=12, kv_dtype=FP8,
+                                  scale_granularity="row")
+    _, query, key, value, positions, slots, table = _inputs(device, dtype, hq, hkv, dh,
+                                                            [1, 40, 17, 1, 33], seed=23)
+    tables = batch.block_tables.cpu()
+    used = {int(tables[b, p]) for b in (1, 2, 4) for p in range((contexts[b] + 15) // 16)}
+    free = [blk for blk in range(12) if blk not in used]
+    slots[0], slots[3] = free[0] * 16 + 5, free[1] * 16 + 15
+    for b in (1, 2, 4):
+        slots[b] = int(tables[b, (contexts[b] - 1) // 16]) * 16 + (contexts[b] - 1) % 16
+    slots[4] = -1
+    positions[0], positions[3] = 0, 7
+    expected, pools = _rows_two_calls(batch, query, key, value, positions, table, slots)
+    actual = ops.rope_append_paged_decode(
+        query, key, value, positions, table, batch.key_cache, batch.value_cache, slots,
+        batch.block_tables, batch.seq_lens, layer_index=0, max_seq_len=batch.max_seq_len,
+        k_scales=batch.k_scales, v_scales=batch.v_scales)
+    torch.cuda.synchronize()
+    _assert_rows_equal(batch, actual, expected, pools, dtype)
+    assert not actual[0].any() and not actual[3].any()

@@ -229,6 +229,29 @@ struct DecodeArgs {
   float k_scale = 1.f;  // e4m3 pools: the new key row is stored as e4m3(key / k_scale)
 };
 
+// fp8 pools with one fp32 scale per pool row (token, KV head): the row's scale is
+// amax / 448, amax its largest |x| (NaN once any value is NaN), and 1 where that
+// quotient is 0, NaN or infinite.
+constexpr float kE4m3Largest = 448.f;
+
+// Largest |x| so far, NaN once any value is NaN.
+__device__ __forceinline__ float abs_max_nan(float m, float x) {
+  const float ax = fabsf(x);
+  return (m != m || ax != ax) ? __builtin_nanf("") : fmaxf(m, ax);
+}
+
+// The same over the 64 lanes of a wave (every lane active).
+__device__ __forceinline__ float wave_abs_max(float m) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) m = abs_max_nan(m, __shfl_xor(m, o, 64));
+  return m;
+}
+
+__device__ __forceinline__ float row_scale_of(float amax) {
+  const float s = amax / kE4m3Largest;
+  return (s > 0.f && s < INFINITY) ? s : 1.f;
+}
+
 struct PrefillArgs {
   const void *q;
   int64_t q_ts, q_hs;  // token and head strides of the packed query

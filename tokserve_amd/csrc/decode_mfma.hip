@@ -229,14 +229,57 @@ __device__ __forceinline__ void store_chunk(KV *dst, typename PageIO<T, KV>::raw
 // the new rows are staged in LDS (k_s, v_s: Dh entries each, in the pool's form):
 // sequence b's key row rotated at its position and its value row, as T or, over
 // e4m3 pools, as the codes of the rotated row (rounded to T first) and of the value
-// row; lanes t < 3 Dh / 16 take part. Returns whether slot a.slots[b] lies in the
-// pool (a negative slot appends nothing).
-template <typename T, typename KV, int DH, int BS>
+// row; lanes t < 3 Dh / 16 take part (every lane of the wave with ROWS, where each
+// row has a scale of its own). Returns whether slot a.slots[b] lies in the pool (a
+// negative slot appends nothing).
+template <typename T, typename KV, int DH, int BS, bool ROWS = false>
 __device__ __forceinline__ bool stage_new_rows(const DecodeArgs &a, int b, int kvh, int t,
-                                               KV *k_s, KV *v_s) {
+                                               KV *k_s, KV *v_s, float *scale_s = nullptr) {
   constexpr int HALF = DH / 2;
   const int64_t slot = a.slots[b];
   if (slot < 0 || slot >= a.pool.num_blocks * BS) return false;
+  if constexpr (ROWS) {
+    // One scale per row (amax / 448 over its Dh values, the key's after the
+    // rotation and its rounding to T): wave maxima over the lanes holding each row,
+    // so every lane of the wave takes part; the scales go to scale_s[0..1].
+    static_assert(sizeof(KV) == 1, "row scales: fp8 pools");
+    const bool kl = t < HALF / 8;
+    const bool vl = !kl && t < HALF / 8 + DH / 8;
+    float o1[8], o2[8], x[8];
+    float kmax = 0.f, vmax = 0.f;
+    if (kl) {
+      const T *kn = static_cast<const T *>(a.k_new) + b * a.kn_ss + (int64_t)kvh * a.kn_hs;
+      const int64_t pos = min(max(a.positions[b], (int64_t)0), a.table_len - 1);
+      float cf[8], sf[8];
+      load_table<T, 8>(static_cast<const T *>(a.cos_t) + pos * HALF,
+                       static_cast<const T *>(a.sin_t) + pos * HALF, t * 8, cf, sf);
+      rotate_values<T, 8>(kn + t * 8, cf, sf, HALF, o1, o2);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        o1[e] = round_through<T>(o1[e]);
+        o2[e] = round_through<T>(o2[e]);
+        kmax = abs_max_nan(abs_max_nan(kmax, o1[e]), o2[e]);
+      }
+    } else if (vl) {
+      const T *vn = static_cast<const T *>(a.v_new) + b * a.vn_ss + (int64_t)kvh * a.vn_hs;
+      unpack<T>(ld16(vn + (t - HALF / 8) * 8), x);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) vmax = abs_max_nan(vmax, x[e]);
+    }
+    const float ks = row_scale_of(wave_abs_max(kmax));
+    const float vs = row_scale_of(wave_abs_max(vmax));
+    if (kl) {
+      store_chunk<T, KV>(k_s + t * 8, pool_chunk<T, KV>(o1, ks));
+      store_chunk<T, KV>(k_s + t * 8 + HALF, pool_chunk<T, KV>(o2, ks));
+    } else if (vl) {
+      store_chunk<T, KV>(v_s + (t - HALF / 8) * 8, pool_chunk<T, KV>(x, vs));
+    }
+    if (t == 0) {
+      scale_s[0] = ks;
+      scale_s[1] = vs;
+    }
+    return true;
+  }
   if (t < HALF / 8) {
     const T *kn = static_cast<const T *>(a.k_new) + b * a.kn_ss + (int64_t)kvh * a.kn_hs;
     const int64_t pos = min(max(a.positions[b], (int64_t)0), a.table_len - 1);
@@ -281,9 +324,12 @@ __device__ __forceinline__ typename PageIO<T, KV>::raw load_chunk(const KV *p) {
 
 // Then the staged rows go from LDS to pool slot a.slots[b] (lanes t < Dh / 4; the
 // slot was checked by stage_new_rows).
-template <typename T, typename KV, int DH, int BS>
+// ROWS: lanes 0 and Dh / 8 also store the rows' scales from scale_s to their slot
+// of the scale arrays.
+template <typename T, typename KV, int DH, int BS, bool ROWS = false>
 __device__ __forceinline__ void write_staged_rows(const DecodeArgs &a, int b, int kvh, int t,
-                                                  const KV *k_s, const KV *v_s) {
+                                                  const KV *k_s, const KV *v_s,
+                                                  const float *scale_s = nullptr) {
   if (t >= DH / 4) return;
   const int64_t slot = a.slots[b];
   const int64_t blk = slot / BS;
@@ -293,6 +339,9 @@ __device__ __forceinline__ void write_staged_rows(const DecodeArgs &a, int b, in
   const int c = (is_k ? t : t - DH / 8) * 8;
   KV *dst = static_cast<KV *>(const_cast<void *>(is_k ? a.kc : a.vc)) + row + c;
   store_chunk<T, KV>(dst, load_chunk<T, KV>((is_k ? k_s : v_s) + c));
+  if constexpr (ROWS) {
+    if (c == 0) const_cast<float *>(is_k ? a.k_rs : a.v_rs)[row / DH] = scale_s[is_k ? 0 : 1];
+  }
 }
 
 // ROPE: RoPE and the KV append of the sequence's new token fused in (DecodeArgs).
@@ -984,7 +1033,7 @@ struct IntConst {
 template <typename T, typename KV, int DH, int G, bool ROPE, bool ROWS = false>
 __global__ __launch_bounds__(64 * kWaves) void decode_pv_kernel(DecodeArgs a) {
   constexpr bool kFp8 = sizeof(KV) == 1;
-  static_assert(!ROWS || (kFp8 && !ROPE), "row scales: fp8 pools, plain decode");
+  static_assert(!ROWS || kFp8, "row scales: fp8 pools");
   constexpr int BS = 16, NC = DH / 32, DT = DH / 16, CPR = DH / 8;
   constexpr int kPage = BS * DH;                        // elements of one K (or V) page
   constexpr int kRowBytes = DH * (int)sizeof(KV);       // one pool row as stored
@@ -1019,6 +1068,7 @@ __global__ __launch_bounds__(64 * kWaves) void decode_pv_kernel(DecodeArgs a) {
   __shared__ __attribute__((aligned(16))) char ring[kRingBytes];
   __shared__ __attribute__((aligned(16))) KV new_k_s[ROPE ? DH : 1];
   __shared__ __attribute__((aligned(16))) KV new_v_s[ROPE ? DH : 1];
+  __shared__ float new_scale_s[(ROPE && ROWS) ? 2 : 1];  // the staged rows' K, V scales
   __shared__ __attribute__((aligned(16))) T q_s[G * DH];
 
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -1041,9 +1091,11 @@ __global__ __launch_bounds__(64 * kWaves) void decode_pv_kernel(DecodeArgs a) {
         out[b * a.o_ss + (int64_t)(kvh * G + i / DH) * a.o_hs + i % DH] = from_float<T>(0.f);
       if constexpr (ROPE) {
         if (n_pages == 0 && threadIdx.x < 64 &&
-            stage_new_rows<T, KV, DH, BS>(a, b, kvh, threadIdx.x, new_k_s, new_v_s)) {
+            stage_new_rows<T, KV, DH, BS, ROWS>(a, b, kvh, threadIdx.x, new_k_s, new_v_s,
+                                                new_scale_s)) {
           wave_lds_sync();
-          write_staged_rows<T, KV, DH, BS>(a, b, kvh, threadIdx.x, new_k_s, new_v_s);
+          write_staged_rows<T, KV, DH, BS, ROWS>(a, b, kvh, threadIdx.x, new_k_s, new_v_s,
+                                                 new_scale_s);
         }
       }
     }
@@ -1061,14 +1113,22 @@ __global__ __launch_bounds__(64 * kWaves) void decode_pv_kernel(DecodeArgs a) {
   bool staged = false;
   bool patch = false;
   const int new_off = ROPE ? (len - 1) % BS : 0;
+  float new_ks = 1.f, new_vs = 1.f;  // ROWS: the staged rows' scales, in registers
   {
     const int t = threadIdx.x;
     if constexpr (ROPE) {
       constexpr int HALF = DH / 2;
       if (w_begin < w_end && w_end == n_pages) {  // wave-uniform
-        staged = stage_new_rows<T, KV, DH, BS>(a, b, kvh, lane, new_k_s, new_v_s);
+        staged = stage_new_rows<T, KV, DH, BS, ROWS>(a, b, kvh, lane, new_k_s, new_v_s,
+                                                     new_scale_s);
         patch = staged && a.seq_lens[b] == len;
         wave_lds_sync();
+        if constexpr (ROWS) {
+          if (staged) {
+            new_ks = new_scale_s[0];
+            new_vs = new_scale_s[1];
+          }
+        }
       }
       if (t < G * HALF / 8) {
         const int64_t pos = min(max(a.positions[b], (int64_t)0), a.table_len - 1);
@@ -1203,6 +1263,12 @@ __global__ __launch_bounds__(64 * kWaves) void decode_pv_kernel(DecodeArgs a) {
         ks4[1] = __uint_as_float(u.y);
         ks4[2] = __uint_as_float(u.z);
         ks4[3] = __uint_as_float(u.w);
+        if constexpr (ROPE) {  // the new token's scale in place of its slot's
+          if (patch && p == n_pages - 1) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) ks4[i] = grp * 4 + i == new_off ? new_ks : ks4[i];
+          }
+        }
       }
       if constexpr (ROPE) {
         // The new token's K codes in place of what was loaded of its slot.
@@ -1257,6 +1323,12 @@ __global__ __launch_bounds__(64 * kWaves) void decode_pv_kernel(DecodeArgs a) {
         vs4[1] = __uint_as_float(u.y);
         vs4[2] = __uint_as_float(u.z);
         vs4[3] = __uint_as_float(u.w);
+        if constexpr (ROPE) {
+          if (patch && p == n_pages - 1) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) vs4[i] = grp * 4 + i == new_off ? new_vs : vs4[i];
+          }
+        }
       }
 #pragma unroll
       for (int j = 0; j < L; ++j) decode_fp8_chunk<T>(raw[j], dec[2 * j], dec[2 * j + 1]);
@@ -1389,7 +1461,8 @@ __global__ __launch_bounds__(64 * kWaves) void decode_pv_kernel(DecodeArgs a) {
 
   // The staged rows to the pool, once this wave has read the page that holds their slot.
   if constexpr (ROPE) {
-    if (staged) write_staged_rows<T, KV, DH, BS>(a, b, kvh, lane, new_k_s, new_v_s);
+    if (staged)
+      write_staged_rows<T, KV, DH, BS, ROWS>(a, b, kvh, lane, new_k_s, new_v_s, new_scale_s);
   }
 
   // Per-wave state, in the ring's memory once every wave is done with it: l summed
@@ -1452,10 +1525,10 @@ int32_t launch_typed(const DecodeArgs &a, int32_t num_seqs, int32_t num_kv_heads
   const dim3 grid(num_kv_heads, num_seqs, a.max_splits);
 #define TKS_DECODE(DH, GG)                                                          \
   if (head_dim == DH && G == GG) {                                                  \
-    if constexpr (sizeof(KV) == 1 && !ROPE) {                                       \
+    if constexpr (sizeof(KV) == 1) {                                                \
       if (a.k_rs != nullptr) {                                                      \
-        if constexpr (kPvMfma)                                                      \
-          decode_pv_kernel<T, KV, DH, GG, false, true><<<grid, 64 * kWaves, 0, s>>>(a); \
+        if constexpr (kPvMfma || ROPE)                                              \
+          decode_pv_kernel<T, KV, DH, GG, ROPE, true><<<grid, 64 * kWaves, 0, s>>>(a); \
         else                                                                        \
           decode_mfma_kernel<T, KV, DH, GG, false, true><<<grid, 64 * kWaves, 0, s>>>(a); \
         return check_launch();                                                      \

@@ -17,24 +17,6 @@ namespace {
 constexpr int kRowThreads = 256;
 constexpr int kRowWaves = kRowThreads / 64;
 constexpr int kMaxRowDh = 256;  // elements per lane: Dh / 64 <= 4
-constexpr float kE4m3Largest = 448.f;
-
-// Largest |x| so far, NaN once any value is NaN.
-__device__ __forceinline__ float abs_max_nan(float m, float x) {
-  const float ax = fabsf(x);
-  return (m != m || ax != ax) ? __builtin_nanf("") : fmaxf(m, ax);
-}
-
-__device__ __forceinline__ float wave_abs_max(float m) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) m = abs_max_nan(m, __shfl_xor(m, o, 64));
-  return m;
-}
-
-__device__ __forceinline__ float row_scale_of(float amax) {
-  const float s = amax / kE4m3Largest;
-  return (s > 0.f && s < INFINITY) ? s : 1.f;
-}
 
 struct RowsArgs {
   // New rows (in the model dtype): key and value per token and KV head.

@@ -596,10 +596,8 @@ int32_t decode_impl(const void *query, int64_t q_seq_stride, int64_t q_head_stri
     // the RoPE + append launch writes the rotated queries into `out`, which the
     // decode then reads as its query (each workgroup reads its rows before it, or
     // the merge, writes them).
-    // Row-scaled pools always take the two launches.
-    const bool fused = mfma && k_rs == nullptr &&
-                       aligned16(ra->key) && aligned16(ra->value) && aligned16(ra->cos_cache) &&
-                       aligned16(ra->sin_cache) && ra->k_ss % 8 == 0 && ra->k_hs % 8 == 0 &&
+    const bool fused = mfma && aligned16(ra->key) && aligned16(ra->value) &&
+                       aligned16(ra->cos_cache) && aligned16(ra->sin_cache) && ra->k_ss % 8 == 0 && ra->k_hs % 8 == 0 &&
                        ra->v_ss % 8 == 0 && ra->v_hs % 8 == 0;
     if (!fused) {
       void *kc = const_cast<void *>(key_cache), *vc = const_cast<void *>(value_cache);
