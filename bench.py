@@ -464,6 +464,8 @@ def main() -> int:
         if not args.no_secondary:
             result["secondary"]["e2e_tinyllama_fp8_kv"] = measure_e2e(
                 device, args.seed, None, kv_dtype=torch.float8_e4m3fn)
+            result["secondary"]["e2e_tinyllama_fp8_kv_rows"] = measure_e2e(
+                device, args.seed, None, kv_dtype=torch.float8_e4m3fn, scale_granularity="row")
             result["secondary"]["e2e_tinyllama_fp32"] = measure_e2e(
                 device, args.seed, None, dtype=torch.float32)
     if baseline is not None:
@@ -1037,7 +1039,7 @@ def measure_norm_rope(device, steps: int, warmup: int, cpu_seconds: float | None
 
 
 def _e2e_engine(model, specs, device, block_size: int = 16, kv_dtype=None, overlap=True,
-                num_blocks: int | None = None):
+                num_blocks: int | None = None, scale_granularity: str = "pool"):
     from tokserve_amd import workloads
     from tokserve_amd.batching.engine import ContinuousBatchEngine
     from tokserve_amd.engine.paged.manager import PagedKVCacheManager
@@ -1049,7 +1051,7 @@ def _e2e_engine(model, specs, device, block_size: int = 16, kv_dtype=None, overl
         num_blocks=num_blocks or workloads.pool_blocks(specs, block_size),
         num_key_value_heads=config.num_key_value_heads, block_size=block_size,
         head_dim=config.head_dim, device=device, dtype=model.embed_tokens.weight.dtype,
-        kv_dtype=kv_dtype)
+        kv_dtype=kv_dtype, **({} if kv_dtype is None else {"scale_granularity": scale_granularity}))
     scheduler = RequestScheduler(max_running_requests=128, cache_manager=manager)
     engine = ContinuousBatchEngine(model, scheduler, manager, overlap_decode=overlap)
     _submit(engine, specs, device)
@@ -1070,12 +1072,13 @@ def _submit(engine, specs, device, prefix: str = "") -> None:
 
 
 def measure_e2e(device, seed: int, cpu_seconds: float | None, kv_dtype=None,
-                dtype=None) -> dict:
+                dtype=None, scale_granularity: str = "pool") -> dict:
     """TinyLlama-1.1B (random init, bf16) serving 128 requests, prompts U[64, 1024],
     128 greedy tokens each, block size 16, max 128 running: the whole run through the
     continuous-batching engine, timed on the host wall clock (each step ends with its
     tokens on the host). tokens/s = generated tokens / wall time. kv_dtype
-    torch.float8_e4m3fn runs the same workload over fp8 K/V pools (scale 1); dtype
+    torch.float8_e4m3fn runs the same workload over fp8 K/V pools (scale 1, or with
+    scale_granularity="row" one scale per pool row, set by each append); dtype
     torch.float32 runs it with the model in fp32 (the configuration whose greedy tokens
     must equal the reference's)."""
 
@@ -1107,7 +1110,7 @@ def measure_e2e(device, seed: int, cpu_seconds: float | None, kv_dtype=None,
 
     def serve(overlap: bool):
         engine = _e2e_engine(model, warm, device, kv_dtype=kv_dtype, overlap=overlap,
-                             num_blocks=blocks)
+                             num_blocks=blocks, scale_granularity=scale_granularity)
         engine.run_until_idle()
         torch.cuda.synchronize()
         first, done = len(engine.history), len(engine.results)
@@ -1134,7 +1137,8 @@ def measure_e2e(device, seed: int, cpu_seconds: float | None, kv_dtype=None,
     if graphs is not None and graphs._graphs:
         captured = graphs._graphs[max(graphs._graphs)]
         replay_ms = _time_ms(captured.graph.replay, 20, 3)
-    pools = "" if kv_dtype is None else "; fp8 e4m3 K/V pools"
+    pools = "" if kv_dtype is None else (
+        "; fp8 e4m3 K/V pools" + (", one scale per pool row" if scale_granularity == "row" else ""))
     dtype_name = {torch.bfloat16: "bf16", torch.float32: "fp32"}.get(dtype, str(dtype))
     result = {
         "workload": "e2e_tinyllama: TinyLlama-1.1B shape (22 layers, hidden 2048, 32/4 heads, "
