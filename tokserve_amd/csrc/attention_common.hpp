@@ -127,6 +127,14 @@ __device__ __forceinline__ void load_lds16(const void *src, void *lds) {
 #endif
 }
 
+// The same with 4 bytes per lane: lane i's bytes land at lds + 4 * i.
+template <int AUX = 0>
+__device__ __forceinline__ void load_lds4(const void *src, void *lds) {
+#if __HIP_DEVICE_COMPILE__
+  __builtin_amdgcn_global_load_lds(src, (lds_void *)lds, 4, 0, AUX);
+#endif
+}
+
 // Max and sum over lanes l, l^16, l^32, l^48 (the four k-groups of an MFMA
 // operand row), with the gfx950 cross-row lane swaps.
 //

@@ -1039,9 +1039,10 @@ __global__ __launch_bounds__(64 * kWaves) void decode_pv_kernel(DecodeArgs a) {
   constexpr int kRowBytes = DH * (int)sizeof(KV);       // one pool row as stored
   constexpr int CPRR = kRowBytes / 16;                  // its 16-byte chunks
   constexpr int kPageBytes = BS * kRowBytes;
-  // ROWS: one load of the page's 16 K and 16 V scales by every lane (lanes 8-63 repeat
-  // lanes 0-7), so the K scales sit at the area's start and the V scales 64 bytes on.
-  constexpr int kScaleBytes = ROWS ? 16 * 64 : 0;
+  // ROWS: one 4-byte load per lane of the page's 16 K and 16 V scales (lanes 32-63
+  // repeat lanes 0-31), so the K scales sit at the area's start and the V scales 64
+  // bytes on.
+  constexpr int kScaleBytes = ROWS ? 4 * 64 : 0;
   constexpr int kStageBytes = 2 * kPageBytes + kScaleBytes;  // K page, V page, scales
   constexpr int L = kPageBytes / (16 * 64);             // HBM -> LDS loads per page tile
   // A page's loads, in issue order: its scales (ROWS), its K tile, its V tile.
@@ -1232,8 +1233,8 @@ __global__ __launch_bounds__(64 * kWaves) void decode_pv_kernel(DecodeArgs a) {
     const char *kp = kcb + blk * block_bytes;
     const char *vp = vcb + blk * block_bytes;
     if constexpr (ROWS) {
-      const float *src = ((lane & 7) < 4 ? ks_page : vs_page) + blk * rows_per_block + (lane & 3) * 4;
-      load_lds16<kPvLoadPolicy>(src, wring + SLOT * kStageBytes + 2 * kPageBytes);
+      const float *src = ((lane & 31) < 16 ? ks_page : vs_page) + blk * rows_per_block + (lane & 15);
+      load_lds4<kPvLoadPolicy>(src, wring + SLOT * kStageBytes + 2 * kPageBytes);
     }
 #pragma unroll
     for (int j = 0; j < L; ++j)
