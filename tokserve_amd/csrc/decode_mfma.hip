@@ -1077,10 +1077,24 @@ __global__ __launch_bounds__(64 * kWaves) void decode_pv_kernel(DecodeArgs a) {
   const int r = lane & 15;    // K rows: token r; S and O^T: head column r
   const int grp = lane >> 4;  // K: dims grp*8 of each 32; S: tokens grp*4 .. +3; O^T: dims
 
-  const int kvh = blockIdx.x;
+  // Work item (rank, KV head) of this workgroup. ROWS with an even KV-head count: the
+  // 16 K (or V) scales of a page are 64 bytes, and the two KV heads of one 128-byte
+  // line go to workgroups 8 apart, i.e. dispatched one after the other on the same
+  // XCD (workgroup i runs on XCD i % 8), so the line comes from HBM once for both. A
+  // bijection on each whole 16 items of a split; the rest keep their places.
+  int kvh_i = blockIdx.x, rank_i = blockIdx.y;
+  if constexpr (ROWS) {
+    const int X = gridDim.x;
+    const int l = blockIdx.x + X * (int)blockIdx.y;
+    if ((X & 1) == 0 && l < ((X * (int)gridDim.y) & ~15)) {
+      const int item = 2 * ((l >> 4) * 8 + (l & 7)) + ((l >> 3) & 1);
+      kvh_i = item % X;
+      rank_i = item / X;
+    }
+  }
+  const int kvh = kvh_i;
   const int split = blockIdx.z;
-  const int b = a.seq_order ? min(max(a.seq_order[blockIdx.y], 0), (int)gridDim.y - 1)
-                            : (int)blockIdx.y;
+  const int b = a.seq_order ? min(max(a.seq_order[rank_i], 0), (int)gridDim.y - 1) : rank_i;
   // A length above the host bound is clamped so no access can leave its buffer.
   const int len = min(a.seq_lens[b], a.key_cap);
   const int n_pages = (len + BS - 1) / BS;
