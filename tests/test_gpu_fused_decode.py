@@ -475,3 +475,19 @@ def test_fused_decode_step_over_row_scaled_pools_empty_and_negative_slots(device
     torch.cuda.synchronize()
     _assert_rows_equal(batch, actual, expected, pools, dtype)
     assert not actual[0].any() and not actual[3].any()
+
+
+@pytest.mark.parametrize("dh", [64, 128])
+@pytest.mark.parametrize("group", [1, 2, 4, 8, 16])
+def test_fused_decode_step_every_mfma_group_over_row_scaled_pools(device, dh, group) -> None:
+    hkv = 2
+    contexts = [1, 15, 16, 17, 130, 700]
+    batch, query, key, value, positions, slots, table = _rows_inputs(
+        device, torch.float16, hkv * group, hkv, dh, contexts, seed=90 + group + dh)
+    expected, pools = _rows_two_calls(batch, query, key, value, positions, table, slots)
+    actual = ops.rope_append_paged_decode(
+        query, key, value, positions, table, batch.key_cache, batch.value_cache, slots,
+        batch.block_tables, batch.seq_lens, layer_index=0, max_seq_len=batch.max_seq_len,
+        k_scales=batch.k_scales, v_scales=batch.v_scales)
+    torch.cuda.synchronize()
+    _assert_rows_equal(batch, actual, expected, pools, torch.float16)
