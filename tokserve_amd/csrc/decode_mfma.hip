@@ -1,6 +1,11 @@
 // Paged decode with MFMA scores, bf16/fp16, block size 16.
 //
-// One workgroup of NW waves per (sequence, KV head[, split]). The pages of the
+// Two kernels. decode_pv_kernel (further below) is the one every launch takes: both
+// products on the MFMA pipe, K/V pages HBM -> LDS by DMA. decode_mfma_kernel, the
+// earlier design described next, computes P.V on the VALU; it is compiled only with
+// kPvMfma set to false, to compare the two.
+//
+// decode_mfma_kernel: one workgroup of NW waves per (sequence, KV head[, split]). The pages of the
 // sequence are cut into NW contiguous ranges, one per wave; the waves' partial
 // softmax states (m, l, acc) are merged through LDS at the end, so no result
 // ever crosses workgroups inside the kernel (a cross-workgroup split, used only

@@ -6,7 +6,7 @@
 // causal mask is key <= query position (:118-123), softmax is accumulated
 // online in fp32 (:125-136) and the output is acc / sum in the query dtype (:138).
 //
-// Decode (one query per sequence) goes to decode_mfma_kernel (decode_mfma.hip)
+// Decode (one query per sequence) goes to decode_pv_kernel (decode_mfma.hip)
 // for bf16/fp16 with block size 16 and Dh 64/128; every other shape and fp32
 // (where 1e-5 parity wants fp32 products) uses attn_generic_kernel below:
 // one 4-wave workgroup per (query row, KV head, split), 64 keys per wave step
