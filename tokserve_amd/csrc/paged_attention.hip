@@ -405,16 +405,18 @@ __global__ __launch_bounds__(128) void merge_splits_kernel(
 //    KV heads, contexts log-uniform in [128, 8192]: 39.3 / 41.8 us at 64 pages,
 //    34.8 / 37.0 us at 48, 39.3 / 45.9 us at 16; 16 sequences unsplit: 59 us).
 //  * Fewer than kSplitBelowItems pairs and a length bound of kSplitFromPages
-//    pages or more: 64-page splits (32 / 64 / 128 such Llama-3-8B sequences:
-//    107 / 145 / 183 -> 61 / 101 / 172 us).
-//  * Otherwise unsplit: 192 and 256 Llama-3-8B sequences (224 vs 256 us, 291 vs
-//    302+ split), and short contexts (128 sequences x 4 KV heads, Dh 64, contexts
-//    up to 1152 under a 2048-token bound: 20.5 us, 20.9 + 5.1 split).
+//    pages or more: 32-page splits (32 / 64 such Llama-3-8B sequences with the
+//    MFMA P.V kernel, split and merge: 45.3 / 90.5 us at 32 pages, 47.6 / 91.2 at
+//    64, 74.1 / 110.7 unsplit).
+//  * Otherwise unsplit: 128, 192 and 256 Llama-3-8B sequences (128: 161.4 us
+//    against 166.2 at 64 pages and 173.3 at 32; 192: 216.4 against 249.6+ split),
+//    and short contexts (128 sequences x 4 KV heads, Dh 64, contexts up to 1152
+//    under a 2048-token bound).
 constexpr int64_t kFillItems = 256;
 constexpr int64_t kMinSplitPages = 16;
 constexpr int64_t kMaxFillSplitPages = 48;
-constexpr int64_t kSplitBelowItems = 1536;
-constexpr int64_t kSplitPages = 64;
+constexpr int64_t kSplitBelowItems = 1024;
+constexpr int64_t kSplitPages = 32;
 constexpr int64_t kSplitFromPages = 256;
 
 int32_t choose_pages_per_split(int32_t num_seqs, int32_t num_kv_heads, int32_t block_size,
