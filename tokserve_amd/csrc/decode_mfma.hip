@@ -910,6 +910,28 @@ struct PvReads8<128> {
     (void)ka, (void)k;
 #endif
   }
+  // keys() and, in the same batch, this lane's four K scales and four V scales of the
+  // page (16 bytes at sa + OFF and sa + OFF + 64).
+  template <int VM, int OFF>
+  static __device__ __forceinline__ void keys_rows(const uint32_t (&ka)[4], u32x2 (&k)[4],
+                                                   uint32_t sa, u32x4 &ks, u32x4 &vs) {
+#if __HIP_DEVICE_COMPILE__
+    asm volatile("s_waitcnt vmcnt(%11)\n\t"
+                 "ds_read_b64 %0, %6 offset:%12\n\t"
+                 "ds_read_b64 %1, %7 offset:%12\n\t"
+                 "ds_read_b64 %2, %8 offset:%12\n\t"
+                 "ds_read_b64 %3, %9 offset:%12\n\t"
+                 "ds_read_b128 %4, %10 offset:%12\n\t"
+                 "ds_read_b128 %5, %10 offset:%13\n\t"
+                 "s_waitcnt lgkmcnt(0)"
+                 : "=&v"(k[0]), "=&v"(k[1]), "=&v"(k[2]), "=&v"(k[3]), "=&v"(ks), "=&v"(vs)
+                 : "v"(ka[0]), "v"(ka[1]), "v"(ka[2]), "v"(ka[3]), "v"(sa), "n"(VM), "i"(OFF),
+                   "i"(OFF + 64)
+                 : "memory");
+#else
+    (void)ka, (void)k, (void)sa, (void)ks, (void)vs;
+#endif
+  }
   template <int VM, int OFF>
   static __device__ __forceinline__ void raw_values(const uint32_t (&ra)[2], u32x4 (&v)[2]) {
 #if __HIP_DEVICE_COMPILE__
@@ -951,6 +973,23 @@ struct PvReads8<64> {
                  : "memory");
 #else
     (void)ka, (void)k;
+#endif
+  }
+  template <int VM, int OFF>
+  static __device__ __forceinline__ void keys_rows(const uint32_t (&ka)[2], u32x2 (&k)[2],
+                                                   uint32_t sa, u32x4 &ks, u32x4 &vs) {
+#if __HIP_DEVICE_COMPILE__
+    asm volatile("s_waitcnt vmcnt(%7)\n\t"
+                 "ds_read_b64 %0, %4 offset:%8\n\t"
+                 "ds_read_b64 %1, %5 offset:%8\n\t"
+                 "ds_read_b128 %2, %6 offset:%8\n\t"
+                 "ds_read_b128 %3, %6 offset:%9\n\t"
+                 "s_waitcnt lgkmcnt(0)"
+                 : "=&v"(k[0]), "=&v"(k[1]), "=&v"(ks), "=&v"(vs)
+                 : "v"(ka[0]), "v"(ka[1]), "v"(sa), "n"(VM), "i"(OFF), "i"(OFF + 64)
+                 : "memory");
+#else
+    (void)ka, (void)k, (void)sa, (void)ks, (void)vs;
 #endif
   }
   template <int VM, int OFF>
@@ -1208,6 +1247,8 @@ __global__ __launch_bounds__(64 * kWaves) void decode_pv_kernel(DecodeArgs a) {
   char *wring = ring + wave * kWaveBytes;
   const uint32_t ring0 = lds_address(wring);
   const uint32_t stage0 = ring0 + D * kStageBytes;
+  // ROWS: this lane's K scales in ring slot 0 (the V scales 64 bytes on).
+  const uint32_t scale_addr = ring0 + 2 * kPageBytes + grp * 16;
   uint32_t ka[NC], va[DT];
 #pragma unroll
   for (int c = 0; c < NC; ++c) {
@@ -1271,24 +1312,37 @@ __global__ __launch_bounds__(64 * kWaves) void decode_pv_kernel(DecodeArgs a) {
     float ks4[4] = {1.f, 1.f, 1.f, 1.f}, vs4[4] = {1.f, 1.f, 1.f, 1.f};
     if constexpr (kFp8) {
       u32x2 kr[NC];
-      if (D > 2 && after >= 2)
-        Reads8::template keys<kTileOps + 2 * kPageOps, KOFF>(ka, kr);
-      else if (after >= 1)
-        Reads8::template keys<kTileOps + kPageOps, KOFF>(ka, kr);
-      else
-        Reads8::template keys<kTileOps, KOFF>(ka, kr);
-      if constexpr (ROWS) {  // this lane's tokens' K scales (the wait above covers them)
-        const uint4 u = lds_read16_now(wring + KOFF + 2 * kPageBytes + grp * 16);
-        ks4[0] = __uint_as_float(u.x);
-        ks4[1] = __uint_as_float(u.y);
-        ks4[2] = __uint_as_float(u.z);
-        ks4[3] = __uint_as_float(u.w);
-        if constexpr (ROPE) {  // the new token's scale in place of its slot's
+      if constexpr (ROWS) {
+        // This lane's tokens' K and V scales, read with the K codes (their load was
+        // issued before the K tile's, so the same wait covers it).
+        u32x4 ku, vu;
+        if (D > 2 && after >= 2)
+          Reads8::template keys_rows<kTileOps + 2 * kPageOps, KOFF>(ka, kr, scale_addr, ku, vu);
+        else if (after >= 1)
+          Reads8::template keys_rows<kTileOps + kPageOps, KOFF>(ka, kr, scale_addr, ku, vu);
+        else
+          Reads8::template keys_rows<kTileOps, KOFF>(ka, kr, scale_addr, ku, vu);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          ks4[i] = __uint_as_float(ku[i]);
+          vs4[i] = __uint_as_float(vu[i]);
+        }
+        if constexpr (ROPE) {  // the new token's scales in place of its slot's
           if (patch && p == n_pages - 1) {
 #pragma unroll
-            for (int i = 0; i < 4; ++i) ks4[i] = grp * 4 + i == new_off ? new_ks : ks4[i];
+            for (int i = 0; i < 4; ++i) {
+              ks4[i] = grp * 4 + i == new_off ? new_ks : ks4[i];
+              vs4[i] = grp * 4 + i == new_off ? new_vs : vs4[i];
+            }
           }
         }
+      } else {
+        if (D > 2 && after >= 2)
+          Reads8::template keys<kTileOps + 2 * kPageOps, KOFF>(ka, kr);
+        else if (after >= 1)
+          Reads8::template keys<kTileOps + kPageOps, KOFF>(ka, kr);
+        else
+          Reads8::template keys<kTileOps, KOFF>(ka, kr);
       }
       if constexpr (ROPE) {
         // The new token's K codes in place of what was loaded of its slot.
@@ -1337,19 +1391,6 @@ __global__ __launch_bounds__(64 * kWaves) void decode_pv_kernel(DecodeArgs a) {
         Reads8::template raw_values<kPageOps, VOFF>(vra, raw);
       else
         Reads8::template raw_values<0, VOFF>(vra, raw);
-      if constexpr (ROWS) {  // this lane's tokens' V scales
-        const uint4 u = lds_read16_now(wring + KOFF + 2 * kPageBytes + BS * 4 + grp * 16);
-        vs4[0] = __uint_as_float(u.x);
-        vs4[1] = __uint_as_float(u.y);
-        vs4[2] = __uint_as_float(u.z);
-        vs4[3] = __uint_as_float(u.w);
-        if constexpr (ROPE) {
-          if (patch && p == n_pages - 1) {
-#pragma unroll
-            for (int i = 0; i < 4; ++i) vs4[i] = grp * 4 + i == new_off ? new_vs : vs4[i];
-          }
-        }
-      }
 #pragma unroll
       for (int j = 0; j < L; ++j) decode_fp8_chunk<T>(raw[j], dec[2 * j], dec[2 * j + 1]);
       Reads8::staged_values(vwa, dec, va, vt);
