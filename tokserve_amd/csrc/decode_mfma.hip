@@ -883,9 +883,10 @@ struct PvReads<64> {
   }
 };
 
-// fp8 pools. keys(): the K rows as e4m3 codes (one 8-byte read per 32 dims).
-// raw_values(): the page's V codes, 16 bytes per lane per 1 KiB of page, in the
-// order the HBM -> LDS loads wrote them (results valid on return). staged_values():
+// fp8 pools. kv_codes(): in one batch with one wait, the K rows as e4m3 codes (one
+// 8-byte read per 32 dims) and the page's V codes, 16 bytes per lane per 1 KiB of
+// page, in the order the HBM -> LDS loads wrote them (results valid on return);
+// kv_codes_rows() adds the lane's four K and four V scales. staged_values():
 // the codes decoded to T go to the wave's staging page (two 16-byte writes per 16
 // codes, in the swizzled layout of pools in the model dtype), and the V^T operands are
 // read back from it (valid after PvReads::wait); LDS operations of one wave complete
@@ -897,51 +898,49 @@ template <int DH>
 struct PvReads8;
 template <>
 struct PvReads8<128> {
-  template <int VM, int OFF>
-  static __device__ __forceinline__ void keys(const uint32_t (&ka)[4], u32x2 (&k)[4]) {
+  // The page's K codes and its raw V codes in one batch (VM: the V tile's wait).
+  template <int VM, int OFF, int VOFF>
+  static __device__ __forceinline__ void kv_codes(const uint32_t (&ka)[4], u32x2 (&k)[4],
+                                                  const uint32_t (&ra)[2], u32x4 (&v)[2]) {
 #if __HIP_DEVICE_COMPILE__
-    asm volatile("s_waitcnt vmcnt(%8)\n\t"
-                 TKS_RD64(0, 4, 9) TKS_RD64(1, 5, 9) TKS_RD64(2, 6, 9) TKS_RD64(3, 7, 9)
+    asm volatile("s_waitcnt vmcnt(%12)\n\t"
+                 "ds_read_b64 %0, %6 offset:%13\n\t"
+                 "ds_read_b64 %1, %7 offset:%13\n\t"
+                 "ds_read_b64 %2, %8 offset:%13\n\t"
+                 "ds_read_b64 %3, %9 offset:%13\n\t"
+                 "ds_read_b128 %4, %10 offset:%14\n\t"
+                 "ds_read_b128 %5, %11 offset:%14\n\t"
                  "s_waitcnt lgkmcnt(0)"
-                 : "=&v"(k[0]), "=&v"(k[1]), "=&v"(k[2]), "=&v"(k[3])
-                 : "v"(ka[0]), "v"(ka[1]), "v"(ka[2]), "v"(ka[3]), "n"(VM), "i"(OFF)
+                 : "=&v"(k[0]), "=&v"(k[1]), "=&v"(k[2]), "=&v"(k[3]), "=&v"(v[0]), "=&v"(v[1])
+                 : "v"(ka[0]), "v"(ka[1]), "v"(ka[2]), "v"(ka[3]), "v"(ra[0]), "v"(ra[1]),
+                   "n"(VM), "i"(OFF), "i"(VOFF)
                  : "memory");
 #else
-    (void)ka, (void)k;
+    (void)ka, (void)k, (void)ra, (void)v;
 #endif
   }
-  // keys() and, in the same batch, this lane's four K scales and four V scales of the
-  // page (16 bytes at sa + OFF and sa + OFF + 64).
-  template <int VM, int OFF>
-  static __device__ __forceinline__ void keys_rows(const uint32_t (&ka)[4], u32x2 (&k)[4],
-                                                   uint32_t sa, u32x4 &ks, u32x4 &vs) {
+  template <int VM, int OFF, int VOFF>
+  static __device__ __forceinline__ void kv_codes_rows(const uint32_t (&ka)[4], u32x2 (&k)[4],
+                                                       const uint32_t (&ra)[2], u32x4 (&v)[2],
+                                                       uint32_t sa, u32x4 &ks, u32x4 &vs) {
 #if __HIP_DEVICE_COMPILE__
-    asm volatile("s_waitcnt vmcnt(%11)\n\t"
-                 "ds_read_b64 %0, %6 offset:%12\n\t"
-                 "ds_read_b64 %1, %7 offset:%12\n\t"
-                 "ds_read_b64 %2, %8 offset:%12\n\t"
-                 "ds_read_b64 %3, %9 offset:%12\n\t"
-                 "ds_read_b128 %4, %10 offset:%12\n\t"
-                 "ds_read_b128 %5, %10 offset:%13\n\t"
+    asm volatile("s_waitcnt vmcnt(%15)\n\t"
+                 "ds_read_b64 %0, %8 offset:%16\n\t"
+                 "ds_read_b64 %1, %9 offset:%16\n\t"
+                 "ds_read_b64 %2, %10 offset:%16\n\t"
+                 "ds_read_b64 %3, %11 offset:%16\n\t"
+                 "ds_read_b128 %4, %12 offset:%18\n\t"
+                 "ds_read_b128 %5, %13 offset:%18\n\t"
+                 "ds_read_b128 %6, %14 offset:%16\n\t"
+                 "ds_read_b128 %7, %14 offset:%17\n\t"
                  "s_waitcnt lgkmcnt(0)"
-                 : "=&v"(k[0]), "=&v"(k[1]), "=&v"(k[2]), "=&v"(k[3]), "=&v"(ks), "=&v"(vs)
-                 : "v"(ka[0]), "v"(ka[1]), "v"(ka[2]), "v"(ka[3]), "v"(sa), "n"(VM), "i"(OFF),
-                   "i"(OFF + 64)
+                 : "=&v"(k[0]), "=&v"(k[1]), "=&v"(k[2]), "=&v"(k[3]), "=&v"(v[0]), "=&v"(v[1]),
+                   "=&v"(ks), "=&v"(vs)
+                 : "v"(ka[0]), "v"(ka[1]), "v"(ka[2]), "v"(ka[3]), "v"(ra[0]), "v"(ra[1]),
+                   "v"(sa), "n"(VM), "i"(OFF), "i"(OFF + 64), "i"(VOFF)
                  : "memory");
 #else
-    (void)ka, (void)k, (void)sa, (void)ks, (void)vs;
-#endif
-  }
-  template <int VM, int OFF>
-  static __device__ __forceinline__ void raw_values(const uint32_t (&ra)[2], u32x4 (&v)[2]) {
-#if __HIP_DEVICE_COMPILE__
-    asm volatile("s_waitcnt vmcnt(%4)\n\t" TKS_RD128(0, 2, 5) TKS_RD128(1, 3, 5)
-                 "s_waitcnt lgkmcnt(0)"
-                 : "=&v"(v[0]), "=&v"(v[1])
-                 : "v"(ra[0]), "v"(ra[1]), "n"(VM), "i"(OFF)
-                 : "memory");
-#else
-    (void)ra, (void)v;
+    (void)ka, (void)k, (void)ra, (void)v, (void)sa, (void)ks, (void)vs;
 #endif
   }
   static __device__ __forceinline__ void staged_values(const uint32_t (&wa)[4], const u32x4 (&d)[4],
@@ -963,44 +962,40 @@ struct PvReads8<128> {
 };
 template <>
 struct PvReads8<64> {
-  template <int VM, int OFF>
-  static __device__ __forceinline__ void keys(const uint32_t (&ka)[2], u32x2 (&k)[2]) {
+  template <int VM, int OFF, int VOFF>
+  static __device__ __forceinline__ void kv_codes(const uint32_t (&ka)[2], u32x2 (&k)[2],
+                                                  const uint32_t (&ra)[1], u32x4 (&v)[1]) {
 #if __HIP_DEVICE_COMPILE__
-    asm volatile("s_waitcnt vmcnt(%4)\n\t" TKS_RD64(0, 2, 5) TKS_RD64(1, 3, 5)
+    asm volatile("s_waitcnt vmcnt(%6)\n\t"
+                 "ds_read_b64 %0, %3 offset:%7\n\t"
+                 "ds_read_b64 %1, %4 offset:%7\n\t"
+                 "ds_read_b128 %2, %5 offset:%8\n\t"
                  "s_waitcnt lgkmcnt(0)"
-                 : "=&v"(k[0]), "=&v"(k[1])
-                 : "v"(ka[0]), "v"(ka[1]), "n"(VM), "i"(OFF)
+                 : "=&v"(k[0]), "=&v"(k[1]), "=&v"(v[0])
+                 : "v"(ka[0]), "v"(ka[1]), "v"(ra[0]), "n"(VM), "i"(OFF), "i"(VOFF)
                  : "memory");
 #else
-    (void)ka, (void)k;
+    (void)ka, (void)k, (void)ra, (void)v;
 #endif
   }
-  template <int VM, int OFF>
-  static __device__ __forceinline__ void keys_rows(const uint32_t (&ka)[2], u32x2 (&k)[2],
-                                                   uint32_t sa, u32x4 &ks, u32x4 &vs) {
+  template <int VM, int OFF, int VOFF>
+  static __device__ __forceinline__ void kv_codes_rows(const uint32_t (&ka)[2], u32x2 (&k)[2],
+                                                       const uint32_t (&ra)[1], u32x4 (&v)[1],
+                                                       uint32_t sa, u32x4 &ks, u32x4 &vs) {
 #if __HIP_DEVICE_COMPILE__
-    asm volatile("s_waitcnt vmcnt(%7)\n\t"
-                 "ds_read_b64 %0, %4 offset:%8\n\t"
-                 "ds_read_b64 %1, %5 offset:%8\n\t"
-                 "ds_read_b128 %2, %6 offset:%8\n\t"
-                 "ds_read_b128 %3, %6 offset:%9\n\t"
+    asm volatile("s_waitcnt vmcnt(%9)\n\t"
+                 "ds_read_b64 %0, %5 offset:%10\n\t"
+                 "ds_read_b64 %1, %6 offset:%10\n\t"
+                 "ds_read_b128 %2, %7 offset:%12\n\t"
+                 "ds_read_b128 %3, %8 offset:%10\n\t"
+                 "ds_read_b128 %4, %8 offset:%11\n\t"
                  "s_waitcnt lgkmcnt(0)"
-                 : "=&v"(k[0]), "=&v"(k[1]), "=&v"(ks), "=&v"(vs)
-                 : "v"(ka[0]), "v"(ka[1]), "v"(sa), "n"(VM), "i"(OFF), "i"(OFF + 64)
+                 : "=&v"(k[0]), "=&v"(k[1]), "=&v"(v[0]), "=&v"(ks), "=&v"(vs)
+                 : "v"(ka[0]), "v"(ka[1]), "v"(ra[0]), "v"(sa), "n"(VM), "i"(OFF), "i"(OFF + 64),
+                   "i"(VOFF)
                  : "memory");
 #else
-    (void)ka, (void)k, (void)sa, (void)ks, (void)vs;
-#endif
-  }
-  template <int VM, int OFF>
-  static __device__ __forceinline__ void raw_values(const uint32_t (&ra)[1], u32x4 (&v)[1]) {
-#if __HIP_DEVICE_COMPILE__
-    asm volatile("s_waitcnt vmcnt(%2)\n\t" TKS_RD128(0, 1, 3) "s_waitcnt lgkmcnt(0)"
-                 : "=&v"(v[0])
-                 : "v"(ra[0]), "n"(VM), "i"(OFF)
-                 : "memory");
-#else
-    (void)ra, (void)v;
+    (void)ka, (void)k, (void)ra, (void)v, (void)sa, (void)ks, (void)vs;
 #endif
   }
   static __device__ __forceinline__ void staged_values(const uint32_t (&wa)[2], const u32x4 (&d)[2],
@@ -1310,6 +1305,7 @@ __global__ __launch_bounds__(64 * kWaves) void decode_pv_kernel(DecodeArgs a) {
     constexpr int KOFF = SLOT * kStageBytes, VOFF = KOFF + kPageBytes;
     f4 s4 = {0.f, 0.f, 0.f, 0.f};
     float ks4[4] = {1.f, 1.f, 1.f, 1.f}, vs4[4] = {1.f, 1.f, 1.f, 1.f};
+    u32x4 raw[kFp8 ? L : 1];  // fp8 pools: the page's V codes, read with its K codes
     if constexpr (kFp8) {
       u32x2 kr[NC];
       if constexpr (ROWS) {
@@ -1317,11 +1313,11 @@ __global__ __launch_bounds__(64 * kWaves) void decode_pv_kernel(DecodeArgs a) {
         // issued before the K tile's, so the same wait covers it).
         u32x4 ku, vu;
         if (D > 2 && after >= 2)
-          Reads8::template keys_rows<kTileOps + 2 * kPageOps, KOFF>(ka, kr, scale_addr, ku, vu);
+          Reads8::template kv_codes_rows<2 * kPageOps, KOFF, VOFF>(ka, kr, vra, raw, scale_addr, ku, vu);
         else if (after >= 1)
-          Reads8::template keys_rows<kTileOps + kPageOps, KOFF>(ka, kr, scale_addr, ku, vu);
+          Reads8::template kv_codes_rows<kPageOps, KOFF, VOFF>(ka, kr, vra, raw, scale_addr, ku, vu);
         else
-          Reads8::template keys_rows<kTileOps, KOFF>(ka, kr, scale_addr, ku, vu);
+          Reads8::template kv_codes_rows<0, KOFF, VOFF>(ka, kr, vra, raw, scale_addr, ku, vu);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           ks4[i] = __uint_as_float(ku[i]);
@@ -1338,11 +1334,11 @@ __global__ __launch_bounds__(64 * kWaves) void decode_pv_kernel(DecodeArgs a) {
         }
       } else {
         if (D > 2 && after >= 2)
-          Reads8::template keys<kTileOps + 2 * kPageOps, KOFF>(ka, kr);
+          Reads8::template kv_codes<2 * kPageOps, KOFF, VOFF>(ka, kr, vra, raw);
         else if (after >= 1)
-          Reads8::template keys<kTileOps + kPageOps, KOFF>(ka, kr);
+          Reads8::template kv_codes<kPageOps, KOFF, VOFF>(ka, kr, vra, raw);
         else
-          Reads8::template keys<kTileOps, KOFF>(ka, kr);
+          Reads8::template kv_codes<0, KOFF, VOFF>(ka, kr, vra, raw);
       }
       if constexpr (ROPE) {
         // The new token's K codes in place of what was loaded of its slot.
@@ -1384,13 +1380,7 @@ __global__ __launch_bounds__(64 * kWaves) void decode_pv_kernel(DecodeArgs a) {
     // page's codes are decoded into the staging page first.
     u32x2 vt[DT];
     if constexpr (kFp8) {
-      u32x4 raw[L], dec[2 * L];
-      if (D > 2 && after >= 2)
-        Reads8::template raw_values<2 * kPageOps, VOFF>(vra, raw);
-      else if (after >= 1)
-        Reads8::template raw_values<kPageOps, VOFF>(vra, raw);
-      else
-        Reads8::template raw_values<0, VOFF>(vra, raw);
+      u32x4 dec[2 * L];
 #pragma unroll
       for (int j = 0; j < L; ++j) decode_fp8_chunk<T>(raw[j], dec[2 * j], dec[2 * j + 1]);
       Reads8::staged_values(vwa, dec, va, vt);
