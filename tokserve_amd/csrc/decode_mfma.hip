@@ -832,6 +832,14 @@ struct PvReads<128> {
     (void)k;
 #endif
   }
+  // The keys, with the page's 8 V^T reads issued behind them still in flight.
+  static __device__ __forceinline__ void wait_before_values(u32x4 (&k)[4]) {
+#if __HIP_DEVICE_COMPILE__
+    asm volatile("s_waitcnt lgkmcnt(8)" : "+v"(k[0]), "+v"(k[1]), "+v"(k[2]), "+v"(k[3])::"memory");
+#else
+    (void)k;
+#endif
+  }
   static __device__ __forceinline__ void wait(u32x2 (&v)[8]) {
 #if __HIP_DEVICE_COMPILE__
     asm volatile("s_waitcnt lgkmcnt(0)"
@@ -870,6 +878,13 @@ struct PvReads<64> {
   static __device__ __forceinline__ void wait(u32x4 (&k)[2]) {
 #if __HIP_DEVICE_COMPILE__
     asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(k[0]), "+v"(k[1])::"memory");
+#else
+    (void)k;
+#endif
+  }
+  static __device__ __forceinline__ void wait_before_values(u32x4 (&k)[2]) {
+#if __HIP_DEVICE_COMPILE__
+    asm volatile("s_waitcnt lgkmcnt(4)" : "+v"(k[0]), "+v"(k[1])::"memory");
 #else
     (void)k;
 #endif
@@ -1306,6 +1321,8 @@ __global__ __launch_bounds__(64 * kWaves) void decode_pv_kernel(DecodeArgs a) {
     f4 s4 = {0.f, 0.f, 0.f, 0.f};
     float ks4[4] = {1.f, 1.f, 1.f, 1.f}, vs4[4] = {1.f, 1.f, 1.f, 1.f};
     u32x4 raw[kFp8 ? L : 1];  // fp8 pools: the page's V codes, read with its K codes
+    // The page's V^T operands (pools in the model dtype: requested with its K rows).
+    u32x2 vt[DT];
     if constexpr (kFp8) {
       u32x2 kr[NC];
       if constexpr (ROWS) {
@@ -1355,13 +1372,17 @@ __global__ __launch_bounds__(64 * kWaves) void decode_pv_kernel(DecodeArgs a) {
         s4 = M::run(IO::k_operand(make_uint2(kr[c][0], kr[c][1])), qa[c], s4);
     } else {
       u32x4 kr[NC];
-      if (D > 2 && after >= 2)
+      if (D > 2 && after >= 2) {
         Reads::template keys<kTileOps + 2 * kPageOps, KOFF>(ka, kr);
-      else if (after >= 1)
+        Reads::template values<2 * kPageOps, VOFF>(va, vt);
+      } else if (after >= 1) {
         Reads::template keys<kTileOps + kPageOps, KOFF>(ka, kr);
-      else
+        Reads::template values<kPageOps, VOFF>(va, vt);
+      } else {
         Reads::template keys<kTileOps, KOFF>(ka, kr);
-      Reads::wait(kr);
+        Reads::template values<0, VOFF>(va, vt);
+      }
+      Reads::wait_before_values(kr);
       if constexpr (ROPE) {
         // The new token's K row in place of what was loaded of its slot.
         if (patch && p == n_pages - 1 && r == new_off) {
@@ -1376,21 +1397,13 @@ __global__ __launch_bounds__(64 * kWaves) void decode_pv_kernel(DecodeArgs a) {
       for (int c = 0; c < NC; ++c)
         s4 = M::run(as_v8<T>(make_uint4(kr[c][0], kr[c][1], kr[c][2], kr[c][3])), qa[c], s4);
     }
-    // This page's V^T operands: requested now, used after the softmax. fp8 pools: the
-    // page's codes are decoded into the staging page first.
-    u32x2 vt[DT];
+    // fp8 pools: the page's V codes are decoded into the staging page, and the V^T
+    // operands read back from it, used after the softmax.
     if constexpr (kFp8) {
       u32x4 dec[2 * L];
 #pragma unroll
       for (int j = 0; j < L; ++j) decode_fp8_chunk<T>(raw[j], dec[2 * j], dec[2 * j + 1]);
       Reads8::staged_values(vwa, dec, va, vt);
-    } else {
-      if (D > 2 && after >= 2)
-        Reads::template values<2 * kPageOps, VOFF>(va, vt);
-      else if (after >= 1)
-        Reads::template values<kPageOps, VOFF>(va, vt);
-      else
-        Reads::template values<0, VOFF>(va, vt);
     }
     float sv[4];
 #pragma unroll
