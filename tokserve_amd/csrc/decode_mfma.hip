@@ -1081,11 +1081,21 @@ struct IntConst {
   static constexpr int value = N;
 };
 
+// Waves per SIMD the register budget is cut for. At Dh 64 LDS holds three
+// workgroups per CU, and asking for three waves keeps the P.V accumulators in
+// VGPRs (left to itself the compiler put them in AGPRs, with a copy per access:
+// fp8 serving shape 10.4 -> 10.0 us). At Dh 128 the budget is left alone: three
+// waves per SIMD over fp8 pools (145 VGPRs) ran the Llama-3-8B decode batch 3 %
+// slower (152.5 vs 148.7 us).
+template <int DH>
+constexpr int kPvMinWaves = DH == 64 ? 3 : 1;
+
 // ROWS: fp8 pools with one scale per pool row (a.k_rs, a.v_rs): a page's 16 K and 16
 // V scales ride in the ring with it; a lane multiplies its scores by its tokens' K
 // scales and its probabilities, after they enter the row sum, by their V scales.
 template <typename T, typename KV, int DH, int G, bool ROPE, bool ROWS = false>
-__global__ __launch_bounds__(64 * kWaves) void decode_pv_kernel(DecodeArgs a) {
+__global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(kPvMinWaves<DH>)))
+void decode_pv_kernel(DecodeArgs a) {
   constexpr bool kFp8 = sizeof(KV) == 1;
   static_assert(!ROWS || kFp8, "row scales: fp8 pools");
   constexpr int BS = 16, NC = DH / 32, DT = DH / 16, CPR = DH / 8;
